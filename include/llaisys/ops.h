@@ -1,0 +1,94 @@
+/*
+ * Operator C-ABI.
+ *
+ * llaisysSelfAttention and the eight other reference ops keep the reference's
+ * declarations (include/llaisys/ops.h:7-15) so python/llaisys/libllaisys/ops.py
+ * binds unchanged. This library implements the KV-cache attention path only:
+ * llaisysSelfAttention runs on LLAISYS_DEVICE_AMD tensors; the other eight ops
+ * are exported so the reference's loader finds them, and fail with an
+ * "outside this library's scope" error, as the reference's stubs fail with
+ * TO_BE_IMPLEMENTED (src/ops/<op>/op.cpp:4-6).
+ *
+ * The llaisysPagedKV* / llaisysPagedAttention* entry points are new. The
+ * reference has no paged KV code; they follow its op conventions
+ * (include/llaisys/ops.h:6-16: tensor handles and scalars in, void out, output
+ * written in place, errors reported as the reference reports them).
+ *
+ * Paged KV pool (one per layer, one for K and one for V):
+ *   shape [num_blocks, nkvh, 16, 128], dtype BF16, device AMD, contiguous.
+ *   A (block, kv-head) page holds 16 tokens x 128 dims = 4 KiB. Inside a page
+ *   the bytes are in the MI355X page format, not row-major [16][128]:
+ *     K page: element (token t, dim d) at bf16 index
+ *             (d / 8) * 128 + t * 8 + (d % 8)              ([16 dim-chunks][16 t][8])
+ *     V page: element (t, d) at bf16 index
+ *             (d / 32) * 512 + (t / 4) * 128 + (d % 16) * 8 + ((d / 16) % 2) * 4 + t % 4
+ *   so that every 1 KiB of a page is exactly one 64-lane x 16-byte load that
+ *   feeds a gfx950 MFMA operand. Only llaisysPagedKVAppend writes this format
+ *   and llaisysPagedKVGather reads it back to row-major; callers never need it.
+ * Block table: [B, max_pages] I32; entry (b, p) is the physical block holding
+ *   tokens [16p, 16p+16) of sequence b. ctx_len: [B] I32 = tokens in the cache.
+ */
+#ifndef LLAISYS_OPS_H
+#define LLAISYS_OPS_H
+
+#include "tensor.h"
+
+__C {
+    /* Reference ops outside the KV path: exported, raise an error (ops.h:7-13,15). */
+    __export void llaisysAdd(llaisysTensor_t c, llaisysTensor_t a, llaisysTensor_t b);
+    __export void llaisysArgmax(llaisysTensor_t max_idx, llaisysTensor_t max_val, llaisysTensor_t vals);
+    __export void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index, llaisysTensor_t weight);
+    __export void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, llaisysTensor_t bias);
+    __export void llaisysRearrange(llaisysTensor_t out, llaisysTensor_t in);
+    __export void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, float eps);
+    __export void llaisysROPE(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t pos_ids, float theta);
+    __export void llaisysSwiGLU(llaisysTensor_t out, llaisysTensor_t gate, llaisysTensor_t up);
+
+    /* Replaces include/llaisys/ops.h:14 (stub src/ops/self_attention/op.cpp:4-6;
+     * semantics README.md:244-266, test/ops/self_attention.py:11-28).
+     * attn_val [L, nh, dv], q [L, nh, d], k [S, nkvh, d], v [S, nkvh, dv], all
+     * contiguous, one dtype (F32, F16 or BF16), nh % nkvh == 0, S >= L,
+     * d, dv <= 256. Query i attends keys j <= i + S - L; query head h reads
+     * kv head h / (nh / nkvh). Accumulates in fp32, rounds once to the dtype. */
+    __export void llaisysSelfAttention(llaisysTensor_t attn_val, llaisysTensor_t q, llaisysTensor_t k,
+                                       llaisysTensor_t v, float scale);
+
+    /* New. Scatter new K/V tokens into their pages.
+     * k_new, v_new: [T, nkvh, 128] BF16. cu_new: [B+1] I32 prefix offsets, or
+     * NULL meaning T == B and one token per sequence. Row r of sequence b
+     * (cu_new[b] <= r < cu_new[b+1]) is written at position
+     * ctx_len[b] + (r - cu_new[b]), i.e. ctx_len is the length BEFORE the append
+     * and is not modified. Pages for every written position must already be
+     * mapped in block_table. Bit-exact copy. */
+    __export void llaisysPagedKVAppend(llaisysTensor_t k_pool, llaisysTensor_t v_pool, llaisysTensor_t k_new,
+                                       llaisysTensor_t v_new, llaisysTensor_t block_table, llaisysTensor_t ctx_len,
+                                       llaisysTensor_t cu_new);
+
+    /* New. Copy the first cu_seqlens[b+1]-cu_seqlens[b] tokens of each
+     * sequence out of the pool into rows [cu_seqlens[b], cu_seqlens[b+1]) of
+     * k_out, v_out: [T, nkvh, 128] BF16 row-major. Bit-exact. */
+    __export void llaisysPagedKVGather(llaisysTensor_t k_out, llaisysTensor_t v_out, llaisysTensor_t k_pool,
+                                       llaisysTensor_t v_pool, llaisysTensor_t block_table,
+                                       llaisysTensor_t cu_seqlens);
+
+    /* New. Batched decode attention (flash-decoding with split-KV and a
+     * log-sum-exp combine): q [B, nh, 128] BF16, out [B, nh, 128] BF16 or F32.
+     * Sequence b's single query attends all ctx_len[b] (>= 1) cached tokens,
+     * which include the token appended for this step.
+     * nh % nkvh == 0 and nh / nkvh <= 16. fp32 accumulation. */
+    __export void llaisysPagedAttention(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor_t k_pool,
+                                        llaisysTensor_t v_pool, llaisysTensor_t block_table, llaisysTensor_t ctx_len,
+                                        float scale);
+
+    /* New. Mixed chunked-prefill + decode attention over paged KV.
+     * q, out [T, nh, 128]; sequence b owns query rows [cu_q[b], cu_q[b+1]) and
+     * Lq = cu_q[b+1]-cu_q[b] (>= 1, <= ctx_len[b]) of its ctx_len[b] cached
+     * tokens are those queries' own tokens (already appended). Query i sits at
+     * position ctx_len[b] - Lq + i and attends keys at positions <= that
+     * (bottom-right causal alignment, test/ops/self_attention.py:18). */
+    __export void llaisysPagedAttentionVarlen(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor_t k_pool,
+                                              llaisysTensor_t v_pool, llaisysTensor_t block_table,
+                                              llaisysTensor_t cu_q, llaisysTensor_t ctx_len, float scale);
+}
+
+#endif /* LLAISYS_OPS_H */

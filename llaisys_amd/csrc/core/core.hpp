@@ -1,0 +1,107 @@
+// Storage, per-device Runtime and the thread-local Context.
+//
+// Behaviour follows the reference's src/core/{storage,runtime,context}:
+//  * a Storage owns one buffer and frees it through the runtime table that
+//    allocated it (storage.cpp:9-11);
+//  * a Runtime is one (device type, id): its table, one stream, allocation
+//    (runtime.cpp:7-12, :49-55);
+//  * the Context is thread-local and activates the first non-CPU device found,
+//    else CPU (context.cpp:7-32, :74-77).
+// Two reference hazards are avoided: the current-runtime pointer starts null
+// (context.hpp:16 leaves it uninitialised) and lazily created runtimes are
+// stored back into the map (context.cpp:55-62 mutates a copy).
+//
+// The AMD runtime also owns the device workspace the attention kernels use:
+// split-KV partial results, self-resetting arrival counters and an error word.
+#pragma once
+
+#include "llaisys/runtime.h"
+
+#include <cstddef>
+#include <map>
+#include <memory>
+#include <vector>
+
+namespace llaisys::core {
+
+class Storage {
+public:
+    Storage(std::byte *mem, size_t size, const LlaisysRuntimeAPI *api, llaisysDeviceType_t type, int id,
+            bool is_host);
+    ~Storage();
+    Storage(const Storage &) = delete;
+    Storage &operator=(const Storage &) = delete;
+
+    std::byte *memory() const { return mem_; }
+    size_t size() const { return size_; }
+    bool isHost() const { return is_host_; }
+    // Host storage reports CPU/0, as storage.cpp:21-35.
+    llaisysDeviceType_t deviceType() const { return is_host_ ? LLAISYS_DEVICE_CPU : type_; }
+    int deviceId() const { return is_host_ ? 0 : id_; }
+
+private:
+    std::byte *mem_;
+    size_t size_;
+    const LlaisysRuntimeAPI *api_;
+    llaisysDeviceType_t type_;
+    int id_;
+    bool is_host_;
+};
+using storage_t = std::shared_ptr<Storage>;
+
+class Runtime {
+public:
+    Runtime(llaisysDeviceType_t type, int id);
+    ~Runtime();
+    Runtime(const Runtime &) = delete;
+    Runtime &operator=(const Runtime &) = delete;
+
+    llaisysDeviceType_t deviceType() const { return type_; }
+    int deviceId() const { return id_; }
+    const LlaisysRuntimeAPI *api() const { return api_; }
+
+    // Stream ops launch on: the override if one is set, else the runtime's own.
+    llaisysStream_t stream() const { return override_stream_ ? override_stream_ : stream_; }
+    void setStreamOverride(llaisysStream_t s) { override_stream_ = s; }
+
+    storage_t allocateDeviceStorage(size_t size);
+    storage_t allocateHostStorage(size_t size);
+
+    // Device workspace (AMD only). Grow-only; growing waits for the device.
+    void *scratch(size_t bytes);
+    // `n` int32 counters, all zero between calls (kernels reset what they use).
+    int *counters(size_t n);
+    // One int32 of kernel-side error bits.
+    int *errorWord();
+    int takeErrorFlags();
+
+    void activate();
+
+private:
+    llaisysDeviceType_t type_;
+    int id_;
+    const LlaisysRuntimeAPI *api_;
+    llaisysStream_t stream_ = nullptr;
+    llaisysStream_t override_stream_ = nullptr;
+    void *scratch_ = nullptr;
+    size_t scratch_bytes_ = 0;
+    int *counters_ = nullptr;
+    size_t counters_n_ = 0;
+    int *error_word_ = nullptr;
+};
+
+class Context {
+public:
+    Context();
+    ~Context();
+    void setDevice(llaisysDeviceType_t type, int id);
+    Runtime &runtime();
+
+private:
+    std::map<llaisysDeviceType_t, std::vector<std::unique_ptr<Runtime>>> runtimes_;
+    Runtime *current_ = nullptr;
+};
+
+Context &context();
+
+} // namespace llaisys::core

@@ -1,0 +1,155 @@
+"""Paged decode / varlen attention on the GPU vs the fp32 C oracle
+(gather + self_attention). Tolerances from BASELINE north_star: fp32 output
+max|err| <= 1e-4 * max|ref|; bf16 output max|err| <= 2e-2."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import llaisys_amd as L
+import oracle
+from paged_cases import make_case, queries
+from utils import from_bits, to_llaisys, to_torch
+
+pytestmark = pytest.mark.gpu
+
+SCALE = 1.0 / 128**0.5
+F32_REL = 1e-4
+BF16_ABS = 2e-2
+
+
+def run_decode(case, q_bits, out_dtype):
+    kp, vp = case.device_pools()
+    table, ctx = case.device_meta()
+    out = to_llaisys(torch.zeros((case.B, case.nh, 128), dtype=out_dtype, device="cuda"))
+    L.Ops.paged_attention(out, to_llaisys(from_bits(q_bits)), kp, vp, table, ctx, SCALE)
+    assert L.device_error_flags() == 0
+    return to_torch(out).float().cpu().numpy()
+
+
+def run_varlen(case, q_bits, cu_q, out_dtype):
+    kp, vp = case.device_pools()
+    table, ctx = case.device_meta()
+    T = q_bits.shape[0]
+    out = to_llaisys(torch.zeros((T, case.nh, 128), dtype=out_dtype, device="cuda"))
+    L.Ops.paged_attention_varlen(out, to_llaisys(from_bits(q_bits)), kp, vp, table,
+                                 to_llaisys(torch.from_numpy(cu_q)), ctx, SCALE)
+    assert L.device_error_flags() == 0
+    return to_torch(out).float().cpu().numpy()
+
+
+def check(got_f32, got_bf16, ref):
+    err = np.max(np.abs(got_f32 - ref)) / np.max(np.abs(ref))
+    assert err <= F32_REL, f"fp32 relative error {err:.3g}"
+    abs_err = np.max(np.abs(got_bf16 - ref))
+    assert abs_err <= BF16_ABS, f"bf16 abs error {abs_err:.3g}"
+
+
+@pytest.mark.parametrize("nh,nkvh", [(12, 2), (16, 1), (4, 4), (8, 2)])
+def test_decode_edge_lengths(nh, nkvh):
+    ctx = np.array([1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 257], np.int32)
+    case = make_case(10 + nh, ctx, nh=nh, nkvh=nkvh)
+    q = queries(99, case.B, nh)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE)
+    check(run_decode(case, q, torch.float32), run_decode(case, q, torch.bfloat16), ref)
+
+
+@pytest.mark.parametrize("pps", ["2", "4", "16", "64"])
+def test_decode_split_invariance(pps, monkeypatch):
+    ctx = oracle.randint(5, 9, 1, 3000).astype(np.int32)
+    case = make_case(21, ctx)
+    q = queries(22, case.B, 12)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE)
+    monkeypatch.setenv("LLAISYS_PAGES_PER_SPLIT", pps)
+    check(run_decode(case, q, torch.float32), run_decode(case, q, torch.bfloat16), ref)
+
+
+def test_decode_ignores_stale_nan_slots():
+    ctx = np.array([5, 16, 33, 70, 129], np.int32)
+    case = make_case(31, ctx, stale_nan=True, extra_pages=2)
+    q = queries(32, case.B, 12)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE)
+    got = run_decode(case, q, torch.float32)
+    assert np.isfinite(got).all()
+    check(got, run_decode(case, q, torch.bfloat16), ref)
+
+
+def test_config3_batch64_decode():
+    # B=64, ctx U[512, 8192], 12:2 GQA, d=128, bf16.
+    ctx = oracle.randint(0, 64, 512, 8192).astype(np.int32)
+    case = make_case(40, ctx)
+    q = queries(41, 64, 12)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE, nthreads=16)
+    check(run_decode(case, q, torch.float32), run_decode(case, q, torch.bfloat16), ref)
+
+
+def test_varlen_small_mixed_batch():
+    ctx = np.array([40, 7, 100, 1, 35, 64], np.int32)
+    lq = np.array([40, 3, 17, 1, 1, 16], np.int32)  # new tokens already in the cache
+    case = make_case(50, ctx)
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = queries(51, int(cu_q[-1]), 12)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE, cu_q=cu_q)
+    check(run_varlen(case, q, cu_q, torch.float32), run_varlen(case, q, cu_q, torch.bfloat16), ref)
+
+
+def test_varlen_with_decode_only_equals_decode():
+    ctx = oracle.randint(55, 7, 1, 900).astype(np.int32)
+    case = make_case(56, ctx)
+    q = queries(57, case.B, 12)
+    cu_q = np.arange(case.B + 1, dtype=np.int32)
+    a = run_varlen(case, q, cu_q, torch.float32)
+    b = run_decode(case, q, torch.float32)
+    assert np.max(np.abs(a - b)) <= 1e-6 * np.max(np.abs(b))
+
+
+def test_config4_mixed_prefill_and_decode():
+    # 4 chunks of 512 over priors {0,1024,2048,4096} + 60 decode, ctx U[256,4096].
+    priors = np.array([0, 1024, 2048, 4096], np.int32)
+    dec = oracle.randint(60, 60, 256, 4096).astype(np.int32)
+    ctx = np.concatenate([priors + 512, dec]).astype(np.int32)
+    lq = np.concatenate([np.full(4, 512), np.ones(60)]).astype(np.int32)
+    case = make_case(61, ctx)
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = queries(62, int(cu_q[-1]), 12)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE, cu_q=cu_q, nthreads=16)
+    check(run_varlen(case, q, cu_q, torch.float32), run_varlen(case, q, cu_q, torch.bfloat16), ref)
+
+
+def test_paged_attention_equals_self_attention_of_gather():
+    ctx = np.array([300, 17, 1024], np.int32)
+    case = make_case(70, ctx)
+    q = queries(71, case.B, 12)
+    got = run_decode(case, q, torch.float32)
+    kp, vp = case.device_pools()
+    table, _ = case.device_meta()
+    cu = np.concatenate([[0], np.cumsum(ctx)]).astype(np.int32)
+    ko = to_llaisys(torch.zeros((int(cu[-1]), 2, 128), dtype=torch.bfloat16, device="cuda"))
+    vo = to_llaisys(torch.zeros((int(cu[-1]), 2, 128), dtype=torch.bfloat16, device="cuda"))
+    L.Ops.paged_kv_gather(ko, vo, kp, vp, table, to_llaisys(torch.from_numpy(cu)))
+    kt, vt = to_torch(ko).float(), to_torch(vo).float()
+    qt = from_bits(q).float()
+    for b in range(case.B):
+        o = to_llaisys(torch.zeros((1, 12, 128), device="cuda"))
+        L.Ops.self_attention(o, to_llaisys(qt[b:b + 1]), to_llaisys(kt[cu[b]:cu[b + 1]]),
+                             to_llaisys(vt[cu[b]:cu[b + 1]]), SCALE)
+        sa = to_torch(o).cpu().numpy()[0]
+        assert np.max(np.abs(sa - got[b])) <= F32_REL * np.max(np.abs(sa))
+
+
+def test_bad_block_id_and_overlong_context_flag_errors():
+    ctx = np.array([40, 20], np.int32)
+    case = make_case(80, ctx)
+    kp, vp = case.device_pools()
+    bad = case.table.copy()
+    bad[1, 0] = 10 ** 6
+    out = to_llaisys(torch.zeros((2, 12, 128), dtype=torch.bfloat16, device="cuda"))
+    q = to_llaisys(from_bits(queries(81, 2, 12)))
+    L.Ops.paged_attention(out, q, kp, vp, to_llaisys(torch.from_numpy(bad)),
+                          to_llaisys(torch.from_numpy(ctx)), SCALE)
+    assert L.device_error_flags() & 1
+    long_ctx = np.array([40, 16 * case.table.shape[1] + 1], np.int32)
+    L.Ops.paged_attention(out, q, kp, vp, to_llaisys(torch.from_numpy(case.table)),
+                          to_llaisys(torch.from_numpy(long_ctx)), SCALE)
+    assert L.device_error_flags() & 2
