@@ -5,6 +5,7 @@ The library is the HIP build for gfx950. If it has not been built, importing
 this module raises: there is no CPU fallback for the kernels it carries.
 """
 import ctypes
+import importlib.util
 import os
 import sys
 from pathlib import Path
@@ -25,6 +26,28 @@ from .tensor import llaisysTensor_t, load_tensor
 LIB_PATH = Path(__file__).resolve().parent / "libllaisys.so"
 
 
+def _share_hip_runtime():
+    """Map the HIP runtime this process should use before libllaisys.so binds one.
+
+    libllaisys.so needs libamdhip64.so.7. PyTorch-ROCm ships its own copy of
+    that library; if libllaisys.so were loaded first it would pull in
+    /opt/rocm's copy and a later `import torch` would bring a second HIP
+    runtime into the process, whose device pointers the first cannot use.
+    So when torch is installed its copy is mapped first (by path, without
+    importing torch), making one runtime serve both. LLAISYS_HIP_RUNTIME
+    names another libamdhip64 to use instead.
+    """
+    path = os.environ.get("LLAISYS_HIP_RUNTIME")
+    if not path:
+        spec = importlib.util.find_spec("torch")
+        if spec and spec.submodule_search_locations:
+            cand = Path(list(spec.submodule_search_locations)[0]) / "lib" / "libamdhip64.so"
+            if cand.is_file():
+                path = os.fspath(cand)
+    if path:
+        ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+
+
 def load_shared_library():
     if not sys.platform.startswith("linux"):
         raise RuntimeError("llaisys_amd targets Linux with ROCm only")
@@ -33,6 +56,7 @@ def load_shared_library():
             f"{LIB_PATH} is missing: build it with `python -m llaisys_amd.build` "
             "(the HIP kernels have no fallback)"
         )
+    _share_hip_runtime()
     return ctypes.CDLL(os.fspath(LIB_PATH))
 
 

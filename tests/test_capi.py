@@ -82,3 +82,18 @@ def test_self_attention_shape_checks():
 def test_last_error_is_cleared_after_read():
     buf = ctypes.create_string_buffer(256)
     assert LIB_LLAISYS.llaisysGetLastError(buf, 256) == 0
+
+
+def test_one_hip_runtime_whatever_the_import_order():
+    # Importing llaisys_amd before torch must not map a second libamdhip64.
+    import subprocess
+    import sys
+
+    code = (
+        "import os, llaisys_amd, torch\n"
+        "segs = {l.split()[-1] for l in open(f'/proc/{os.getpid()}/maps') if 'amdhip64' in l and 'r-xp' in l}\n"
+        "print(len(segs))\n"
+    )
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=str(ROOT))
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "1"
