@@ -1,0 +1,376 @@
+"""Benchmark of the LLAISYS KV-cache hot path on one MI355X.
+
+Default workload: batched paged decode attention, B=64,
+context lengths U[512, 8192] (seeded), 16-token pages over a randomly permuted
+pool, GQA 12 query heads : 2 KV heads, head_dim 128, bf16 Q/K/V, fp32
+accumulation, split-KV flash-decoding with the log-sum-exp combine.
+
+One step = one llaisysPagedAttention call over the whole batch (one kernel
+launch). Inputs are resident in HBM before timing. Two independent copies of
+the inputs (pools, tables, queries) alternate between steps so that no step
+finds the previous step's KV in the 256 MB MALL.
+
+Printed (rank 0, one JSON line): the metric of BASELINE.json = achieved HBM
+GB/s of the attention kernel (algorithmic bytes / average kernel time from HIP
+events on the stream the kernel runs on), with tokens/s, the roofline
+fraction against 8 TB/s and a CPU baseline (the C oracle on host cores, a
+bounded sample of the same workload).
+
+Other workloads (parity configs, for measurement): --workload append_gather
+(config 2), mixed (config 4), copy (plain device copy, for rocprof counter
+calibration).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+SCALE = 1.0 / 128 ** 0.5
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy"])
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args()
+
+
+# ----------------------------------------------------------------- inputs
+
+
+def seeded_ints(seed, n, lo, hi):
+    import oracle  # seeded generator only (same draws as the parity tests)
+
+    return oracle.randint(seed, n, lo, hi).astype("int32")
+
+
+class Instance:
+    """One resident copy of a paged-attention problem (pools, table, lengths, q)."""
+
+    def __init__(self, ctx, lq, seed, dev_torch):
+        import numpy as np
+        import torch
+
+        import llaisys_amd as L
+
+        self.ctx = np.asarray(ctx, np.int32)
+        self.lq = np.asarray(lq, np.int32)
+        pages = (self.ctx + 15) // 16
+        self.maxp = int(pages.max())
+        self.nb = int(pages.sum())
+        g = torch.Generator(device=dev_torch).manual_seed(seed)
+        perm = torch.randperm(self.nb, generator=g, device=dev_torch).to(torch.int32).cpu().numpy()
+        table = np.full((len(self.ctx), self.maxp), -1, np.int32)
+        used = 0
+        for b, p in enumerate(pages):
+            table[b, :p] = perm[used:used + p]
+            used += p
+        self.table_np = table
+        self.T = int(self.lq.sum())
+
+        def resident(t):
+            """Move a torch tensor into a llaisys tensor and drop the torch copy."""
+            lt = L.Tensor(tuple(t.shape), dtype={torch.bfloat16: L.DataType.BF16, torch.int32: L.DataType.I32,
+                                                  torch.float32: L.DataType.F32}[t.dtype], device=L.DeviceType.AMD)
+            L.RuntimeAPI(L.DeviceType.AMD).memcpy_sync(lt.data_ptr(), t.data_ptr(), t.numel() * t.element_size(),
+                                                       L.MemcpyKind.D2D)
+            return lt
+
+        shape = (self.nb, 2, 16, 128)
+        # i.i.d. N(0,1) values: any permutation inside a page is the same distribution.
+        self.k_pool = resident(torch.randn(shape, generator=g, device=dev_torch, dtype=torch.float32).to(torch.bfloat16))
+        self.v_pool = resident(torch.randn(shape, generator=g, device=dev_torch, dtype=torch.float32).to(torch.bfloat16))
+        self.q = resident(torch.randn((self.T, 12, 128), generator=g, device=dev_torch).to(torch.bfloat16))
+        self.out = resident(torch.zeros((self.T, 12, 128), device=dev_torch, dtype=torch.bfloat16))
+        self.table = resident(torch.from_numpy(table).to(dev_torch))
+        self.ctx_t = resident(torch.from_numpy(self.ctx).to(dev_torch))
+        cu = np.concatenate([[0], np.cumsum(self.lq)]).astype(np.int32)
+        self.cu_np = cu
+        self.cu_q = resident(torch.from_numpy(cu).to(dev_torch))
+        torch.cuda.synchronize()
+
+    def algorithmic_bytes(self):
+        """KV read once per (token, kv head) + q + out + table + lengths (bf16 KV = 1024 B/token)."""
+        kv = int(self.ctx.sum()) * 2 * 2 * 128 * 2
+        qo = 2 * self.T * 12 * 128 * 2
+        meta = int(((self.ctx + 15) // 16).sum()) * 4 + len(self.ctx) * 4
+        return kv + qo + meta
+
+    def decode(self, L):
+        L.Ops.paged_attention(self.out, self.q, self.k_pool, self.v_pool, self.table, self.ctx_t, SCALE)
+
+    def mixed(self, L):
+        L.Ops.paged_attention_varlen(self.out, self.q, self.k_pool, self.v_pool, self.table, self.cu_q, self.ctx_t,
+                                     SCALE)
+
+
+# ----------------------------------------------------------------- timing
+
+
+def time_steps(step, stream, steps, warmup):
+    """HIP events on the library's stream around exactly `steps` launches,
+    bracketed by device synchronisation; returns (avg kernel ms, wall ms/step)."""
+    import torch
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return start.elapsed_time(end) / steps, wall
+
+
+def cpu_baseline_decode(inst, budget_s):
+    """The C oracle (OpenMP over sequences) on the first sequences of the batch,
+    as many as fit ~budget_s; GB/s over the same per-token byte count."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from llaisys_amd import MemcpyKind, RuntimeAPI, DeviceType
+
+    api = RuntimeAPI(DeviceType.AMD)
+
+    def host_copy(lt, dtype, shape):
+        t = torch.empty(shape, dtype=dtype)
+        api.memcpy_sync(t.data_ptr(), lt.data_ptr(), t.numel() * t.element_size(), MemcpyKind.D2H)
+        return t
+
+    kdev = host_copy(inst.k_pool, torch.int16, (inst.nb, 2, 16, 128)).numpy().view(np.uint16)
+    vdev = host_copy(inst.v_pool, torch.int16, (inst.nb, 2, 16, 128)).numpy().view(np.uint16)
+    k_log = oracle.unpack_pages_np(kdev, False)
+    v_log = oracle.unpack_pages_np(vdev, True)
+    q = host_copy(inst.q, torch.int16, (inst.T, 12, 128)).numpy().view(np.uint16)
+    threads = min(os.cpu_count() or 1, 16)
+    # Grow the sample (a prefix of the batch) until one pass takes >= 1 s, then repeat within the budget.
+    nseq = 4
+    while True:
+        t0 = time.perf_counter()
+        oracle.paged_attention(q[:nseq], k_log, v_log, inst.table_np[:nseq], inst.ctx[:nseq], SCALE, nthreads=threads)
+        dt = time.perf_counter() - t0
+        if dt >= 1.0 or nseq >= len(inst.ctx):
+            break
+        nseq = min(len(inst.ctx), nseq * 2)
+    reps, total = 0, 0.0
+    while total < budget_s:
+        t0 = time.perf_counter()
+        ref = oracle.paged_attention(q[:nseq], k_log, v_log, inst.table_np[:nseq], inst.ctx[:nseq], SCALE,
+                                     nthreads=threads)
+        total += time.perf_counter() - t0
+        reps += 1
+    sample_bytes = int(inst.ctx[:nseq].sum()) * 1024 + 2 * nseq * 12 * 128 * 2
+    # Sanity: the GPU result for the sample agrees with the CPU result.
+    got = host_copy(inst.out, torch.bfloat16, (inst.T, 12, 128))[:nseq].float().numpy()
+    max_err = float(np.max(np.abs(got - ref)))
+    return {
+        "value": round(sample_bytes * reps / total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle/oracle.c paged attention (fp32) on the first {nseq} of {len(inst.ctx)} sequences "
+                  f"({int(inst.ctx[:nseq].sum())} tokens), {reps} reps in {total:.1f} s; "
+                  f"GPU bf16 vs CPU max|err| {max_err:.2e}",
+    }
+
+
+# ----------------------------------------------------------------- workloads
+
+
+def run_decode(args):
+    import numpy as np
+    import torch
+
+    import llaisys_amd as L
+
+    B = 64
+    ctx = seeded_ints(args.seed, B, 512, 8192)
+    insts = [Instance(ctx, np.ones(B, np.int32), args.seed + 1 + i, "cuda") for i in range(2)]
+    stream = torch.cuda.ExternalStream(L.context_stream())
+    kern_ms, wall_ms = time_steps(lambda i: insts[i % 2].decode(L), stream, args.steps, args.warmup)
+    assert L.device_error_flags() == 0
+    nbytes = insts[0].algorithmic_bytes()
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    line = {
+        "metric": "paged decode attention achieved HBM GB/s (% of peak) + decode tokens/s, 1 GPU",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "kernel_ms": round(kern_ms, 5),
+        "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "decode_tokens_per_s": round(B / (kern_ms * 1e-3), 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V, seeded context lengths and block permutation)",
+        "config": {
+            "workload": "batched paged decode attention (BASELINE config 3)",
+            "batch": B, "ctx_range": [512, 8192], "ctx_total": int(ctx.sum()), "block_size": 16,
+            "q_heads": 12, "kv_heads": 2, "head_dim": 128, "accumulate": "fp32",
+            "split": "split-KV, in-kernel log-sum-exp combine",
+            "pages_per_split": int(os.environ.get("LLAISYS_PAGES_PER_SPLIT", "16")),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("paged_decode_attention"),
+            "algorithmic_bytes_per_launch": nbytes,
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_decode(insts[0], args.cpu_seconds)
+    return line
+
+
+def run_mixed(args):
+    import numpy as np
+    import torch
+
+    import llaisys_amd as L
+
+    priors = np.array([0, 1024, 2048, 4096], np.int32)
+    dec = seeded_ints(args.seed + 60, 60, 256, 4096)
+    ctx = np.concatenate([priors + 512, dec]).astype(np.int32)
+    lq = np.concatenate([np.full(4, 512), np.ones(60)]).astype(np.int32)
+    insts = [Instance(ctx, lq, args.seed + 1 + i, "cuda") for i in range(2)]
+    stream = torch.cuda.ExternalStream(L.context_stream())
+    kern_ms, wall_ms = time_steps(lambda i: insts[i % 2].mixed(L), stream, args.steps, args.warmup)
+    assert L.device_error_flags() == 0
+    # Causal (query, key) pairs: prefill chunk queries see prior + i + 1 keys; decode queries see ctx keys.
+    pairs = sum(int(p) * 512 + 512 * 513 // 2 for p in priors) + int(dec.sum())
+    flops = pairs * 12 * 128 * 4
+    return {
+        "metric": "mixed chunked-prefill + decode paged attention TFLOP/s, 1 GPU",
+        "value": round(flops / (kern_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 5),
+        "kernel_ms": round(kern_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: 4x512 prefill chunks over priors {0,1024,2048,4096} + 60 decode"},
+        "roofline": {"bound": "mfma", "achieved": round(flops / (kern_ms * 1e-3) / 1e12, 3), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(flops / (kern_ms * 1e-3) / 1e12 / 2500.0, 4), "traffic": None},
+    }
+
+
+def run_append_gather(args):
+    import numpy as np
+    import torch
+
+    import llaisys_amd as L
+
+    B, nb = 32, 4096
+    seed = args.seed
+    while True:
+        lens = seeded_ints(seed, B, 1, 2048)
+        if ((lens + 16) // 16).sum() <= nb:
+            break
+        seed += 1
+    need = (lens + 16) // 16
+    maxp = int(need.max())
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    perm = torch.randperm(nb, generator=g, device="cuda").to(torch.int32).cpu().numpy()
+    table = np.full((B, maxp), -1, np.int32)
+    used = 0
+    for b, p in enumerate(need):
+        table[b, :p] = perm[used:used + p]
+        used += p
+    pool_k = torch.randn((nb, 2, 16, 128), device="cuda").to(torch.bfloat16)
+    pool_v = torch.randn((nb, 2, 16, 128), device="cuda").to(torch.bfloat16)
+    sys.path.insert(0, str(ROOT / "tests"))
+    from utils import to_llaisys
+
+    kp, vp = to_llaisys(pool_k), to_llaisys(pool_v)
+    kn = to_llaisys(torch.randn((B, 2, 128), device="cuda").to(torch.bfloat16))
+    vn = to_llaisys(torch.randn((B, 2, 128), device="cuda").to(torch.bfloat16))
+    tab = to_llaisys(torch.from_numpy(table))
+    ctx = to_llaisys(torch.from_numpy(lens))
+    cu = np.concatenate([[0], np.cumsum(lens + 1)]).astype(np.int32)
+    T = int(cu[-1])
+    ko = to_llaisys(torch.zeros((T, 2, 128), dtype=torch.bfloat16, device="cuda"))
+    vo = to_llaisys(torch.zeros((T, 2, 128), dtype=torch.bfloat16, device="cuda"))
+    cut = to_llaisys(torch.from_numpy(cu))
+    stream = torch.cuda.ExternalStream(L.context_stream())
+
+    def step(i):
+        L.Ops.paged_kv_append(kp, vp, kn, vn, tab, ctx)
+        L.Ops.paged_kv_gather(ko, vo, kp, vp, tab, cut)
+
+    kern_ms, wall_ms = time_steps(step, stream, args.steps, args.warmup)
+    nbytes = 2 * T * 1024 + 2 * B * 1024
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    return {
+        "metric": "paged KV append+gather achieved HBM GB/s, 1 GPU", "value": round(gbs, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 5),
+        "kernel_ms": round(kern_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "BASELINE config 2: 32 seqs len U[1,2048], 4096-block pool, append 1 + gather"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+
+
+def run_copy(args):
+    """A plain 512 MiB device copy, to calibrate rocprof FETCH_SIZE/WRITE_SIZE."""
+    import torch
+
+    n = 512 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    stream = torch.cuda.current_stream()
+    kern_ms, wall_ms = time_steps(lambda i: b.copy_(a), stream, args.steps, args.warmup)
+    return {"metric": "device copy GB/s (read+write)", "value": round(2 * n / (kern_ms * 1e-3) / 1e9, 2),
+            "unit": "GB/s", "bytes_per_launch_read": n, "bytes_per_launch_written": n, "kernel_ms": kern_ms}
+
+
+def traffic_from_profiles(kernel_tag):
+    """HBM bytes per launch measured by rocprofv3 PMC, if a summary is committed under profiles/."""
+    f = ROOT / "profiles" / f"{kernel_tag}_traffic.json"
+    if f.is_file():
+        try:
+            return json.loads(f.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the KV-cache path "
+              "is built and measured on a single MI355X", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    line = {"decode": run_decode, "mixed": run_mixed, "append_gather": run_append_gather, "copy": run_copy}[
+        args.workload](args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

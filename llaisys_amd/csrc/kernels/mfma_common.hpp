@@ -1,0 +1,162 @@
+// Shared pieces of the gfx950 paged-attention kernels: vector types, the
+// bf16 MFMA, and the page-pair step (scores, online softmax, P.V).
+//
+// Lane layout (64 lanes, n = lane % 16 "column", grp = lane / 16):
+//   S^T[16 keys x 16 cols] = K_page[16 x 128] . Q^T[128 x 16]
+//       4 x v_mfma_f32_16x16x32_bf16 per page; A operand (K) is one
+//       coalesced 1 KiB load per 32 dims thanks to the K page format;
+//       the accumulator gives each lane keys 4*grp+i of its column.
+//   O^T[128 x 16 cols] += V^T[128 x 32 keys] . P^T[32 keys x 16 cols]
+//       the 32 keys are 2 pages; key slot 8*grp+e is page A key 4*grp+e
+//       (e<4) or page B key 4*grp+e-4, which is exactly what the S^T
+//       accumulators of the two pages hold and what one 16 B load of the V
+//       page format holds per 16-dim block pair. P = hi + lo (two bf16), so
+//       the product is accurate to ~2^-17 relative, V being exact bf16.
+// Nothing crosses lanes except the running max (2 shuffles).
+#pragma once
+
+#include "launch.hpp"
+
+#include <hip/hip_runtime.h>
+
+namespace llaisys::kernels::mfma {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kErrBadBlock = 1;
+constexpr int kErrTooLong = 2;
+
+__device__ __forceinline__ bf16x8 asBf16(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float exp2Fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Keeps the 16-bit halves of a word whose key is valid.
+__device__ __forceinline__ uint32_t keepPair(bool lo, bool hi) {
+    return (lo ? 0x0000ffffu : 0u) | (hi ? 0xffff0000u : 0u);
+}
+
+// Registers of one page pair (K and V of pages A and B).
+struct PagePair {
+    u32x4 ka[4], kb[4], va[4], vb[4];
+};
+
+// Issue the 16 loads of a page pair: page bases in u32x4 units, lane offset applied.
+__device__ __forceinline__ void loadPair(PagePair &r, const u32x4 *kp, const u32x4 *vp, size_t oa, size_t ob) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        r.ka[s] = __builtin_nontemporal_load(kp + oa + s * 64);
+        r.kb[s] = __builtin_nontemporal_load(kp + ob + s * 64);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        r.va[s] = __builtin_nontemporal_load(vp + oa + s * 64);
+        r.vb[s] = __builtin_nontemporal_load(vp + ob + s * 64);
+    }
+}
+
+// Running attention state of one lane (its column, its 32 output dims).
+struct Acc {
+    f32x4 o[8];
+    float m;
+    float l;
+    __device__ __forceinline__ void reset() {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m = -INFINITY;
+        l = 0.f;
+    }
+};
+
+// Consume one page pair. first_key = key position of page A's token 0;
+// pos = last key this lane's column may see (-1: none); ctx = keys in cache
+// (keys >= ctx are stale bytes and get zeroed V); hasB = page B exists.
+__device__ __forceinline__ void consumePair(Acc &acc, PagePair &r, const u32x4 (&qop)[4], int first_key, int pos,
+                                           int ctx, bool hasB, int grp, float scale_log2) {
+    f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        sa = mfma(asBf16(r.ka[s]), asBf16(qop[s]), sa);
+        sb = mfma(asBf16(r.kb[s]), asBf16(qop[s]), sb);
+    }
+    const int kbase = first_key + grp * 4;
+    float sv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sv[i] = (kbase + i <= pos) ? sa[i] * scale_log2 : -INFINITY;
+        sv[4 + i] = (hasB && kbase + 16 + i <= pos) ? sb[i] * scale_log2 : -INFINITY;
+    }
+    float mloc = sv[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mloc = fmaxf(mloc, sv[i]);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const float m_new = fmaxf(acc.m, mloc);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = exp2Fast(acc.m - m_use);
+    float p[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        p[i] = exp2Fast(sv[i] - m_use);
+        psum += p[i];
+    }
+    acc.l = acc.l * alpha + psum;
+    acc.m = m_new;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc.o[i] *= alpha;
+
+    bf16x8 phi, plo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const __bf16 hi = (__bf16)p[i];
+        phi[i] = hi;
+        plo[i] = (__bf16)(p[i] - (float)hi);
+    }
+
+    // Keys at or past ctx may hold stale bytes (even NaN patterns): zero their
+    // V so 0 * V stays 0. Only a sequence's last pair has any.
+    if (first_key + 32 > ctx || !hasB) {
+        const uint32_t ma01 = keepPair(kbase < ctx, kbase + 1 < ctx);
+        const uint32_t ma23 = keepPair(kbase + 2 < ctx, kbase + 3 < ctx);
+        const uint32_t mb01 = hasB ? keepPair(kbase + 16 < ctx, kbase + 17 < ctx) : 0u;
+        const uint32_t mb23 = hasB ? keepPair(kbase + 18 < ctx, kbase + 19 < ctx) : 0u;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            r.va[s] &= u32x4{ma01, ma23, ma01, ma23};
+            r.vb[s] &= u32x4{mb01, mb23, mb01, mb23};
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const bf16x8 v0 = asBf16(u32x4{r.va[s][0], r.va[s][1], r.vb[s][0], r.vb[s][1]});
+        const bf16x8 v1 = asBf16(u32x4{r.va[s][2], r.va[s][3], r.vb[s][2], r.vb[s][3]});
+        acc.o[2 * s] = mfma(v0, phi, acc.o[2 * s]);
+        acc.o[2 * s] = mfma(v0, plo, acc.o[2 * s]);
+        acc.o[2 * s + 1] = mfma(v1, phi, acc.o[2 * s + 1]);
+        acc.o[2 * s + 1] = mfma(v1, plo, acc.o[2 * s + 1]);
+    }
+}
+
+// Output dims of lane (n, grp) for block i: 16*i + 4*grp + {0..3}.
+template <bool OUT_F32>
+__device__ __forceinline__ void storeOut(void *out, size_t row_base, int blk, int grp, f32x4 v) {
+    const size_t idx = row_base + blk * 16 + grp * 4;
+    if constexpr (OUT_F32) {
+        *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + idx) = v;
+    } else {
+        const __bf16 e0 = (__bf16)v[0], e1 = (__bf16)v[1], e2 = (__bf16)v[2], e3 = (__bf16)v[3];
+        const uint32_t w0 =
+            uint32_t(__builtin_bit_cast(uint16_t, e0)) | (uint32_t(__builtin_bit_cast(uint16_t, e1)) << 16);
+        const uint32_t w1 =
+            uint32_t(__builtin_bit_cast(uint16_t, e2)) | (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
+        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + idx) = make_uint2(w0, w1);
+    }
+}
+
+} // namespace llaisys::kernels::mfma

@@ -211,17 +211,14 @@ __global__ void __launch_bounds__(64) pagedAttentionKernel(Args a) {
     float m = -INFINITY;
     float lsum = 0.f;
 
-    PageRegs cur, nxt;
-    load(p0, cur);
-    for (int pp = p0; pp < p1; pp += 2) {
-        if (pp + 2 < p1) load(pp + 2, nxt);
+    // One page pair: scores, online softmax, P.V. Loads for it were issued earlier.
+    auto consume = [&](PageRegs &r, int pp) {
         const bool hasB = pp + 1 < p1;
-
         f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            sa = mfma(asBf16(cur.ka[s]), asBf16(qop[s]), sa);
-            sb = mfma(asBf16(cur.kb[s]), asBf16(qop[s]), sb);
+            sa = mfma(asBf16(r.ka[s]), asBf16(qop[s]), sa);
+            sb = mfma(asBf16(r.kb[s]), asBf16(qop[s]), sb);
         }
         const int kbase = pp * 16 + grp * 4;
         float sv[8];
@@ -267,20 +264,33 @@ __global__ void __launch_bounds__(64) pagedAttentionKernel(Args a) {
             const uint32_t mb23 = hasB ? keepPair(kbase + 18 < ctx, kbase + 19 < ctx) : 0u;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                cur.va[s] &= u32x4{ma01, ma23, ma01, ma23};
-                cur.vb[s] &= u32x4{mb01, mb23, mb01, mb23};
+                r.va[s] &= u32x4{ma01, ma23, ma01, ma23};
+                r.vb[s] &= u32x4{mb01, mb23, mb01, mb23};
             }
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const bf16x8 v0 = asBf16(u32x4{cur.va[s][0], cur.va[s][1], cur.vb[s][0], cur.vb[s][1]});
-            const bf16x8 v1 = asBf16(u32x4{cur.va[s][2], cur.va[s][3], cur.vb[s][2], cur.vb[s][3]});
+            const bf16x8 v0 = asBf16(u32x4{r.va[s][0], r.va[s][1], r.vb[s][0], r.vb[s][1]});
+            const bf16x8 v1 = asBf16(u32x4{r.va[s][2], r.va[s][3], r.vb[s][2], r.vb[s][3]});
             o[2 * s] = mfma(v0, phi, o[2 * s]);
             o[2 * s] = mfma(v0, plo, o[2 * s]);
             o[2 * s + 1] = mfma(v1, phi, o[2 * s + 1]);
             o[2 * s + 1] = mfma(v1, plo, o[2 * s + 1]);
         }
-        cur = nxt;
+    };
+
+    // Two register sets in a ring, loads always issued (past the end they
+    // re-read the last pair, an L2 hit) so the compiler can count the loads
+    // in flight and wait only for the set about to be consumed.
+    const int last_pair = p0 + ((p1 - 1 - p0) & ~1);
+    PageRegs ra, rb;
+    load(p0, ra);
+    load(min(p0 + 2, last_pair), rb);
+    for (int pp = p0; pp < p1; pp += 4) {
+        consume(ra, pp);
+        load(min(pp + 4, last_pair), ra);
+        if (pp + 2 < p1) consume(rb, pp + 2);
+        load(min(pp + 6, last_pair), rb);
     }
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);

@@ -3,6 +3,8 @@
 #include "../common.hpp"
 #include "../kernels/launch.hpp"
 
+#include <algorithm>
+
 namespace llaisys::ops {
 
 namespace {
@@ -205,8 +207,29 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
     if (T == 0 || B == 0) return;
     const int max_pages = int(block_table->shape()[1]);
     LLAISYS_CHECK(max_pages > 0, op << ": block_table has no pages");
-    auto plan = K::planPagedAttention(int(B), int(T), int(nkvh), int(nh / nkvh), max_pages, bool(cu_q));
     auto &rt = core::context().runtime();
+    const int G = int(nh / nkvh);
+    if (!cu_q) {
+        // Decode: sequences are independent, so large batches run in chunks
+        // whose length prefix fits the kernel's LDS.
+        for (size_t b0 = 0; b0 < B; b0 += K::kDecodeMaxBatch) {
+            const int Bc = int(std::min<size_t>(K::kDecodeMaxBatch, B - b0));
+            auto plan = K::planDecode(Bc, int(nkvh), G, max_pages);
+            float *records = static_cast<float *>(rt.scratch(plan.record_bytes));
+            const size_t esz = out->dtype() == LLAISYS_DTYPE_F32 ? 4 : 2;
+            K::pagedDecode(static_cast<std::byte *>(out->data()) + b0 * nh * K::kHeadDim * esz,
+                           out->dtype() == LLAISYS_DTYPE_F32,
+                           reinterpret_cast<const uint16_t *>(q->data()) + b0 * nh * K::kHeadDim,
+                           reinterpret_cast<const uint16_t *>(k_pool->data()),
+                           reinterpret_cast<const uint16_t *>(v_pool->data()),
+                           reinterpret_cast<const int32_t *>(block_table->data()) + b0 * size_t(max_pages),
+                           reinterpret_cast<const int32_t *>(ctx_len->data()) + b0, Bc, int(nh), int(nkvh),
+                           max_pages, int(k_pool->shape()[0]), scale, plan, records,
+                           rt.counters(1), rt.errorWord(), rt.stream());
+        }
+        return;
+    }
+    auto plan = K::planPagedAttention(int(B), int(T), int(nkvh), G, max_pages, true);
     float *partial = plan.max_splits > 1 ? static_cast<float *>(rt.scratch(plan.partial_bytes)) : nullptr;
     int *counters = rt.counters(size_t(plan.units_padded));
     K::pagedAttention(out->data(), out->dtype() == LLAISYS_DTYPE_F32, reinterpret_cast<const uint16_t *>(q->data()),
@@ -214,9 +237,8 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
                       reinterpret_cast<const uint16_t *>(v_pool->data()),
                       reinterpret_cast<const int32_t *>(block_table->data()),
                       reinterpret_cast<const int32_t *>(ctx_len->data()),
-                      cu_q ? reinterpret_cast<const int32_t *>(cu_q->data()) : nullptr, int(B), int(T), int(nh),
-                      int(nkvh), max_pages, int(k_pool->shape()[0]), scale, plan, partial, counters, rt.errorWord(),
-                      rt.stream());
+                      reinterpret_cast<const int32_t *>(cu_q->data()), int(B), int(T), int(nh), int(nkvh), max_pages,
+                      int(k_pool->shape()[0]), scale, plan, partial, counters, rt.errorWord(), rt.stream());
 }
 
 } // namespace llaisys::ops

@@ -23,7 +23,8 @@ from .ops import load_ops
 from .runtime import LlaisysRuntimeAPI, load_runtime
 from .tensor import llaisysTensor_t, load_tensor
 
-LIB_PATH = Path(__file__).resolve().parent / "libllaisys.so"
+# LLAISYS_LIBRARY may name another build of the same library (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("LLAISYS_LIBRARY") or Path(__file__).resolve().parent / "libllaisys.so")
 
 
 def _share_hip_runtime():
