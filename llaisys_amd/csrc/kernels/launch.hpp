@@ -27,10 +27,10 @@ void pagedGather(uint16_t *k_out, uint16_t *v_out, const uint16_t *k_pool, const
                  const int32_t *block_table, const int32_t *cu_seqlens, int T, int B, int nkvh, int max_pages,
                  int num_blocks, int *err, void *stream);
 
-// Batched decode (one query per sequence): persistent waves over a dynamic
-// queue of page-pair chunks, then a combine kernel.
+// Batched decode (one query per sequence): stream-K over all page pairs, then
+// a combine kernel for sequences split across waves.
 struct DecodePlan {
-    int waves;           // persistent grid of single-wave workgroups
+    int waves;           // grid of single-wave workgroups
     int stages;          // page pairs in flight per wave
     size_t record_bytes; // workspace for split records
     size_t lds_bytes;    // per-workgroup LDS (length prefix)
@@ -39,8 +39,7 @@ constexpr int kDecodeMaxBatch = 4096; // sequences per launch (LDS-resident pref
 DecodePlan planDecode(int B, int nkvh, int group, int max_pages);
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                  const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *queue, int *err,
-                 void *stream);
+                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *err, void *stream);
 
 struct PagedAttentionPlan {
     int units;          // (query tile, kv head) work units

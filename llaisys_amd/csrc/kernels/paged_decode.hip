@@ -1,26 +1,26 @@
-// Batched paged decode attention for gfx950: flash-decoding over a dynamic
-// queue of page-pair chunks.
+// Batched paged decode attention for gfx950: stream-K flash-decoding.
 //
 // Work = every (sequence b, kv head h) unit's page pairs, laid end to end:
 // unit u = b*nkvh + h owns npairs(b) = ceil(ceil(ctx_b/16)/2) consecutive
-// pair indices; chunk c is pairs [c*kChunk, (c+1)*kChunk). A persistent grid
-// of single-wave workgroups (about one per SIMD) takes chunks from a global
-// atomic counter, so waves on faster XCDs simply take more chunks. Each wave
-// streams its chunks through a ring of NSTAGE page pairs in flight; the next
-// chunk's id is taken two chunks ahead and its block ids one chunk ahead, so
-// the ring never drains between chunks. Every wave does the same small prefix
-// scan of ctx into LDS to map pair indices to (b, h, page), so no host-side
-// knowledge of the lengths and no planning kernel is needed.
+// pair indices. A grid of W single-wave workgroups (about two per CU) splits
+// the N pairs evenly: wave w takes pairs [w*N/W, (w+1)*N/W), at most 64, and
+// streams them through a ring of NSTAGE page pairs in flight, crossing unit
+// boundaries without draining the ring. Every wave does the same small prefix
+// scan of ctx into LDS to find its slice, so no host-side knowledge of the
+// lengths and no planning kernel is needed.
 //
-// A unit whose pairs all fall in one chunk is finished there (normalised
-// output). Otherwise each chunk holding part of it writes a record
-// (unnormalised O, running max m, sum l) into slot 0 (the chunk's first unit)
-// or slot 1 (its last unit), and the combine kernel, launched next on the same
-// stream, merges the records with log-sum-exp weights and resets the queue
-// counter. The kernel boundary orders records before the merge: no wave ever
-// waits on another, and no cache-maintaining fences are issued.
+// A unit whose pairs all fall in one wave is finished by that wave
+// (normalised output). Otherwise every wave holding part of it writes a
+// record (unnormalised O, running max m, sum l) into one of its two slots
+// (slot 0: its first unit, slot 1: its last), and the combine kernel,
+// launched next on the same stream, merges each split unit's records with
+// log-sum-exp weights. The kernel boundary makes the records visible to the
+// combine on every XCD. (Merging inside this kernel instead needs either
+// agent-scope fences, which write back / invalidate a whole L2 per wave, or
+// device-scope record traffic plus a serial merge at the tail; both measured
+// slower than the second launch.)
 //
-// Per pair the wave reads 16 KiB of K/V plus the unit's query rows (1 KiB per
+// Per pair a wave reads 16 KiB of K/V plus the unit's query rows (1 KiB per
 // 16 columns, from L2) and issues 24 MFMAs (mfma_common.hpp has the layout).
 #include "mfma_common.hpp"
 
@@ -37,7 +37,8 @@ namespace {
 
 using namespace mfma;
 
-constexpr int kChunk = 4; // page pairs per queue entry
+constexpr int kPairsPerWave = 64; // one pair per lane in the wave's block-id window
+constexpr int kMergeBatch = 4;    // records whose loads are in flight together
 
 struct DecodeArgs {
     const uint16_t *q;
@@ -47,7 +48,6 @@ struct DecodeArgs {
     const int32_t *table;
     const int32_t *ctx;
     float *records;
-    int *counters;
     int *err;
     int B, nh, nkvh, G, max_pages, num_blocks, W;
     float scale_log2;
@@ -55,10 +55,10 @@ struct DecodeArgs {
 
 // Exclusive prefix (over b) of nkvh * npairs(b) into S[0..B], lengths into C.
 // Invalid lengths (< 1 or beyond the block table) count as empty and raise
-// kErrTooLong when `report`. Returns the total pair count N. Run by the first
-// wave of the workgroup only; the caller synchronises before reading S/C.
+// kErrTooLong when `report`. Returns the total pair count N. One wave; the
+// caller synchronises before reading S/C from other waves.
 __device__ int scanPairs(const DecodeArgs &a, int *S, int *C, bool report) {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     int carry = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int bb = base + lane;
@@ -87,97 +87,95 @@ __device__ int scanPairs(const DecodeArgs &a, int *S, int *C, bool report) {
     return carry;
 }
 
+__device__ __forceinline__ int waveStart(long long w, long long N, long long W) { return int(w * N / W); }
+
+// Wave holding pair g: the largest w with waveStart(w) <= g.
+__device__ __forceinline__ int waveOf(long long g, long long N, long long W) {
+    const long long w = ((g + 1) * W + N - 1) / N - 1;
+    return int(w < W - 1 ? w : W - 1);
+}
+
+// Record r (2 per wave) holds, for the G live columns, O as 128*G floats in
+// [blk][col][dims 4*grp .. 4*grp+3] order, so a lane's 16 B access for one
+// block lands in a contiguous G*64 B run, then (m, l) per column.
+__device__ __forceinline__ float *recordAt(const DecodeArgs &a, int r) {
+    return a.records + size_t(r) * a.G * (kHeadDim + 2);
+}
+__device__ __forceinline__ int recordO(int G, int blk, int col, int grp) { return (blk * G + col) * 16 + grp * 4; }
+__device__ __forceinline__ int recordML(int G, int col) { return G * kHeadDim + 2 * col; }
+
 template <int NSTAGE> struct Ring {
     PagePair pp[NSTAGE];
     u32x4 q[NSTAGE][4];
 };
 
-// Lane i < kChunk describes pair chunk*kChunk + i (clamped into the chunk and
-// below N): sequence, kv head, pair index within the unit, block ids.
-struct Window {
-    int b, h, j, bidA, bidB;
-};
-
-__device__ Window loadWindow(const DecodeArgs &a, const int *S, const int *C, int chunk, int N) {
-    const int lane = threadIdx.x;
-    const int g = min(chunk * kChunk + min(lane, kChunk - 1), N - 1);
-    int lo = 0, hi = a.B - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (S[mid] <= g)
-            lo = mid;
-        else
-            hi = mid - 1;
-    }
-    Window w;
-    w.b = lo;
-    const int np = (C[lo] + 15) >> 4;
-    const int npr = (np + 1) >> 1;
-    const int rem = g - S[lo];
-    w.h = rem / npr;
-    w.j = rem - w.h * npr;
-    const int pa = 2 * w.j;
-    const int pb = min(pa + 1, np - 1);
-    const int32_t *row = a.table + size_t(lo) * a.max_pages;
-    // Range-checked where used (issue): checking here would wait on the load.
-    w.bidA = row[pa];
-    w.bidB = row[pb];
-    return w;
-}
-
 template <bool OUT_F32, int NSTAGE>
 __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
-    static_assert(kChunk % NSTAGE == 0, "ring slots must line up across chunks");
     extern __shared__ int lds[];
     int *S = lds;
     int *C = lds + a.B + 1;
     const int lane = threadIdx.x;
     const int n = lane & 15;
     const int grp = lane >> 4;
+    const int w = blockIdx.x;
     const int G = a.G;
-    int *queue = a.counters;
 
-    const int N = scanPairs(a, S, C, blockIdx.x == 0);
+    const int N = scanPairs(a, S, C, w == 0);
     __syncthreads();
-    const int NC = (N + kChunk - 1) / kChunk;
-    // Chunks w and W + w are this wave's by construction; later ones come from
-    // the queue, which hands out 2W, 2W+1, ... (all waves hitting one counter
-    // at kernel start would serialise on it). A queue value stays in lane 0 of
-    // a vector register until read (chunkOf): reading it forces a wait on the
-    // atomic, and with in-order load counters that wait would drain the load
-    // ring, so every id is taken a full chunk before it is read.
-    const int W = gridDim.x;
-    auto grab = [&]() {
-        int c = 0;
-        if (lane == 0) c = atomicAdd(queue, 1);
-        return c;
-    };
-    auto chunkOf = [&](int raw) { return 2 * W + __builtin_amdgcn_readfirstlane(raw); };
-    int c_cur = blockIdx.x;
-    if (c_cur >= NC) return;
-    int c_nxt = W + blockIdx.x;
-    Window cur = loadWindow(a, S, C, c_cur, N);
-    Window nxt = loadWindow(a, S, C, min(c_nxt, NC - 1), N);
-    int raw_after = grab();
+    const int s = waveStart(w, N, a.W);
+    const int e = waveStart(w + 1, N, a.W);
+    const int cnt = e - s;
+    if (cnt <= 0) return;
+    if (cnt > kPairsPerWave) { // the host sizes W so this cannot happen
+        if (lane == 0) atomicOr(a.err, kErrTooLong);
+        return;
+    }
+
+    // Block-id window: lane i describes pair s + i. Block ids are range-checked
+    // where used (issue): checking here would wait on the loads.
+    int lb, lh, lj, bidA, bidB;
+    {
+        const int g = s + min(lane, cnt - 1);
+        int lo = 0, hi = a.B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (S[mid] <= g)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        lb = lo;
+        const int np = (C[lb] + 15) >> 4;
+        const int npr = (np + 1) >> 1;
+        const int rem = g - S[lb];
+        lh = rem / npr;
+        lj = rem - lh * npr;
+        const int pa = 2 * lj;
+        const int pb = min(pa + 1, np - 1);
+        const int32_t *row = a.table + size_t(lb) * a.max_pages;
+        bidA = row[pa];
+        bidB = row[pb];
+    }
 
     const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
     const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
     const int ncol = min(n, G - 1); // columns past G read a valid row and are masked later
 
     Ring<NSTAGE> ring;
-    // Load page pair (window `use_nxt ? nxt : cur`, lane k) into ring slot st.
-    // The window choice is a uniform select, never a branch around the loads,
-    // so the compiler can keep counting the loads in flight.
     bool bad_block = false;
-    auto issue = [&](int st, bool use_nxt, int k) {
-        int bA = use_nxt ? __builtin_amdgcn_readlane(nxt.bidA, k) : __builtin_amdgcn_readlane(cur.bidA, k);
-        int bB = use_nxt ? __builtin_amdgcn_readlane(nxt.bidB, k) : __builtin_amdgcn_readlane(cur.bidB, k);
+    // Pair k of the window into ring slot st; past the end it re-reads the
+    // last pair (an L2 hit), so loads are never conditional and the compiler
+    // can count them and wait only for the slot about to be consumed.
+    auto issue = [&](int st, int k) {
+        const int kk = min(k, cnt - 1);
+        int bA = __builtin_amdgcn_readlane(bidA, kk);
+        int bB = __builtin_amdgcn_readlane(bidB, kk);
         const bool bad = unsigned(bA) >= unsigned(a.num_blocks) || unsigned(bB) >= unsigned(a.num_blocks);
         bad_block |= bad;
         bA = bad ? 0 : bA;
         bB = bad ? 0 : bB;
-        const int b = use_nxt ? __builtin_amdgcn_readlane(nxt.b, k) : __builtin_amdgcn_readlane(cur.b, k);
-        const int h = use_nxt ? __builtin_amdgcn_readlane(nxt.h, k) : __builtin_amdgcn_readlane(cur.h, k);
+        const int b = __builtin_amdgcn_readlane(lb, kk);
+        const int h = __builtin_amdgcn_readlane(lh, kk);
         loadPair(ring.pp[st], kp, vp, (size_t(bA) * a.nkvh + h) * 256, (size_t(bB) * a.nkvh + h) * 256);
         const uint16_t *qrow = a.q + (size_t(b) * a.nh + h * G + ncol) * kHeadDim + grp * 8;
 #pragma unroll
@@ -187,7 +185,6 @@ __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
     Acc acc;
     acc.reset();
     int cur_b = -1, cur_h = 0;
-    int chunk_lo = 0, chunk_hi = 0; // pair range of the chunk being consumed
 
     auto finish = [&]() {
         float lt = acc.l + __shfl_xor(acc.l, 16);
@@ -195,40 +192,33 @@ __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
         const int np = (C[cur_b] + 15) >> 4;
         const int npr = (np + 1) >> 1;
         const int first = S[cur_b] + cur_h * npr;
-        if (first >= chunk_lo && first + npr <= chunk_hi) {
+        if (first >= s && first + npr <= e) {
             if (n < G) {
                 const float inv = 1.f / lt;
                 const size_t row = (size_t(cur_b) * a.nh + cur_h * G + n) * kHeadDim;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, acc.o[i] * inv);
             }
-        } else if (n < G) {
-            const int slot = first <= chunk_lo ? 0 : 1;
-            float *rec = a.records + size_t(2 * (chunk_lo / kChunk) + slot) * size_t(G * (kHeadDim + 2));
+            return;
+        }
+        if (n < G) {
+            float *rec = recordAt(a, 2 * w + (first <= s ? 0 : 1));
 #pragma unroll
-            for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4 *>(rec + n * kHeadDim + i * 16 + grp * 4) = acc.o[i];
-            if (grp == 0) {
-                rec[G * kHeadDim + 2 * n] = acc.m;
-                rec[G * kHeadDim + 2 * n + 1] = lt;
-            }
+            for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4 *>(rec + recordO(G, i, n, grp)) = acc.o[i];
+            if (grp == 0) *reinterpret_cast<float2 *>(rec + recordML(G, n)) = make_float2(acc.m, lt);
         }
     };
 
-    int len_cur = min(kChunk, N - c_cur * kChunk);
 #pragma unroll
-    for (int st = 0; st < NSTAGE; ++st) issue(st, false, min(st, len_cur - 1));
-    while (true) {
-        const bool more = c_nxt < NC;
-        const int len_nxt = more ? min(kChunk, N - c_nxt * kChunk) : 0;
-        chunk_lo = c_cur * kChunk;
-        chunk_hi = chunk_lo + len_cur;
+    for (int st = 0; st < NSTAGE; ++st) issue(st, st);
+    for (int k0 = 0; k0 < cnt; k0 += NSTAGE) {
 #pragma unroll
-        for (int p = 0; p < kChunk; ++p) {
-            const int st = p % NSTAGE;
-            if (p < len_cur) {
-                const int b = __builtin_amdgcn_readlane(cur.b, p);
-                const int h = __builtin_amdgcn_readlane(cur.h, p);
-                const int j = __builtin_amdgcn_readlane(cur.j, p);
+        for (int st = 0; st < NSTAGE; ++st) {
+            const int k = k0 + st;
+            if (k < cnt) {
+                const int b = __builtin_amdgcn_readlane(lb, k);
+                const int h = __builtin_amdgcn_readlane(lh, k);
+                const int j = __builtin_amdgcn_readlane(lj, k);
                 if (b != cur_b || h != cur_h) {
                     if (cur_b >= 0) finish();
                     acc.reset();
@@ -242,35 +232,21 @@ __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
                 for (int t = 0; t < 4; ++t) qop[t] = n < G ? ring.q[st][t] : u32x4{0, 0, 0, 0};
                 consumePair(acc, ring.pp[st], qop, 32 * j, c - 1, c, hasB, grp, a.scale_log2);
             }
-            // Refill this slot with the pair NSTAGE ahead (from the next chunk
-            // near the end; past the last chunk it re-reads a pair, an L2 hit).
-            const int q = p + NSTAGE;
-            if (q < kChunk)
-                issue(st, false, min(q, len_cur - 1));
-            else
-                issue(st, more, more ? min(q - kChunk, len_nxt - 1) : len_cur - 1);
+            issue(st, k + NSTAGE);
         }
-        finish();
-        cur_b = -1;
-        if (!more) break;
-        c_cur = c_nxt;
-        cur = nxt;
-        len_cur = len_nxt;
-        c_nxt = chunkOf(raw_after);
-        nxt = loadWindow(a, S, C, min(c_nxt, NC - 1), N);
-        raw_after = grab();
     }
+    finish();
     if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
 }
 
-// Merge the records of every unit that spans more than one chunk.
-// 256 threads = 4 waves per unit. Wave 0 scans the lengths into LDS; then
-// wave v takes every 4th batch of the unit's records, with all loads of a
-// batch in flight, and merges them online (O = sum 2^(m_r - M) O_r, l
-// likewise); the four partial states meet in LDS and wave 0 writes the
-// output. Block 0 also resets the chunk queue for the next launch.
+// Merge the records of every unit that spans more than one wave.
+// 256 threads = 4 waves per unit. Wave 0 scans the lengths into LDS. Lane k
+// works out which wave/slot record k of the unit lives in (the integer
+// divisions run lane-parallel); wave v then takes records v, v+4, ... in
+// batches with all loads of a batch in flight, merging online
+// (O = sum_r 2^(m_r - M) O_r, l likewise); the four partial states meet in
+// LDS and wave 0 writes the output.
 constexpr int kCombineWaves = 4;
-constexpr int kMergeBatch = 4;
 
 template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) decodeCombineKernel(DecodeArgs a) {
     extern __shared__ int lds[];
@@ -283,9 +259,9 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
     const int n = lane & 15;
     const int grp = lane >> 4;
     const int G = a.G;
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.counters[0] = 0;
     if (wave == 0) scanPairs(a, S, C, false);
     __syncthreads();
+    const int N = S[a.B];
     const int u = blockIdx.x;
     const int b = u / a.nkvh;
     const int h = u - b * a.nkvh;
@@ -293,45 +269,50 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
     const int npr = (np + 1) >> 1;
     if (npr == 0) return;
     const int first = S[b] + h * npr;
-    const int c0 = first / kChunk;
-    const int c1 = (first + npr - 1) / kChunk;
-    if (c0 == c1) return;
-    const int nrec = c1 - c0 + 1;
-    const size_t stride = size_t(G) * (kHeadDim + 2);
+    const int w0 = waveOf(first, N, a.W);
+    const int w1 = waveOf(first + npr - 1, N, a.W);
+    if (w0 == w1) return;
     const int col = min(n, G - 1);
-    // Record k of the unit: chunk c0 + k, slot 1 for chunk c0 unless the unit starts it.
-    auto recordOf = [&](int k) {
-        const int c = c0 + k;
-        return a.records + size_t(2 * c + ((k == 0 && first % kChunk != 0) ? 1 : 0)) * stride;
-    };
 
     float M = -INFINITY, L = 0.f;
     f32x4 o[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = wave * kMergeBatch; k0 < nrec; k0 += kCombineWaves * kMergeBatch) {
-        float mr[kMergeBatch], lr[kMergeBatch];
-        f32x4 orr[kMergeBatch][8];
-#pragma unroll
-        for (int t = 0; t < kMergeBatch; ++t) {
-            const float *rec = recordOf(min(k0 + t, nrec - 1));
-            mr[t] = rec[G * kHeadDim + 2 * col];
-            lr[t] = rec[G * kHeadDim + 2 * col + 1];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                orr[t][i] = *reinterpret_cast<const f32x4 *>(rec + col * kHeadDim + i * 16 + grp * 4);
-            if (k0 + t >= nrec) mr[t] = -INFINITY; // weight 0
+    for (int base = w0; base <= w1; base += 64) {
+        // Lane k: record of wave base+k, or -1 if that wave's range is empty
+        // (possible when N < W).
+        const int wk = base + lane;
+        int rec_k = -1;
+        if (wk <= w1) {
+            const int st = waveStart(wk, N, a.W);
+            if (waveStart(wk + 1, N, a.W) > st) rec_k = 2 * wk + ((wk == w0 && st < first) ? 1 : 0);
         }
+        const int cnt = min(64, w1 - base + 1);
+        for (int k0 = wave * kMergeBatch; k0 < cnt; k0 += kCombineWaves * kMergeBatch) {
+            float mr[kMergeBatch], lr[kMergeBatch];
+            f32x4 orr[kMergeBatch][8];
 #pragma unroll
-        for (int t = 0; t < kMergeBatch; ++t) {
-            if (mr[t] == -INFINITY) continue;
-            const float Mn = fmaxf(M, mr[t]);
-            const float sa = exp2Fast(M - Mn);
-            const float sb = exp2Fast(mr[t] - Mn);
-            L = L * sa + lr[t] * sb;
+            for (int t = 0; t < kMergeBatch; ++t) {
+                const int r = __builtin_amdgcn_readlane(rec_k, min(k0 + t, cnt - 1));
+                const float *rec = recordAt(a, r < 0 ? 0 : r);
+                const float2 ml = *reinterpret_cast<const float2 *>(rec + recordML(G, col));
+                mr[t] = ml.x;
+                lr[t] = ml.y;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = o[i] * sa + orr[t][i] * sb;
-            M = Mn;
+                for (int i = 0; i < 8; ++i) orr[t][i] = *reinterpret_cast<const f32x4 *>(rec + recordO(G, i, col, grp));
+                if (r < 0 || k0 + t >= cnt) mr[t] = -INFINITY; // weight 0
+            }
+#pragma unroll
+            for (int t = 0; t < kMergeBatch; ++t) {
+                if (mr[t] == -INFINITY) continue;
+                const float Mn = fmaxf(M, mr[t]);
+                const float sa = exp2Fast(M - Mn);
+                const float sb = exp2Fast(mr[t] - Mn);
+                L = L * sa + lr[t] * sb;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] = o[i] * sa + orr[t][i] * sb;
+                M = Mn;
+            }
         }
     }
     if (wave > 0) {
@@ -385,18 +366,17 @@ int computeUnits() {
 DecodePlan planDecode(int B, int nkvh, int group, int max_pages) {
     DecodePlan p{};
     const long long max_pairs = (long long)B * nkvh * ((max_pages + 1) / 2);
-    const long long max_chunks = (max_pairs + kChunk - 1) / kChunk;
-    p.waves = std::max(1, envInt("LLAISYS_DECODE_WAVES", 4 * computeUnits()));
-    p.record_bytes = size_t(2) * size_t(std::max(1LL, max_chunks)) * group * (kHeadDim + 2) * sizeof(float);
+    const int fill = std::max(1, envInt("LLAISYS_DECODE_WAVES", 2 * computeUnits()));
+    p.waves = int(std::max<long long>(fill, (max_pairs + kPairsPerWave - 1) / kPairsPerWave));
+    p.record_bytes = size_t(2) * p.waves * group * (kHeadDim + 2) * sizeof(float);
     p.lds_bytes = size_t(2 * B + 1) * sizeof(int);
-    p.stages = envInt("LLAISYS_DECODE_STAGES", 2) >= 4 ? 4 : 2;
+    p.stages = envInt("LLAISYS_DECODE_STAGES", 2) >= 3 ? 3 : 2;
     return p;
 }
 
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                  const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *counters, int *err,
-                 void *stream) {
+                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *err, void *stream) {
     if (B == 0) return;
     DecodeArgs a;
     a.q = q;
@@ -406,7 +386,6 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
     a.table = block_table;
     a.ctx = ctx_len;
     a.records = records;
-    a.counters = counters;
     a.err = err;
     a.B = B;
     a.nh = nh;
@@ -418,20 +397,19 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
     a.scale_log2 = scale * 1.4426950408889634f;
     auto s = static_cast<hipStream_t>(stream);
     const unsigned lds = unsigned(plan.lds_bytes);
-    const dim3 grid(plan.waves), comb(B * nkvh);
-    const dim3 one(64), four(64 * kCombineWaves);
+    const dim3 grid(plan.waves), block(64), comb(B * nkvh), comb_block(64 * kCombineWaves);
     if (out_f32) {
-        if (plan.stages == 4)
-            hipLaunchKernelGGL((decodeKernel<true, 4>), grid, one, lds, s, a);
+        if (plan.stages == 3)
+            hipLaunchKernelGGL((decodeKernel<true, 3>), grid, block, lds, s, a);
         else
-            hipLaunchKernelGGL((decodeKernel<true, 2>), grid, one, lds, s, a);
-        hipLaunchKernelGGL((decodeCombineKernel<true>), comb, four, lds, s, a);
+            hipLaunchKernelGGL((decodeKernel<true, 2>), grid, block, lds, s, a);
+        hipLaunchKernelGGL((decodeCombineKernel<true>), comb, comb_block, lds, s, a);
     } else {
-        if (plan.stages == 4)
-            hipLaunchKernelGGL((decodeKernel<false, 4>), grid, one, lds, s, a);
+        if (plan.stages == 3)
+            hipLaunchKernelGGL((decodeKernel<false, 3>), grid, block, lds, s, a);
         else
-            hipLaunchKernelGGL((decodeKernel<false, 2>), grid, one, lds, s, a);
-        hipLaunchKernelGGL((decodeCombineKernel<false>), comb, four, lds, s, a);
+            hipLaunchKernelGGL((decodeKernel<false, 2>), grid, block, lds, s, a);
+        hipLaunchKernelGGL((decodeCombineKernel<false>), comb, comb_block, lds, s, a);
     }
     HIP_CHECK(hipGetLastError());
 }

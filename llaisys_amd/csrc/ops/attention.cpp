@@ -224,8 +224,7 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
                            reinterpret_cast<const uint16_t *>(v_pool->data()),
                            reinterpret_cast<const int32_t *>(block_table->data()) + b0 * size_t(max_pages),
                            reinterpret_cast<const int32_t *>(ctx_len->data()) + b0, Bc, int(nh), int(nkvh),
-                           max_pages, int(k_pool->shape()[0]), scale, plan, records,
-                           rt.counters(1), rt.errorWord(), rt.stream());
+                           max_pages, int(k_pool->shape()[0]), scale, plan, records, rt.errorWord(), rt.stream());
         }
         return;
     }

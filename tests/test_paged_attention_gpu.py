@@ -57,8 +57,8 @@ def test_decode_edge_lengths(nh, nkvh):
 
 @pytest.mark.parametrize("waves", ["1", "7", "64", "1024", "5000"])
 def test_decode_wave_count_invariance(waves, monkeypatch):
-    # The grid size only changes which wave takes which chunk: from one wave
-    # doing everything to more waves than chunks (some find the queue empty).
+    # The grid size only changes where sequences are cut into records: from
+    # every unit whole in one wave to more waves than page pairs (empty ranges).
     ctx = oracle.randint(5, 9, 1, 3000).astype(np.int32)
     case = make_case(21, ctx)
     q = queries(22, case.B, 12)
@@ -67,7 +67,7 @@ def test_decode_wave_count_invariance(waves, monkeypatch):
     check(run_decode(case, q, torch.float32), run_decode(case, q, torch.bfloat16), ref)
 
 
-@pytest.mark.parametrize("stages", ["2", "4"])
+@pytest.mark.parametrize("stages", ["2", "3"])
 def test_decode_ring_depth(stages, monkeypatch):
     ctx = oracle.randint(6, 11, 1, 2000).astype(np.int32)
     case = make_case(23, ctx)
