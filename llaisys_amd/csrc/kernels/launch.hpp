@@ -27,8 +27,10 @@ void pagedGather(uint16_t *k_out, uint16_t *v_out, const uint16_t *k_pool, const
                  const int32_t *block_table, const int32_t *cu_seqlens, int T, int B, int nkvh, int max_pages,
                  int num_blocks, int *err, void *stream);
 
-// Batched decode (one query per sequence): stream-K over all page pairs, then
-// a combine kernel for sequences split across waves.
+// Batched decode: stream-K over all page pairs, then a combine kernel for
+// sequences split across waves. cu_q == nullptr: sequence b's query is row b
+// (T == B); else its row is cu_q[b] and sequences with cu_q[b+1]-cu_q[b] != 1
+// are skipped (left to pagedPrefill).
 struct DecodePlan {
     int waves;           // grid of single-wave workgroups
     int stages;          // page pairs in flight per wave
@@ -38,24 +40,23 @@ struct DecodePlan {
 constexpr int kDecodeMaxBatch = 4096; // sequences per launch (LDS-resident prefix)
 DecodePlan planDecode(int B, int nkvh, int group, int max_pages);
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
-                 const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *err, void *stream);
+                 const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
+                 int nkvh, int max_pages, int num_blocks, float scale, const DecodePlan &plan, float *records,
+                 int *err, void *stream);
 
+// Chunked prefill: the sequences of a varlen batch with >= 2 queries, as
+// (16-column query tile, kv head) units split over pages, then a combine kernel.
 struct PagedAttentionPlan {
-    int units;          // (query tile, kv head) work units
-    int units_padded;   // rounded up to a multiple of the XCD count
-    int max_splits;     // split-KV partitions per unit
+    int units;           // (query tile, kv head) work units (upper bound)
+    int units_padded;    // rounded up to a multiple of the XCD count
+    int max_splits;      // split-KV partitions per unit
     int pages_per_split;
-    size_t partial_bytes; // workspace for split partials
+    size_t partial_bytes; // workspace for split records
 };
-
-// Decode (cu_q == nullptr: one query per sequence, T == B) or varlen
-// (chunked prefill + decode). out is F32 when out_f32 else BF16.
-PagedAttentionPlan planPagedAttention(int B, int T, int nkvh, int group, int max_pages, bool varlen);
-
-void pagedAttention(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
-                    const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
-                    int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
-                    float *partial, int *counters, int *err, void *stream);
+PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages);
+void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
+                  int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
+                  float *records, int *err, void *stream);
 
 } // namespace llaisys::kernels

@@ -1,38 +1,22 @@
-// Paged flash-decoding / chunked-prefill attention for gfx950 (MI355X).
+// Chunked-prefill attention over paged KV for gfx950 (the multi-query
+// sequences of a mixed batch; single-query sequences go to the decode kernel).
 //
-// Work unit = (query tile, kv head). A query tile is 16 "columns"; column n is
-// the (query row, query head) pair number tile*16+n of its sequence, pairs
+// Work unit = (query tile, kv head). A query tile is 16 "columns"; column n
+// is the (query row, query head) pair number tile*16+n of its sequence, pairs
 // ordered query-major: pair = qi*G + g, G = nh/nkvh query heads per kv head.
-// A decode sequence (one query) is one tile whose first G columns are live.
-// Each unit's visible pages are cut into splits of `pages_per_split` pages;
-// one wave (one 64-lane workgroup) runs one (unit, split).
+// Query qi of a sequence with Lq new tokens sits at position ctx - Lq + qi
+// and sees keys at positions <= that (bottom-right causal alignment). A
+// unit's visible pages are cut into splits of `pages_per_split` pages; one
+// wave (one 64-lane workgroup) runs one (unit, split), streaming page pairs
+// through a two-stage register ring (loads never conditional) into the MFMA
+// step of mfma_common.hpp. A unit with one split writes its normalised
+// output; with more, each split writes a record (O, m, l) and the combine
+// kernel launched next merges them (the kernel boundary orders the records;
+// no fences, no waiting between waves).
 //
-// Per pair of pages (32 keys) a wave issues, all from registers:
-//   S^T[16 keys x 16 cols]  = K_page[16 x 128] . Q^T[128 x 16]
-//       4 x v_mfma_f32_16x16x32_bf16 per page; the K page format makes each
-//       A operand one coalesced 1 KiB load (64 lanes x 16 B);
-//   online softmax in base 2 on the 8 scores each lane holds (its column,
-//       keys 4*(lane/16)+i of both pages); max across the 4 lane groups by
-//       two lane shuffles; fp32 throughout;
-//   O^T[128 x 16 cols] += V^T[128 x 32 keys] . P^T[32 keys x 16 cols]
-//       8 dim blocks x 2 MFMAs: P is split as P = hi + lo (two bf16 parts,
-//       ~16 significant bits), so the product is fp32-accurate to ~1e-5 while
-//       V (bf16 data) is exact. The V page format makes each A operand half of
-//       one coalesced 1 KiB load.
-// The lane layouts line up so nothing crosses lanes except the max: the S^T
-// accumulator a lane holds is the P^T operand it needs, and O^T's column is the
-// lane's own column, so rescaling by exp2(m_old - m_new) is lane-local.
-//
-// Split-KV combine: a unit with one split writes the normalised output. With
-// more, each wave writes (O, m, l) for its split, then bumps the unit's
-// arrival counter; the wave that arrives last merges all splits with
-// log-sum-exp weights, writes the output and resets the counter to zero. No
-// wave ever waits on another, so no ordering between waves is assumed.
-//
-// Workgroup ids are split-major over units padded to a multiple of 8, so every
-// split of a unit runs on the same XCD (id % 8) and the combine reads its
-// partials from that XCD's L2.
-#include "launch.hpp"
+// Workgroup ids are split-major over units padded to a multiple of 8, so all
+// splits of a unit run on one XCD and share its L2 for the unit's K/V pages.
+#include "mfma_common.hpp"
 
 #include "../device/hip_check.hpp"
 
@@ -43,14 +27,10 @@ namespace llaisys::kernels {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+using namespace mfma;
 
-constexpr int kErrBadBlock = 1;
-constexpr int kErrTooLong = 2;
 constexpr int kXcds = 8;
-constexpr int kPartialFloats = 16 * kHeadDim + 32; // O for 16 columns, then (m, l) per column
+constexpr int kRecordFloats = 16 * (kHeadDim + 2); // O for 16 columns, then (m, l) per column
 
 struct Args {
     const uint16_t *q;
@@ -60,45 +40,66 @@ struct Args {
     const int32_t *table;
     const int32_t *ctx;
     const int32_t *cu_q;
-    float *partial;
-    int *counters;
+    float *records;
     int *err;
     int B, T, nh, nkvh, G, max_pages, num_blocks, pps, max_splits, units, units_padded;
     float scale_log2;
 };
 
-__device__ __forceinline__ bf16x8 asBf16(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+// Sequence and tile of unit-row `tile_global`: tiles are numbered sequence by
+// sequence, ceil(Lq*G/16) for each sequence with Lq >= 2 queries. Returns
+// false past the last tile. One wave.
+__device__ bool locateTile(const Args &a, int tile_global, int &b, int &tile) {
+    const int lane = threadIdx.x & 63;
+    int remaining = tile_global;
+    for (int base = 0; base < a.B; base += 64) {
+        const int bb = base + lane;
+        int nt = 0;
+        if (bb < a.B) {
+            const int lq = a.cu_q[bb + 1] - a.cu_q[bb];
+            nt = lq >= 2 ? (lq * a.G + 15) >> 4 : 0;
+        }
+        int incl = nt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(incl, off);
+            if (lane >= off) incl += y;
+        }
+        const int total = __shfl(incl, 63);
+        if (remaining < total) {
+            const unsigned long long hit = __ballot(incl > remaining);
+            const int first = __ffsll(hit) - 1;
+            b = base + first;
+            tile = remaining - (__shfl(incl, first) - __shfl(nt, first));
+            return true;
+        }
+        remaining -= total;
+    }
+    return false;
 }
 
-__device__ __forceinline__ float exp2Fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-struct PageRegs {
-    u32x4 ka[4], kb[4], va[4], vb[4];
+// Per-unit geometry shared by the attention and combine kernels.
+struct TileGeom {
+    int b, tile, q0, Lq, ctx, npages, nsplit;
 };
 
-// Keeps the halves of each 32-bit word whose key is valid.
-__device__ __forceinline__ uint32_t keepPair(bool lo, bool hi) {
-    return (lo ? 0x0000ffffu : 0u) | (hi ? 0xffff0000u : 0u);
-}
-
-template <bool OUT_F32>
-__device__ __forceinline__ void storeOut(void *out, size_t base, int blk, int grp, f32x4 v) {
-    const size_t idx = base + blk * 16 + grp * 4;
-    if constexpr (OUT_F32) {
-        *reinterpret_cast<f32x4 *>(static_cast<float *>(out) + idx) = v;
-    } else {
-        const __bf16 e0 = (__bf16)v[0], e1 = (__bf16)v[1], e2 = (__bf16)v[2], e3 = (__bf16)v[3];
-        const uint32_t w0 = uint32_t(__builtin_bit_cast(uint16_t, e0)) | (uint32_t(__builtin_bit_cast(uint16_t, e1)) << 16);
-        const uint32_t w1 = uint32_t(__builtin_bit_cast(uint16_t, e2)) | (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
-        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(out) + idx) = make_uint2(w0, w1);
+__device__ bool tileGeom(const Args &a, int tile_global, TileGeom &t, bool report) {
+    if (!locateTile(a, tile_global, t.b, t.tile)) return false;
+    t.q0 = a.cu_q[t.b];
+    t.Lq = a.cu_q[t.b + 1] - t.q0;
+    t.ctx = a.ctx[t.b];
+    if (t.q0 < 0 || t.q0 + t.Lq > a.T || t.ctx > a.max_pages * 16 || t.Lq > t.ctx) {
+        if (report && (threadIdx.x & 63) == 0) atomicOr(a.err, kErrTooLong);
+        return false;
     }
+    const int qi_max = min(t.Lq - 1, (t.tile * 16 + 15) / a.G);
+    const int kv_len = t.ctx - t.Lq + qi_max + 1; // keys some column of the tile sees
+    t.npages = (kv_len + 15) >> 4;
+    t.nsplit = (t.npages + a.pps - 1) / a.pps;
+    return true;
 }
 
-template <bool OUT_F32, bool VARLEN>
-__global__ void __launch_bounds__(64) pagedAttentionKernel(Args a) {
+template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillKernel(Args a) {
     const int lane = threadIdx.x;
     const int n = lane & 15;
     const int grp = lane >> 4;
@@ -106,241 +107,129 @@ __global__ void __launch_bounds__(64) pagedAttentionKernel(Args a) {
     const int unit = blockIdx.x - split * a.units_padded;
     if (unit >= a.units) return;
     const int h = unit % a.nkvh;
-    const int tile_global = unit / a.nkvh;
+    TileGeom t;
+    if (!tileGeom(a, unit / a.nkvh, t, split == 0)) return;
     const int G = a.G;
+    const int p0 = split * a.pps;
+    if (p0 >= t.npages) return;
+    const int p1 = min(t.npages, p0 + a.pps);
 
-    // ---- locate (sequence, tile)
-    int b, tile, q0, Lq;
-    if constexpr (!VARLEN) {
-        b = tile_global;
-        tile = 0;
-        q0 = b;
-        Lq = 1;
-    } else {
-        b = -1;
-        tile = 0;
-        int remaining = tile_global;
-        for (int base = 0; base < a.B; base += 64) {
-            const int bb = base + lane;
-            int nt = 0;
-            if (bb < a.B) nt = ((a.cu_q[bb + 1] - a.cu_q[bb]) * G + 15) >> 4;
-            int incl = nt;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int y = __shfl_up(incl, off);
-                if (lane >= off) incl += y;
-            }
-            const int total = __shfl(incl, 63);
-            if (remaining < total) {
-                const unsigned long long hit = __ballot(incl > remaining);
-                const int first = __ffsll(hit) - 1;
-                b = base + first;
-                tile = remaining - (__shfl(incl, first) - __shfl(nt, first));
-                break;
-            }
-            remaining -= total;
-        }
-        if (b < 0) return;
-        q0 = a.cu_q[b];
-        Lq = a.cu_q[b + 1] - q0;
-        if (q0 < 0 || Lq < 0 || q0 + Lq > a.T) { // query rows outside q/out: refuse the sequence
-            if (lane == 0) atomicOr(a.err, kErrTooLong);
-            return;
-        }
-    }
-    const int ctx = a.ctx[b];
-    if (ctx > a.max_pages * 16 || Lq > ctx || ctx <= 0) {
-        if (lane == 0) atomicOr(a.err, kErrTooLong);
-        return;
-    }
-
-    // ---- columns of this tile
-    const int pair = tile * 16 + n;
+    // Columns of this tile.
+    const int pair = t.tile * 16 + n;
     const int qi = pair / G;
     const int g = pair - qi * G;
-    const bool col_ok = qi < Lq;
-    const int pos = col_ok ? ctx - Lq + qi : -1; // last key this column sees
-    const int qi_max = min(Lq - 1, (tile * 16 + 15) / G);
-    const int kv_len = ctx - Lq + qi_max + 1;
-    const int npages = (kv_len + 15) >> 4;
-    const int nsplit = (npages + a.pps - 1) / a.pps;
-    const int p0 = split * a.pps;
-    if (p0 >= npages) return;
-    const int p1 = min(npages, p0 + a.pps);
+    const bool col_ok = qi < t.Lq;
+    const int pos = col_ok ? t.ctx - t.Lq + qi : -1;
 
     int bid = 0;
-    if (lane < p1 - p0) {
-        bid = a.table[size_t(b) * a.max_pages + p0 + lane];
-        if (bid < 0 || bid >= a.num_blocks) {
-            atomicOr(a.err, kErrBadBlock);
-            bid = 0;
-        }
-    }
+    if (lane < p1 - p0) bid = a.table[size_t(t.b) * a.max_pages + p0 + lane];
 
     u32x4 qop[4];
     {
-        const uint16_t *qrow = a.q + (size_t(q0 + (col_ok ? qi : 0)) * a.nh + h * G + g) * kHeadDim + grp * 8;
+        const uint16_t *qrow = a.q + (size_t(t.q0 + (col_ok ? qi : 0)) * a.nh + h * G + (col_ok ? g : 0)) * kHeadDim + grp * 8;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            qop[s] = col_ok ? *reinterpret_cast<const u32x4 *>(qrow + 32 * s) : u32x4{0, 0, 0, 0};
-        }
+        for (int s = 0; s < 4; ++s) qop[s] = *reinterpret_cast<const u32x4 *>(qrow + 32 * s);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qop[s] = col_ok ? qop[s] : u32x4{0, 0, 0, 0};
     }
 
     const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
     const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
-    auto load = [&](int pp, PageRegs &r) {
-        const int ba = __builtin_amdgcn_readlane(bid, pp - p0);
-        const int bb = (pp + 1 < p1) ? __builtin_amdgcn_readlane(bid, pp + 1 - p0) : ba;
-        const size_t oa = (size_t(ba) * a.nkvh + h) * 256;
-        const size_t ob = (size_t(bb) * a.nkvh + h) * 256;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            r.ka[s] = __builtin_nontemporal_load(kp + oa + s * 64);
-            r.kb[s] = __builtin_nontemporal_load(kp + ob + s * 64);
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            r.va[s] = __builtin_nontemporal_load(vp + oa + s * 64);
-            r.vb[s] = __builtin_nontemporal_load(vp + ob + s * 64);
-        }
+    bool bad_block = false;
+    const int last_pair = p0 + ((p1 - 1 - p0) & ~1);
+    // Loads for the pair starting at page pp (clamped: past the end it
+    // re-reads the last pair, so loads are never conditional).
+    auto issue = [&](PagePair &r, int pp) {
+        pp = min(pp, last_pair);
+        int ba = __builtin_amdgcn_readlane(bid, pp - p0);
+        int bb = (pp + 1 < p1) ? __builtin_amdgcn_readlane(bid, pp + 1 - p0) : ba;
+        const bool bad = unsigned(ba) >= unsigned(a.num_blocks) || unsigned(bb) >= unsigned(a.num_blocks);
+        bad_block |= bad;
+        ba = bad ? 0 : ba;
+        bb = bad ? 0 : bb;
+        loadPair(r, kp, vp, (size_t(ba) * a.nkvh + h) * 256, (size_t(bb) * a.nkvh + h) * 256);
     };
 
+    Acc acc;
+    acc.reset();
+    PagePair ra, rb;
+    issue(ra, p0);
+    issue(rb, p0 + 2);
+    for (int pp = p0; pp < p1; pp += 4) {
+        consumePair(acc, ra, qop, pp * 16, pos, t.ctx, pp + 1 < p1, grp, a.scale_log2);
+        issue(ra, pp + 4);
+        if (pp + 2 < p1) consumePair(acc, rb, qop, (pp + 2) * 16, pos, t.ctx, pp + 3 < p1, grp, a.scale_log2);
+        issue(rb, pp + 6);
+    }
+    if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
+    float lt = acc.l + __shfl_xor(acc.l, 16);
+    lt += __shfl_xor(lt, 32);
+    if (!col_ok) return;
+    if (t.nsplit == 1) {
+        const size_t row = (size_t(t.q0 + qi) * a.nh + h * G + g) * kHeadDim;
+        const float inv = 1.f / lt;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, acc.o[i] * inv);
+        return;
+    }
+    float *rec = a.records + (size_t(unit) * a.max_splits + split) * kRecordFloats;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4 *>(rec + (i * 16 + n) * 16 + grp * 4) = acc.o[i];
+    if (grp == 0) *reinterpret_cast<float2 *>(rec + 16 * kHeadDim + 2 * n) = make_float2(acc.m, lt);
+}
+
+// Merge the split records of each unit with more than one split.
+constexpr int kMergeBatch = 4;
+
+template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillCombineKernel(Args a) {
+    const int lane = threadIdx.x;
+    const int n = lane & 15;
+    const int grp = lane >> 4;
+    const int unit = blockIdx.x;
+    if (unit >= a.units) return;
+    const int h = unit % a.nkvh;
+    TileGeom t;
+    if (!tileGeom(a, unit / a.nkvh, t, false) || t.nsplit <= 1) return;
+    const int G = a.G;
+    const int pair = t.tile * 16 + n;
+    const int qi = pair / G;
+    const int g = pair - qi * G;
+    const bool col_ok = qi < t.Lq;
+    const float *recs = a.records + size_t(unit) * a.max_splits * kRecordFloats;
+    float M = -INFINITY, L = 0.f;
     f32x4 o[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY;
-    float lsum = 0.f;
-
-    // One page pair: scores, online softmax, P.V. Loads for it were issued earlier.
-    auto consume = [&](PageRegs &r, int pp) {
-        const bool hasB = pp + 1 < p1;
-        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < t.nsplit; k0 += kMergeBatch) {
+        float mr[kMergeBatch], lr[kMergeBatch];
+        f32x4 orr[kMergeBatch][8];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            sa = mfma(asBf16(r.ka[s]), asBf16(qop[s]), sa);
-            sb = mfma(asBf16(r.kb[s]), asBf16(qop[s]), sb);
-        }
-        const int kbase = pp * 16 + grp * 4;
-        float sv[8];
+        for (int s = 0; s < kMergeBatch; ++s) {
+            const float *rec = recs + size_t(min(k0 + s, t.nsplit - 1)) * kRecordFloats;
+            const float2 ml = *reinterpret_cast<const float2 *>(rec + 16 * kHeadDim + 2 * n);
+            mr[s] = k0 + s < t.nsplit ? ml.x : -INFINITY;
+            lr[s] = ml.y;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sv[i] = (kbase + i <= pos) ? sa[i] * a.scale_log2 : -INFINITY;
-            sv[4 + i] = (hasB && kbase + 16 + i <= pos) ? sb[i] * a.scale_log2 : -INFINITY;
-        }
-        float mloc = sv[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i) mloc = fmaxf(mloc, sv[i]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float m_new = fmaxf(m, mloc);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float alpha = exp2Fast(m - m_use);
-        float p[8];
-        float psum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            p[i] = exp2Fast(sv[i] - m_use);
-            psum += p[i];
-        }
-        lsum = lsum * alpha + psum;
-        m = m_new;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] *= alpha;
-
-        bf16x8 phi, plo;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const __bf16 hi = (__bf16)p[i];
-            phi[i] = hi;
-            plo[i] = (__bf16)(p[i] - (float)hi);
-        }
-
-        // Keys at or past ctx may hold stale bytes (even NaN patterns): zero
-        // their V so 0 * V stays 0. Only the last pair of a sequence has any.
-        if (pp * 16 + 32 > ctx || !hasB) {
-            const uint32_t ma01 = keepPair(kbase < ctx, kbase + 1 < ctx);
-            const uint32_t ma23 = keepPair(kbase + 2 < ctx, kbase + 3 < ctx);
-            const uint32_t mb01 = hasB ? keepPair(kbase + 16 < ctx, kbase + 17 < ctx) : 0u;
-            const uint32_t mb23 = hasB ? keepPair(kbase + 18 < ctx, kbase + 19 < ctx) : 0u;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                r.va[s] &= u32x4{ma01, ma23, ma01, ma23};
-                r.vb[s] &= u32x4{mb01, mb23, mb01, mb23};
-            }
+            for (int i = 0; i < 8; ++i) orr[s][i] = *reinterpret_cast<const f32x4 *>(rec + (i * 16 + n) * 16 + grp * 4);
         }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const bf16x8 v0 = asBf16(u32x4{r.va[s][0], r.va[s][1], r.vb[s][0], r.vb[s][1]});
-            const bf16x8 v1 = asBf16(u32x4{r.va[s][2], r.va[s][3], r.vb[s][2], r.vb[s][3]});
-            o[2 * s] = mfma(v0, phi, o[2 * s]);
-            o[2 * s] = mfma(v0, plo, o[2 * s]);
-            o[2 * s + 1] = mfma(v1, phi, o[2 * s + 1]);
-            o[2 * s + 1] = mfma(v1, plo, o[2 * s + 1]);
-        }
-    };
-
-    // Two register sets in a ring, loads always issued (past the end they
-    // re-read the last pair, an L2 hit) so the compiler can count the loads
-    // in flight and wait only for the set about to be consumed.
-    const int last_pair = p0 + ((p1 - 1 - p0) & ~1);
-    PageRegs ra, rb;
-    load(p0, ra);
-    load(min(p0 + 2, last_pair), rb);
-    for (int pp = p0; pp < p1; pp += 4) {
-        consume(ra, pp);
-        load(min(pp + 4, last_pair), ra);
-        if (pp + 2 < p1) consume(rb, pp + 2);
-        load(min(pp + 6, last_pair), rb);
-    }
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-
-    const size_t out_base = (size_t(q0 + (col_ok ? qi : 0)) * a.nh + h * G + g) * kHeadDim;
-    if (nsplit == 1) {
-        if (col_ok) {
-            const float inv = 1.f / lsum;
+        for (int s = 0; s < kMergeBatch; ++s) {
+            // A split can lie wholly past a column's causal limit: m = -inf, weight 0.
+            if (mr[s] == -INFINITY) continue;
+            const float Mn = fmaxf(M, mr[s]);
+            const float sa = exp2Fast(M - Mn);
+            const float sb = exp2Fast(mr[s] - Mn);
+            L = L * sa + lr[s] * sb;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, out_base, i, grp, o[i] * inv);
-        }
-        return;
-    }
-
-    float *part = a.partial + (size_t(unit) * a.max_splits) * kPartialFloats;
-    if (col_ok) {
-        float *mine = part + size_t(split) * kPartialFloats;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4 *>(mine + n * kHeadDim + i * 16 + grp * 4) = o[i];
-        if (grp == 0) {
-            mine[16 * kHeadDim + 2 * n] = m;
-            mine[16 * kHeadDim + 2 * n + 1] = lsum;
+            for (int i = 0; i < 8; ++i) o[i] = o[i] * sa + orr[s][i] * sb;
+            M = Mn;
         }
     }
-    __threadfence();
-    int prev = 0;
-    if (lane == 0) prev = atomicAdd(a.counters + unit, 1);
-    prev = __shfl(prev, 0);
-    if (prev != nsplit - 1) return;
-    __threadfence();
-    if (col_ok) {
-        float M = -INFINITY;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part[size_t(s) * kPartialFloats + 16 * kHeadDim + 2 * n]);
-        float L = 0.f;
-        f32x4 acc[8];
+    if (!col_ok) return;
+    const float inv = 1.f / L;
+    const size_t row = (size_t(t.q0 + qi) * a.nh + h * G + g) * kHeadDim;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < nsplit; ++s) {
-            const float *ps = part + size_t(s) * kPartialFloats;
-            const float w = exp2Fast(ps[16 * kHeadDim + 2 * n] - M);
-            L += w * ps[16 * kHeadDim + 2 * n + 1];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                acc[i] += w * *reinterpret_cast<const f32x4 *>(ps + n * kHeadDim + i * 16 + grp * 4);
-        }
-        const float inv = 1.f / L;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, out_base, i, grp, acc[i] * inv);
-    }
-    if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, o[i] * inv);
 }
 
 int envInt(const char *name, int fallback) {
@@ -351,24 +240,24 @@ int envInt(const char *name, int fallback) {
 
 } // namespace
 
-PagedAttentionPlan planPagedAttention(int B, int T, int nkvh, int group, int max_pages, bool varlen) {
+PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages) {
     PagedAttentionPlan p{};
-    const int tiles = varlen ? (T * group + 15) / 16 + B : B;
+    const int tiles = (T * group + 15) / 16 + B;
     p.units = tiles * nkvh;
     p.units_padded = (p.units + kXcds - 1) / kXcds * kXcds;
     // Pages per split: even (pairs of pages), at most 64 (one block id per lane).
-    int pps = envInt("LLAISYS_PAGES_PER_SPLIT", varlen ? 32 : 16);
+    int pps = envInt("LLAISYS_PAGES_PER_SPLIT", 64);
     pps = std::max(2, std::min(64, pps & ~1));
     p.pages_per_split = pps;
     p.max_splits = std::max(1, (max_pages + pps - 1) / pps);
-    p.partial_bytes = size_t(p.units_padded) * p.max_splits * kPartialFloats * sizeof(float);
+    p.partial_bytes = size_t(p.units_padded) * p.max_splits * kRecordFloats * sizeof(float);
     return p;
 }
 
-void pagedAttention(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
-                    const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
-                    int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
-                    float *partial, int *counters, int *err, void *stream) {
+void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
+                  int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
+                  float *records, int *err, void *stream) {
     if (B == 0 || T == 0) return;
     Args a;
     a.q = q;
@@ -378,8 +267,7 @@ void pagedAttention(void *out, bool out_f32, const uint16_t *q, const uint16_t *
     a.table = block_table;
     a.ctx = ctx_len;
     a.cu_q = cu_q;
-    a.partial = partial;
-    a.counters = counters;
+    a.records = records;
     a.err = err;
     a.B = B;
     a.T = T;
@@ -393,19 +281,14 @@ void pagedAttention(void *out, bool out_f32, const uint16_t *q, const uint16_t *
     a.units = plan.units;
     a.units_padded = plan.units_padded;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const dim3 grid(plan.units_padded * plan.max_splits);
+    const dim3 grid(plan.units_padded * plan.max_splits), block(64);
     auto s = static_cast<hipStream_t>(stream);
-    const bool varlen = cu_q != nullptr;
     if (out_f32) {
-        if (varlen)
-            hipLaunchKernelGGL((pagedAttentionKernel<true, true>), grid, dim3(64), 0, s, a);
-        else
-            hipLaunchKernelGGL((pagedAttentionKernel<true, false>), grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((prefillKernel<true>), grid, block, 0, s, a);
+        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<true>), dim3(plan.units), block, 0, s, a);
     } else {
-        if (varlen)
-            hipLaunchKernelGGL((pagedAttentionKernel<false, true>), grid, dim3(64), 0, s, a);
-        else
-            hipLaunchKernelGGL((pagedAttentionKernel<false, false>), grid, dim3(64), 0, s, a);
+        hipLaunchKernelGGL((prefillKernel<false>), grid, block, 0, s, a);
+        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<false>), dim3(plan.units), block, 0, s, a);
     }
     HIP_CHECK(hipGetLastError());
 }

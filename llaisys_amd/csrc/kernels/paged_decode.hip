@@ -47,39 +47,55 @@ struct DecodeArgs {
     const uint16_t *v_pool;
     const int32_t *table;
     const int32_t *ctx;
+    const int32_t *cu_q; // null: query row b is sequence b; else row cu_q[b], and only
+                         // sequences with exactly one query are handled here
     float *records;
     int *err;
-    int B, nh, nkvh, G, max_pages, num_blocks, W;
+    int B, T, nh, nkvh, G, max_pages, num_blocks, W;
     float scale_log2;
 };
 
-// Exclusive prefix (over b) of nkvh * npairs(b) into S[0..B], lengths into C.
-// Invalid lengths (< 1 or beyond the block table) count as empty and raise
-// kErrTooLong when `report`. Returns the total pair count N. One wave; the
-// caller synchronises before reading S/C from other waves.
-__device__ int scanPairs(const DecodeArgs &a, int *S, int *C, bool report) {
+// Exclusive prefix (over b) of nkvh * npairs(b) into S[0..B], lengths into C,
+// query rows into Q. Invalid lengths (< 1 or beyond the block table) count as
+// empty and raise kErrTooLong when `report`; so do sequences with more than one
+// query when cu_q is given (they are the prefill kernel's), without an error.
+// Returns the total pair count N. One wave; the caller synchronises before
+// reading S/C/Q from other waves.
+__device__ int scanPairs(const DecodeArgs &a, int *S, int *C, int *Q, bool report) {
     const int lane = threadIdx.x & 63;
     int carry = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int bb = base + lane;
-        int c = 0;
+        int c = 0, row = bb;
         if (bb < a.B) {
             c = a.ctx[bb];
-            if (c < 1 || c > a.max_pages * 16) {
-                if (report) atomicOr(a.err, kErrTooLong);
-                c = 0;
+            bool mine = true;
+            if (a.cu_q) {
+                row = a.cu_q[bb];
+                const int lq = a.cu_q[bb + 1] - row;
+                mine = lq == 1;
+                if (mine && (row < 0 || row >= a.T)) {
+                    if (report) atomicOr(a.err, kErrTooLong);
+                    mine = false;
+                }
             }
+            if (mine && (c < 1 || c > a.max_pages * 16)) {
+                if (report) atomicOr(a.err, kErrTooLong);
+                mine = false;
+            }
+            if (!mine) c = 0;
         }
-        const int mine = ((((c + 15) >> 4) + 1) >> 1) * a.nkvh;
-        int incl = mine;
+        const int mine_pairs = ((((c + 15) >> 4) + 1) >> 1) * a.nkvh;
+        int incl = mine_pairs;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const int y = __shfl_up(incl, off);
             if (lane >= off) incl += y;
         }
         if (bb < a.B) {
-            S[bb] = carry + incl - mine;
+            S[bb] = carry + incl - mine_pairs;
             C[bb] = c;
+            Q[bb] = row;
         }
         carry += __shfl(incl, 63);
     }
@@ -114,13 +130,14 @@ __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
     extern __shared__ int lds[];
     int *S = lds;
     int *C = lds + a.B + 1;
+    int *Q = C + a.B;
     const int lane = threadIdx.x;
     const int n = lane & 15;
     const int grp = lane >> 4;
     const int w = blockIdx.x;
     const int G = a.G;
 
-    const int N = scanPairs(a, S, C, w == 0);
+    const int N = scanPairs(a, S, C, Q, w == 0);
     __syncthreads();
     const int s = waveStart(w, N, a.W);
     const int e = waveStart(w + 1, N, a.W);
@@ -177,7 +194,7 @@ __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
         const int b = __builtin_amdgcn_readlane(lb, kk);
         const int h = __builtin_amdgcn_readlane(lh, kk);
         loadPair(ring.pp[st], kp, vp, (size_t(bA) * a.nkvh + h) * 256, (size_t(bB) * a.nkvh + h) * 256);
-        const uint16_t *qrow = a.q + (size_t(b) * a.nh + h * G + ncol) * kHeadDim + grp * 8;
+        const uint16_t *qrow = a.q + (size_t(Q[b]) * a.nh + h * G + ncol) * kHeadDim + grp * 8;
 #pragma unroll
         for (int t = 0; t < 4; ++t) ring.q[st][t] = *reinterpret_cast<const u32x4 *>(qrow + 32 * t);
     };
@@ -195,7 +212,7 @@ __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
         if (first >= s && first + npr <= e) {
             if (n < G) {
                 const float inv = 1.f / lt;
-                const size_t row = (size_t(cur_b) * a.nh + cur_h * G + n) * kHeadDim;
+                const size_t row = (size_t(Q[cur_b]) * a.nh + cur_h * G + n) * kHeadDim;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, acc.o[i] * inv);
             }
@@ -252,6 +269,7 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
     extern __shared__ int lds[];
     int *S = lds;
     int *C = lds + a.B + 1;
+    int *Q = C + a.B;
     __shared__ float part_o[kCombineWaves - 1][8][64][4];
     __shared__ float part_ml[kCombineWaves - 1][2][64];
     const int wave = threadIdx.x >> 6;
@@ -259,7 +277,7 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
     const int n = lane & 15;
     const int grp = lane >> 4;
     const int G = a.G;
-    if (wave == 0) scanPairs(a, S, C, false);
+    if (wave == 0) scanPairs(a, S, C, Q, false);
     __syncthreads();
     const int N = S[a.B];
     const int u = blockIdx.x;
@@ -340,7 +358,7 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
         M = Mn;
     }
     const float inv = 1.f / L;
-    const size_t row = (size_t(b) * a.nh + h * G + n) * kHeadDim;
+    const size_t row = (size_t(Q[b]) * a.nh + h * G + n) * kHeadDim;
 #pragma unroll
     for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, o[i] * inv);
 }
@@ -369,13 +387,14 @@ DecodePlan planDecode(int B, int nkvh, int group, int max_pages) {
     const int fill = std::max(1, envInt("LLAISYS_DECODE_WAVES", 2 * computeUnits()));
     p.waves = int(std::max<long long>(fill, (max_pairs + kPairsPerWave - 1) / kPairsPerWave));
     p.record_bytes = size_t(2) * p.waves * group * (kHeadDim + 2) * sizeof(float);
-    p.lds_bytes = size_t(2 * B + 1) * sizeof(int);
+    p.lds_bytes = size_t(3 * B + 1) * sizeof(int);
     p.stages = envInt("LLAISYS_DECODE_STAGES", 2) >= 3 ? 3 : 2;
     return p;
 }
 
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
-                 const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                 const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
+                 int nkvh, int max_pages,
                  int num_blocks, float scale, const DecodePlan &plan, float *records, int *err, void *stream) {
     if (B == 0) return;
     DecodeArgs a;
@@ -385,9 +404,11 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
     a.v_pool = v_pool;
     a.table = block_table;
     a.ctx = ctx_len;
+    a.cu_q = cu_q;
     a.records = records;
     a.err = err;
     a.B = B;
+    a.T = T;
     a.nh = nh;
     a.nkvh = nkvh;
     a.G = nh / nkvh;

@@ -209,6 +209,13 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
     LLAISYS_CHECK(max_pages > 0, op << ": block_table has no pages");
     auto &rt = core::context().runtime();
     const int G = int(nh / nkvh);
+    const bool f32 = out->dtype() == LLAISYS_DTYPE_F32;
+    const auto *qp = reinterpret_cast<const uint16_t *>(q->data());
+    const auto *kp = reinterpret_cast<const uint16_t *>(k_pool->data());
+    const auto *vp = reinterpret_cast<const uint16_t *>(v_pool->data());
+    const auto *tab = reinterpret_cast<const int32_t *>(block_table->data());
+    const auto *ctx = reinterpret_cast<const int32_t *>(ctx_len->data());
+    const int nb = int(k_pool->shape()[0]);
     if (!cu_q) {
         // Decode: sequences are independent, so large batches run in chunks
         // whose length prefix fits the kernel's LDS.
@@ -216,28 +223,25 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
             const int Bc = int(std::min<size_t>(K::kDecodeMaxBatch, B - b0));
             auto plan = K::planDecode(Bc, int(nkvh), G, max_pages);
             float *records = static_cast<float *>(rt.scratch(plan.record_bytes));
-            const size_t esz = out->dtype() == LLAISYS_DTYPE_F32 ? 4 : 2;
-            K::pagedDecode(static_cast<std::byte *>(out->data()) + b0 * nh * K::kHeadDim * esz,
-                           out->dtype() == LLAISYS_DTYPE_F32,
-                           reinterpret_cast<const uint16_t *>(q->data()) + b0 * nh * K::kHeadDim,
-                           reinterpret_cast<const uint16_t *>(k_pool->data()),
-                           reinterpret_cast<const uint16_t *>(v_pool->data()),
-                           reinterpret_cast<const int32_t *>(block_table->data()) + b0 * size_t(max_pages),
-                           reinterpret_cast<const int32_t *>(ctx_len->data()) + b0, Bc, int(nh), int(nkvh),
-                           max_pages, int(k_pool->shape()[0]), scale, plan, records, rt.errorWord(), rt.stream());
+            const size_t esz = f32 ? 4 : 2;
+            K::pagedDecode(static_cast<std::byte *>(out->data()) + b0 * nh * K::kHeadDim * esz, f32,
+                           qp + b0 * nh * K::kHeadDim, kp, vp, tab + b0 * size_t(max_pages), ctx + b0, nullptr, Bc,
+                           Bc, int(nh), int(nkvh), max_pages, nb, scale, plan, records, rt.errorWord(), rt.stream());
         }
         return;
     }
-    auto plan = K::planPagedAttention(int(B), int(T), int(nkvh), G, max_pages, true);
-    float *partial = plan.max_splits > 1 ? static_cast<float *>(rt.scratch(plan.partial_bytes)) : nullptr;
-    int *counters = rt.counters(size_t(plan.units_padded));
-    K::pagedAttention(out->data(), out->dtype() == LLAISYS_DTYPE_F32, reinterpret_cast<const uint16_t *>(q->data()),
-                      reinterpret_cast<const uint16_t *>(k_pool->data()),
-                      reinterpret_cast<const uint16_t *>(v_pool->data()),
-                      reinterpret_cast<const int32_t *>(block_table->data()),
-                      reinterpret_cast<const int32_t *>(ctx_len->data()),
-                      reinterpret_cast<const int32_t *>(cu_q->data()), int(B), int(T), int(nh), int(nkvh), max_pages,
-                      int(k_pool->shape()[0]), scale, plan, partial, counters, rt.errorWord(), rt.stream());
+    // Varlen: single-query sequences through the decode kernel, the rest
+    // through the prefill kernel; both read the same cu_q and skip the other's.
+    LLAISYS_CHECK(B <= size_t(K::kDecodeMaxBatch),
+                  op << ": at most " << K::kDecodeMaxBatch << " sequences per varlen call");
+    const auto *cu = reinterpret_cast<const int32_t *>(cu_q->data());
+    auto dplan = K::planDecode(int(B), int(nkvh), G, max_pages);
+    auto pplan = K::planPrefill(int(B), int(T), int(nkvh), G, max_pages);
+    float *records = static_cast<float *>(rt.scratch(std::max(dplan.record_bytes, pplan.partial_bytes)));
+    K::pagedDecode(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
+                   scale, dplan, records, rt.errorWord(), rt.stream());
+    K::pagedPrefill(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
+                    scale, pplan, records, rt.errorWord(), rt.stream());
 }
 
 } // namespace llaisys::ops
