@@ -45,6 +45,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--summarize", nargs=6, metavar=("STATS", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE", "TAG"),
+                   help="summarise rocprofv3 output directories into profiles/TAG.md and profiles/TAG_traffic.json")
+    p.add_argument("--profiled-args", default="--no-cpu --steps 200", help="bench arguments of the kernel-trace run")
+    p.add_argument("--pmc-args", default="--no-cpu --steps 20 --warmup 5", help="bench arguments of the PMC runs")
     return p.parse_args()
 
 
@@ -220,7 +224,7 @@ def run_decode(args):
         "ms_per_step": round(wall_ms, 5),
         "kernel_ms": round(kern_ms, 5),
         "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "decode_tokens_per_s": round(B / (kern_ms * 1e-3), 1),
+        "decode_tokens_per_s_one_attention_layer": round(B / (kern_ms * 1e-3), 1),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -230,8 +234,9 @@ def run_decode(args):
             "workload": "batched paged decode attention (BASELINE config 3)",
             "batch": B, "ctx_range": [512, 8192], "ctx_total": int(ctx.sum()), "block_size": 16,
             "q_heads": 12, "kv_heads": 2, "head_dim": 128, "accumulate": "fp32",
-            "split": "split-KV, in-kernel log-sum-exp combine",
-            "pages_per_split": int(os.environ.get("LLAISYS_PAGES_PER_SPLIT", "16")),
+            "split": "stream-K over page pairs, log-sum-exp combine kernel",
+            "waves": int(os.environ.get("LLAISYS_DECODE_WAVES",
+                                        2 * torch.cuda.get_device_properties(0).multi_processor_count)),
         },
         "roofline": {
             "bound": "hbm",
@@ -239,7 +244,7 @@ def run_decode(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles("paged_decode_attention"),
+            "traffic": traffic_from_profiles("paged_decode_attention_b64"),
             "algorithmic_bytes_per_launch": nbytes,
         },
     }
@@ -347,6 +352,78 @@ def run_copy(args):
             "unit": "GB/s", "bytes_per_launch_read": n, "bytes_per_launch_written": n, "kernel_ms": kern_ms}
 
 
+def summarize(args):
+    """Markdown + JSON summary of rocprofv3 output directories.
+
+    --summarize STATS_DIR FETCH_DIR WRITE_DIR COPY_FETCH_DIR COPY_WRITE_DIR TAG
+    STATS_DIR holds a --kernel-trace --stats run; the PMC dirs hold one-counter
+    runs of the same workload (FETCH_SIZE, WRITE_SIZE, KiB per dispatch) and of
+    --workload copy, whose known byte counts give the scale of each counter.
+    """
+    import csv
+    import glob
+    from collections import defaultdict
+
+    stats_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir, tag = args.summarize
+
+    def csvs(d, suffix):
+        return glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)
+
+    def counter_means(d):
+        acc = defaultdict(list)
+        for f in csvs(d, "counter_collection.csv"):
+            for r in csv.DictReader(open(f)):
+                acc[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+    copy_bytes = 512 << 20
+    fetch_scale = copy_bytes / 1024 / max(v for k, v in counter_means(cfetch_dir).items() if "copy" in k.lower())
+    write_scale = copy_bytes / 1024 / max(v for k, v in counter_means(cwrite_dir).items() if "copy" in k.lower())
+    fetch, write = counter_means(fetch_dir), counter_means(write_dir)
+    def short(name):
+        name = name.replace("(anonymous namespace)::", "").replace("void ", "")
+        return name.split("(")[0]
+
+    stats = []
+    for f in csvs(stats_dir, "kernel_stats.csv"):
+        stats += [r for r in csv.DictReader(open(f)) if "llaisys" in r["Name"]]
+    lines = [f"# {tag}: rocprofv3 summary", "", "Commands (from the repo root, on the MI355X box):", "", "```"]
+    lines += [f"rocprofv3 --kernel-trace --stats --output-format csv -d {stats_dir} -o run -- python3 bench.py {args.profiled_args}"]
+    for c, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        lines += [f"rocprofv3 --pmc {c} --output-format csv -d {d} -o run -- python3 bench.py {args.pmc_args}"]
+    for c, d in (("FETCH_SIZE", cfetch_dir), ("WRITE_SIZE", cwrite_dir)):
+        lines += [f"rocprofv3 --pmc {c} --output-format csv -d {d} -o run -- python3 bench.py --workload copy --steps 5 --warmup 2"]
+    lines += [f"python3 bench.py --summarize {' '.join(args.summarize)} --profiled-args '{args.profiled_args}' "
+              f"--pmc-args '{args.pmc_args}'", "```", ""]
+    lines += ["## Kernel time (kernel trace)", "", "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    total_us = 0.0
+    for r in stats:
+        name = short(r["Name"])
+        avg = float(r["AverageNs"]) / 1e3
+        total_us += avg
+        lines.append(f"| `{name}` | {r['Calls']} | {avg:.2f} | {float(r['MinNs'])/1e3:.2f} | {float(r['MaxNs'])/1e3:.2f} |")
+    lines += ["", f"Sum of the averages (one op call): {total_us:.2f} us", ""]
+    lines += ["## HBM traffic per dispatch (PMC, scaled)", "",
+              f"Counter scale from a plain {copy_bytes >> 20} MiB device copy: FETCH_SIZE x{fetch_scale:.3f}, "
+              f"WRITE_SIZE x{write_scale:.3f} (copy reads and writes exactly {copy_bytes} bytes).", "",
+              "| kernel | FETCH raw KiB | WRITE raw KiB | read MB | written MB |", "|---|---|---|---|---|"]
+    total_bytes = 0.0
+    for k in sorted(set(fetch) | set(write)):
+        if "llaisys" not in k:
+            continue
+        fr, wr = fetch.get(k, 0.0), write.get(k, 0.0)
+        rb, wb = fr * 1024 * fetch_scale, wr * 1024 * write_scale
+        total_bytes += rb + wb
+        lines.append(f"| `{short(k)}` | {fr:.1f} | {wr:.1f} | {rb/1e6:.2f} | {wb/1e6:.2f} |")
+    lines += ["", f"HBM bytes per op call (all llaisys kernels): {total_bytes/1e6:.2f} MB", ""]
+    print("\n".join(lines))
+    out = {"tag": tag, "hbm_bytes_per_launch": int(total_bytes), "op_time_us_rocprof": round(total_us, 3),
+           "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}
+    (ROOT / "profiles").mkdir(exist_ok=True)
+    (ROOT / "profiles" / f"{tag}_traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
+
+
 def traffic_from_profiles(kernel_tag):
     """HBM bytes per launch measured by rocprofv3 PMC, if a summary is committed under profiles/."""
     f = ROOT / "profiles" / f"{kernel_tag}_traffic.json"
@@ -360,6 +437,9 @@ def traffic_from_profiles(kernel_tag):
 
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the KV-cache path "
               "is built and measured on a single MI355X", file=sys.stderr)

@@ -34,7 +34,6 @@ Runtime::~Runtime() {
         api_->set_device(id_);
         if (type_ != LLAISYS_DEVICE_CPU) api_->device_synchronize();
         if (scratch_) api_->free_device(scratch_);
-        if (counters_) api_->free_device(counters_);
         if (error_word_) api_->free_device(error_word_);
         api_->destroy_stream(stream_);
     } catch (...) {
@@ -63,20 +62,6 @@ void *Runtime::scratch(size_t bytes) {
         scratch_bytes_ = grown;
     }
     return scratch_;
-}
-
-int *Runtime::counters(size_t n) {
-    LLAISYS_CHECK(type_ == LLAISYS_DEVICE_AMD, "device workspace exists on AMD runtimes only");
-    if (n > counters_n_) {
-        api_->device_synchronize();
-        if (counters_) api_->free_device(counters_);
-        size_t grown = std::max(n, counters_n_ * 2);
-        counters_ = static_cast<int *>(api_->malloc_device(grown * sizeof(int)));
-        if (hipMemset(counters_, 0, grown * sizeof(int)) != hipSuccess) LLAISYS_RAISE("hipMemset failed");
-        api_->device_synchronize();
-        counters_n_ = grown;
-    }
-    return counters_;
 }
 
 int *Runtime::errorWord() {

@@ -12,7 +12,7 @@
 // stored back into the map (context.cpp:55-62 mutates a copy).
 //
 // The AMD runtime also owns the device workspace the attention kernels use:
-// split-KV partial results, self-resetting arrival counters and an error word.
+// split-KV partial results and an error word.
 #pragma once
 
 #include "llaisys/runtime.h"
@@ -69,8 +69,6 @@ public:
 
     // Device workspace (AMD only). Grow-only; growing waits for the device.
     void *scratch(size_t bytes);
-    // `n` int32 counters, all zero between calls (kernels reset what they use).
-    int *counters(size_t n);
     // One int32 of kernel-side error bits.
     int *errorWord();
     int takeErrorFlags();
@@ -85,8 +83,6 @@ private:
     llaisysStream_t override_stream_ = nullptr;
     void *scratch_ = nullptr;
     size_t scratch_bytes_ = 0;
-    int *counters_ = nullptr;
-    size_t counters_n_ = 0;
     int *error_word_ = nullptr;
 };
 
