@@ -10,8 +10,10 @@
 //       the 32 keys are 2 pages; key slot 8*grp+e is page A key 4*grp+e
 //       (e<4) or page B key 4*grp+e-4, which is exactly what the S^T
 //       accumulators of the two pages hold and what one 16 B load of the V
-//       page format holds per 16-dim block pair. P = hi + lo (two bf16), so
-//       the product is accurate to ~2^-17 relative, V being exact bf16.
+//       page format holds per 16-dim block pair. For fp32 output P = hi + lo
+//       (two bf16, two MFMAs), so the product is accurate to ~2^-17 relative,
+//       V being exact bf16; for bf16 output P is rounded once to bf16 (its
+//       2^-9 error is below the output's own rounding), one MFMA.
 // Nothing crosses lanes except the running max (2 shuffles).
 #pragma once
 
@@ -76,6 +78,8 @@ struct Acc {
 // Consume one page pair. first_key = key position of page A's token 0;
 // pos = last key this lane's column may see (-1: none); ctx = keys in cache
 // (keys >= ctx are stale bytes and get zeroed V); hasB = page B exists.
+// SPLIT_P: P enters P.V as hi + lo bf16 parts (fp32-accurate) or as one bf16.
+template <bool SPLIT_P>
 __device__ __forceinline__ void consumePair(Acc &acc, PagePair &r, const u32x4 (&qop)[4], int first_key, int pos,
                                            int ctx, bool hasB, int grp, float scale_log2) {
     f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
@@ -116,7 +120,7 @@ __device__ __forceinline__ void consumePair(Acc &acc, PagePair &r, const u32x4 (
     for (int i = 0; i < 8; ++i) {
         const __bf16 hi = (__bf16)p[i];
         phi[i] = hi;
-        plo[i] = (__bf16)(p[i] - (float)hi);
+        if constexpr (SPLIT_P) plo[i] = (__bf16)(p[i] - (float)hi);
     }
 
     // Keys at or past ctx may hold stale bytes (even NaN patterns): zero their
@@ -137,9 +141,11 @@ __device__ __forceinline__ void consumePair(Acc &acc, PagePair &r, const u32x4 (
         const bf16x8 v0 = asBf16(u32x4{r.va[s][0], r.va[s][1], r.vb[s][0], r.vb[s][1]});
         const bf16x8 v1 = asBf16(u32x4{r.va[s][2], r.va[s][3], r.vb[s][2], r.vb[s][3]});
         acc.o[2 * s] = mfma(v0, phi, acc.o[2 * s]);
-        acc.o[2 * s] = mfma(v0, plo, acc.o[2 * s]);
         acc.o[2 * s + 1] = mfma(v1, phi, acc.o[2 * s + 1]);
-        acc.o[2 * s + 1] = mfma(v1, plo, acc.o[2 * s + 1]);
+        if constexpr (SPLIT_P) {
+            acc.o[2 * s] = mfma(v0, plo, acc.o[2 * s]);
+            acc.o[2 * s + 1] = mfma(v1, plo, acc.o[2 * s + 1]);
+        }
     }
 }
 

@@ -1,9 +1,12 @@
 // Chunked-prefill attention over paged KV for gfx950 (the multi-query
 // sequences of a mixed batch; single-query sequences go to the decode kernel).
 //
-// Work unit = (query tile, kv head). A query tile is 16 "columns"; column n
-// is the (query row, query head) pair number tile*16+n of its sequence, pairs
-// ordered query-major: pair = qi*G + g, G = nh/nkvh query heads per kv head.
+// Work unit = (query group, kv head). A query tile is 16 "columns"; column n
+// of tile t is the (query row, query head) pair number t*16+n of its
+// sequence, pairs ordered query-major: pair = qi*G + g, G = nh/nkvh query
+// heads per kv head. A group is kTiles adjacent tiles: one wave carries all of
+// them, so each K/V page pair it loads feeds kTiles x 24 MFMAs (the kernel is
+// otherwise bound by re-streaming the same pages from L2 per tile).
 // Query qi of a sequence with Lq new tokens sits at position ctx - Lq + qi
 // and sees keys at positions <= that (bottom-right causal alignment). A
 // unit's visible pages are cut into splits of `pages_per_split` pages; one
@@ -30,7 +33,8 @@ namespace {
 using namespace mfma;
 
 constexpr int kXcds = 8;
-constexpr int kRecordFloats = 16 * (kHeadDim + 2); // O for 16 columns, then (m, l) per column
+constexpr int kTiles = 2;                                    // query tiles per wave
+constexpr int kRecordFloats = kTiles * 16 * (kHeadDim + 2); // O for the group's columns, then (m, l)
 
 struct Args {
     const uint16_t *q;
@@ -46,18 +50,18 @@ struct Args {
     float scale_log2;
 };
 
-// Sequence and tile of unit-row `tile_global`: tiles are numbered sequence by
-// sequence, ceil(Lq*G/16) for each sequence with Lq >= 2 queries. Returns
-// false past the last tile. One wave.
-__device__ bool locateTile(const Args &a, int tile_global, int &b, int &tile) {
+// Sequence and group of unit-row `group_global`: groups are numbered sequence
+// by sequence, ceil(ceil(Lq*G/16)/kTiles) for each sequence with Lq >= 2
+// queries. Returns false past the last group. One wave.
+__device__ bool locateGroup(const Args &a, int group_global, int &b, int &group) {
     const int lane = threadIdx.x & 63;
-    int remaining = tile_global;
+    int remaining = group_global;
     for (int base = 0; base < a.B; base += 64) {
         const int bb = base + lane;
         int nt = 0;
         if (bb < a.B) {
             const int lq = a.cu_q[bb + 1] - a.cu_q[bb];
-            nt = lq >= 2 ? (lq * a.G + 15) >> 4 : 0;
+            nt = lq >= 2 ? (((lq * a.G + 15) >> 4) + kTiles - 1) / kTiles : 0;
         }
         int incl = nt;
 #pragma unroll
@@ -70,7 +74,7 @@ __device__ bool locateTile(const Args &a, int tile_global, int &b, int &tile) {
             const unsigned long long hit = __ballot(incl > remaining);
             const int first = __ffsll(hit) - 1;
             b = base + first;
-            tile = remaining - (__shfl(incl, first) - __shfl(nt, first));
+            group = remaining - (__shfl(incl, first) - __shfl(nt, first));
             return true;
         }
         remaining -= total;
@@ -80,11 +84,11 @@ __device__ bool locateTile(const Args &a, int tile_global, int &b, int &tile) {
 
 // Per-unit geometry shared by the attention and combine kernels.
 struct TileGeom {
-    int b, tile, q0, Lq, ctx, npages, nsplit;
+    int b, group, q0, Lq, ctx, npages, nsplit;
 };
 
-__device__ bool tileGeom(const Args &a, int tile_global, TileGeom &t, bool report) {
-    if (!locateTile(a, tile_global, t.b, t.tile)) return false;
+__device__ bool tileGeom(const Args &a, int group_global, TileGeom &t, bool report) {
+    if (!locateGroup(a, group_global, t.b, t.group)) return false;
     t.q0 = a.cu_q[t.b];
     t.Lq = a.cu_q[t.b + 1] - t.q0;
     t.ctx = a.ctx[t.b];
@@ -92,8 +96,8 @@ __device__ bool tileGeom(const Args &a, int tile_global, TileGeom &t, bool repor
         if (report && (threadIdx.x & 63) == 0) atomicOr(a.err, kErrTooLong);
         return false;
     }
-    const int qi_max = min(t.Lq - 1, (t.tile * 16 + 15) / a.G);
-    const int kv_len = t.ctx - t.Lq + qi_max + 1; // keys some column of the tile sees
+    const int qi_max = min(t.Lq - 1, ((t.group + 1) * kTiles * 16 - 1) / a.G);
+    const int kv_len = t.ctx - t.Lq + qi_max + 1; // keys some column of the group sees
     t.npages = (kv_len + 15) >> 4;
     t.nsplit = (t.npages + a.pps - 1) / a.pps;
     return true;
@@ -114,23 +118,30 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillKernel(Args
     if (p0 >= t.npages) return;
     const int p1 = min(t.npages, p0 + a.pps);
 
-    // Columns of this tile.
-    const int pair = t.tile * 16 + n;
-    const int qi = pair / G;
-    const int g = pair - qi * G;
-    const bool col_ok = qi < t.Lq;
-    const int pos = col_ok ? t.ctx - t.Lq + qi : -1;
+    // Columns of the group's tiles.
+    int qi[kTiles], g[kTiles], pos[kTiles];
+    bool col_ok[kTiles];
+#pragma unroll
+    for (int k = 0; k < kTiles; ++k) {
+        const int pair = (t.group * kTiles + k) * 16 + n;
+        qi[k] = pair / G;
+        g[k] = pair - qi[k] * G;
+        col_ok[k] = qi[k] < t.Lq;
+        pos[k] = col_ok[k] ? t.ctx - t.Lq + qi[k] : -1;
+    }
 
     int bid = 0;
     if (lane < p1 - p0) bid = a.table[size_t(t.b) * a.max_pages + p0 + lane];
 
-    u32x4 qop[4];
-    {
-        const uint16_t *qrow = a.q + (size_t(t.q0 + (col_ok ? qi : 0)) * a.nh + h * G + (col_ok ? g : 0)) * kHeadDim + grp * 8;
+    u32x4 qop[kTiles][4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) qop[s] = *reinterpret_cast<const u32x4 *>(qrow + 32 * s);
+    for (int k = 0; k < kTiles; ++k) {
+        const uint16_t *qrow =
+            a.q + (size_t(t.q0 + (col_ok[k] ? qi[k] : 0)) * a.nh + h * G + (col_ok[k] ? g[k] : 0)) * kHeadDim + grp * 8;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) qop[s] = col_ok ? qop[s] : u32x4{0, 0, 0, 0};
+        for (int s = 0; s < 4; ++s) qop[k][s] = *reinterpret_cast<const u32x4 *>(qrow + 32 * s);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qop[k][s] = col_ok[k] ? qop[k][s] : u32x4{0, 0, 0, 0};
     }
 
     const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
@@ -150,32 +161,43 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillKernel(Args
         loadPair(r, kp, vp, (size_t(ba) * a.nkvh + h) * 256, (size_t(bb) * a.nkvh + h) * 256);
     };
 
-    Acc acc;
-    acc.reset();
+    Acc acc[kTiles];
+#pragma unroll
+    for (int k = 0; k < kTiles; ++k) acc[k].reset();
+    auto consume = [&](PagePair &r, int pp) {
+#pragma unroll
+        for (int k = 0; k < kTiles; ++k) consumePair<OUT_F32>(acc[k], r, qop[k], pp * 16, pos[k], t.ctx, pp + 1 < p1, grp, a.scale_log2);
+    };
     PagePair ra, rb;
     issue(ra, p0);
     issue(rb, p0 + 2);
     for (int pp = p0; pp < p1; pp += 4) {
-        consumePair(acc, ra, qop, pp * 16, pos, t.ctx, pp + 1 < p1, grp, a.scale_log2);
+        consume(ra, pp);
         issue(ra, pp + 4);
-        if (pp + 2 < p1) consumePair(acc, rb, qop, (pp + 2) * 16, pos, t.ctx, pp + 3 < p1, grp, a.scale_log2);
+        if (pp + 2 < p1) consume(rb, pp + 2);
         issue(rb, pp + 6);
     }
     if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
-    float lt = acc.l + __shfl_xor(acc.l, 16);
-    lt += __shfl_xor(lt, 32);
-    if (!col_ok) return;
-    if (t.nsplit == 1) {
-        const size_t row = (size_t(t.q0 + qi) * a.nh + h * G + g) * kHeadDim;
-        const float inv = 1.f / lt;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, acc.o[i] * inv);
-        return;
-    }
     float *rec = a.records + (size_t(unit) * a.max_splits + split) * kRecordFloats;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4 *>(rec + (i * 16 + n) * 16 + grp * 4) = acc.o[i];
-    if (grp == 0) *reinterpret_cast<float2 *>(rec + 16 * kHeadDim + 2 * n) = make_float2(acc.m, lt);
+    for (int k = 0; k < kTiles; ++k) {
+        float lt = acc[k].l + __shfl_xor(acc[k].l, 16);
+        lt += __shfl_xor(lt, 32);
+        if (!col_ok[k]) continue;
+        if (t.nsplit == 1) {
+            const size_t row = (size_t(t.q0 + qi[k]) * a.nh + h * G + g[k]) * kHeadDim;
+            const float inv = 1.f / lt;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, acc[k].o[i] * inv);
+            continue;
+        }
+        const int c = k * 16 + n; // column within the group
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<f32x4 *>(rec + (i * kTiles * 16 + c) * 16 + grp * 4) = acc[k].o[i];
+        if (grp == 0)
+            *reinterpret_cast<float2 *>(rec + kTiles * 16 * kHeadDim + 2 * c) = make_float2(acc[k].m, lt);
+    }
 }
 
 // Merge the split records of each unit with more than one split.
@@ -185,16 +207,18 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillCombineKern
     const int lane = threadIdx.x;
     const int n = lane & 15;
     const int grp = lane >> 4;
-    const int unit = blockIdx.x;
+    const int unit = blockIdx.x / kTiles;
+    const int k = blockIdx.x - unit * kTiles; // tile of the group this wave merges
     if (unit >= a.units) return;
     const int h = unit % a.nkvh;
     TileGeom t;
     if (!tileGeom(a, unit / a.nkvh, t, false) || t.nsplit <= 1) return;
     const int G = a.G;
-    const int pair = t.tile * 16 + n;
+    const int pair = (t.group * kTiles + k) * 16 + n;
     const int qi = pair / G;
     const int g = pair - qi * G;
     const bool col_ok = qi < t.Lq;
+    const int c = k * 16 + n;
     const float *recs = a.records + size_t(unit) * a.max_splits * kRecordFloats;
     float M = -INFINITY, L = 0.f;
     f32x4 o[8];
@@ -206,11 +230,12 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillCombineKern
 #pragma unroll
         for (int s = 0; s < kMergeBatch; ++s) {
             const float *rec = recs + size_t(min(k0 + s, t.nsplit - 1)) * kRecordFloats;
-            const float2 ml = *reinterpret_cast<const float2 *>(rec + 16 * kHeadDim + 2 * n);
+            const float2 ml = *reinterpret_cast<const float2 *>(rec + kTiles * 16 * kHeadDim + 2 * c);
             mr[s] = k0 + s < t.nsplit ? ml.x : -INFINITY;
             lr[s] = ml.y;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) orr[s][i] = *reinterpret_cast<const f32x4 *>(rec + (i * 16 + n) * 16 + grp * 4);
+            for (int i = 0; i < 8; ++i)
+                orr[s][i] = *reinterpret_cast<const f32x4 *>(rec + (i * kTiles * 16 + c) * 16 + grp * 4);
         }
 #pragma unroll
         for (int s = 0; s < kMergeBatch; ++s) {
@@ -242,8 +267,8 @@ int envInt(const char *name, int fallback) {
 
 PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages) {
     PagedAttentionPlan p{};
-    const int tiles = (T * group + 15) / 16 + B;
-    p.units = tiles * nkvh;
+    const int groups = ((T * group + 15) / 16 + kTiles - 1) / kTiles + B;
+    p.units = groups * nkvh;
     p.units_padded = (p.units + kXcds - 1) / kXcds * kXcds;
     // Pages per split: even (pairs of pages), at most 64 (one block id per lane).
     int pps = envInt("LLAISYS_PAGES_PER_SPLIT", 64);
@@ -285,10 +310,10 @@ void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_
     auto s = static_cast<hipStream_t>(stream);
     if (out_f32) {
         hipLaunchKernelGGL((prefillKernel<true>), grid, block, 0, s, a);
-        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<true>), dim3(plan.units), block, 0, s, a);
+        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<true>), dim3(plan.units * kTiles), block, 0, s, a);
     } else {
         hipLaunchKernelGGL((prefillKernel<false>), grid, block, 0, s, a);
-        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<false>), dim3(plan.units), block, 0, s, a);
+        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<false>), dim3(plan.units * kTiles), block, 0, s, a);
     }
     HIP_CHECK(hipGetLastError());
 }

@@ -2,7 +2,7 @@
 //
 // Work = every (sequence b, kv head h) unit's page pairs, laid end to end:
 // unit u = b*nkvh + h owns npairs(b) = ceil(ceil(ctx_b/16)/2) consecutive
-// pair indices. A grid of W single-wave workgroups (about two per CU) splits
+// pair indices. A grid of W single-wave workgroups (about one per CU) splits
 // the N pairs evenly: wave w takes pairs [w*N/W, (w+1)*N/W), at most 64, and
 // streams them through a ring of NSTAGE page pairs in flight, crossing unit
 // boundaries without draining the ring. Every wave does the same small prefix
@@ -247,7 +247,7 @@ __global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
                 u32x4 qop[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) qop[t] = n < G ? ring.q[st][t] : u32x4{0, 0, 0, 0};
-                consumePair(acc, ring.pp[st], qop, 32 * j, c - 1, c, hasB, grp, a.scale_log2);
+                consumePair<OUT_F32>(acc, ring.pp[st], qop, 32 * j, c - 1, c, hasB, grp, a.scale_log2);
             }
             issue(st, k + NSTAGE);
         }
@@ -384,7 +384,7 @@ int computeUnits() {
 DecodePlan planDecode(int B, int nkvh, int group, int max_pages) {
     DecodePlan p{};
     const long long max_pairs = (long long)B * nkvh * ((max_pages + 1) / 2);
-    const int fill = std::max(1, envInt("LLAISYS_DECODE_WAVES", 2 * computeUnits()));
+    const int fill = std::max(1, envInt("LLAISYS_DECODE_WAVES", computeUnits()));
     p.waves = int(std::max<long long>(fill, (max_pairs + kPairsPerWave - 1) / kPairsPerWave));
     p.record_bytes = size_t(2) * p.waves * group * (kHeadDim + 2) * sizeof(float);
     p.lds_bytes = size_t(3 * B + 1) * sizeof(int);
