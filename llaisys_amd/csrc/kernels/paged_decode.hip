@@ -126,7 +126,7 @@ template <int NSTAGE> struct Ring {
 };
 
 template <bool OUT_F32, int NSTAGE>
-__global__ void __launch_bounds__(64) decodeKernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) decodeKernel(DecodeArgs a) {
     extern __shared__ int lds[];
     int *S = lds;
     int *C = lds + a.B + 1;
