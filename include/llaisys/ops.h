@@ -71,6 +71,11 @@ __C {
                                        llaisysTensor_t v_pool, llaisysTensor_t block_table,
                                        llaisysTensor_t cu_seqlens);
 
+    /* New. Copy whole (block, all kv heads) pages inside the pools:
+     * pairs [P, 2] I32 of (src, dst) block ids, as produced by
+     * llaisysKVSeqReserve for copy-on-write of a shared last block. */
+    __export void llaisysPagedKVCopyBlocks(llaisysTensor_t k_pool, llaisysTensor_t v_pool, llaisysTensor_t pairs);
+
     /* New. Batched decode attention (flash-decoding with split-KV and a
      * log-sum-exp combine): q [B, nh, 128] BF16, out [B, nh, 128] BF16 or F32.
      * Sequence b's single query attends all ctx_len[b] (>= 1) cached tokens,

@@ -3,6 +3,7 @@
 // src/llaisys/llaisys_tensor.hpp:7-9). Every entry point catches exceptions:
 // the message is already on stderr, is kept for llaisysGetLastError(), and the
 // function returns its neutral value (NULL / 0 / nothing).
+#include "llaisys/kv_cache.h"
 #include "llaisys/ops.h"
 #include "llaisys/runtime.h"
 #include "llaisys/tensor.h"
@@ -10,6 +11,7 @@
 #include "common.hpp"
 #include "core/core.hpp"
 #include "device/runtime_api.hpp"
+#include "kvcache/block_manager.hpp"
 #include "ops/ops.hpp"
 #include "tensor/tensor.hpp"
 
@@ -18,6 +20,10 @@
 
 struct LlaisysTensor {
     llaisys::tensor_t tensor;
+};
+
+struct LlaisysKVBlockManager {
+    llaisys::kvcache::BlockManager impl;
 };
 
 namespace {
@@ -240,6 +246,61 @@ void llaisysPagedAttentionVarlen(llaisysTensor_t out, llaisysTensor_t q, llaisys
         llaisys::ops::pagedAttention(unbox(out, w), unbox(q, w), unbox(k_pool, w), unbox(v_pool, w),
                                      unbox(block_table, w), unbox(ctx_len, w), unbox(cu_q, w), scale);
     });
+}
+
+void llaisysPagedKVCopyBlocks(llaisysTensor_t k_pool, llaisysTensor_t v_pool, llaisysTensor_t pairs) {
+    guardedVoid([&] {
+        const char *w = "paged_kv_copy_blocks";
+        llaisys::ops::pagedKVCopyBlocks(unbox(k_pool, w), unbox(v_pool, w), unbox(pairs, w));
+    });
+}
+
+// ---------------- kv_cache.h
+namespace {
+llaisys::kvcache::BlockManager &mgr(llaisysKVBlockManager_t m) {
+    if (!m) LLAISYS_RAISE("kv block manager: null handle");
+    return m->impl;
+}
+} // namespace
+
+llaisysKVBlockManager_t llaisysKVBlockManagerCreate(int num_blocks) {
+    return guarded([&]() -> llaisysKVBlockManager_t { return new LlaisysKVBlockManager{llaisys::kvcache::BlockManager(num_blocks)}; },
+                   nullptr);
+}
+
+void llaisysKVBlockManagerDestroy(llaisysKVBlockManager_t m) { delete m; }
+
+int llaisysKVNumFreeBlocks(llaisysKVBlockManager_t m) {
+    return guarded([&] { return mgr(m).numFree(); }, -1);
+}
+
+int llaisysKVSeqCreate(llaisysKVBlockManager_t m, int64_t seq_id, const int64_t *tokens, size_t ntokens) {
+    return guarded([&] { return mgr(m).create(seq_id, tokens, ntokens); }, -1);
+}
+
+int llaisysKVSeqFork(llaisysKVBlockManager_t m, int64_t parent, int64_t child) {
+    return guarded([&] { mgr(m).fork(parent, child); return 0; }, -1);
+}
+
+int llaisysKVSeqReserve(llaisysKVBlockManager_t m, int64_t seq_id, int ntokens, int32_t *cow_pairs, int cow_capacity) {
+    return guarded([&] { return mgr(m).reserve(seq_id, ntokens, cow_pairs, cow_capacity); }, -1);
+}
+
+int llaisysKVSeqCommit(llaisysKVBlockManager_t m, int64_t seq_id, int ntokens, const int64_t *tokens) {
+    return guarded([&] { mgr(m).commit(seq_id, ntokens, tokens); return 0; }, -1);
+}
+
+int llaisysKVSeqFree(llaisysKVBlockManager_t m, int64_t seq_id) {
+    return guarded([&] { mgr(m).release(seq_id); return 0; }, -1);
+}
+
+int llaisysKVSeqLength(llaisysKVBlockManager_t m, int64_t seq_id) {
+    return guarded([&] { return mgr(m).length(seq_id); }, -1);
+}
+
+int llaisysKVBuildBlockTable(llaisysKVBlockManager_t m, const int64_t *seq_ids, size_t B, int32_t *table,
+                             size_t max_pages, int32_t *ctx_len) {
+    return guarded([&] { return mgr(m).buildTable(seq_ids, B, table, max_pages, ctx_len); }, -1);
 }
 
 } // extern "C"

@@ -46,6 +46,10 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
 
 // Chunked prefill: the sequences of a varlen batch with >= 2 queries, as
 // (16-column query tile, kv head) units split over pages, then a combine kernel.
+// Copy whole blocks (all kv heads, K and V): pairs[P][2] = (src, dst).
+void pagedCopyBlocks(uint16_t *k_pool, uint16_t *v_pool, const int32_t *pairs, int P, int nkvh, int num_blocks,
+                     int *err, void *stream);
+
 struct PagedAttentionPlan {
     int units;           // (query tile, kv head) work units (upper bound)
     int units_padded;    // rounded up to a multiple of the XCD count

@@ -128,7 +128,31 @@ __global__ void __launch_bounds__(256) gatherKernel(uint16_t *__restrict__ k_out
     *reinterpret_cast<uint4 *>(v_out + dst) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// One 256-thread block per (pair, pool): 16 B per thread per 4 KiB page,
+// looping over the kv heads of the block.
+__global__ void __launch_bounds__(256) copyBlocksKernel(uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool,
+                                                        const int32_t *__restrict__ pairs, int nkvh, int num_blocks,
+                                                        int *err) {
+    const int src = pairs[2 * blockIdx.x];
+    const int dst = pairs[2 * blockIdx.x + 1];
+    if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) {
+        if (threadIdx.x == 0) atomicOr(err, kErrBadBlock);
+        return;
+    }
+    uint4 *pool = reinterpret_cast<uint4 *>(blockIdx.y == 0 ? k_pool : v_pool);
+    const size_t per_block = size_t(nkvh) * kPageElems / 8; // uint4 per block
+    for (size_t i = threadIdx.x; i < per_block; i += 256) pool[dst * per_block + i] = pool[src * per_block + i];
+}
+
 } // namespace
+
+void pagedCopyBlocks(uint16_t *k_pool, uint16_t *v_pool, const int32_t *pairs, int P, int nkvh, int num_blocks,
+                     int *err, void *stream) {
+    if (P == 0) return;
+    hipLaunchKernelGGL(copyBlocksKernel, dim3(P, 2), dim3(256), 0, static_cast<hipStream_t>(stream), k_pool, v_pool,
+                       pairs, nkvh, num_blocks, err);
+    HIP_CHECK(hipGetLastError());
+}
 
 void pagedAppend(uint16_t *k_pool, uint16_t *v_pool, const uint16_t *k_new, const uint16_t *v_new,
                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_new, int T, int B, int nkvh,

@@ -177,6 +177,19 @@ void pagedKVGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t 
                    int(block_table->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
 }
 
+void pagedKVCopyBlocks(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_t &pairs) {
+    const char *op = "paged_kv_copy_blocks";
+    LLAISYS_CHECK(k_pool && v_pool && pairs, op << ": null tensor");
+    checkPool(k_pool, v_pool, op);
+    LLAISYS_CHECK(pairs->ndim() == 2 && pairs->shape()[1] == 2, op << ": pairs must be [P, 2], got " << shapeStr(pairs));
+    requireDtype(pairs, LLAISYS_DTYPE_I32, op, "pairs");
+    requireContiguous(pairs, op, "pairs");
+    requireAmd(op, {&k_pool, &v_pool, &pairs});
+    K::pagedCopyBlocks(reinterpret_cast<uint16_t *>(k_pool->data()), reinterpret_cast<uint16_t *>(v_pool->data()),
+                       reinterpret_cast<const int32_t *>(pairs->data()), int(pairs->shape()[0]),
+                       int(k_pool->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
+}
+
 void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_pool, const tensor_t &v_pool,
                     const tensor_t &block_table, const tensor_t &ctx_len, const tensor_t &cu_q, float scale) {
     const char *op = cu_q ? "paged_attention_varlen" : "paged_attention";

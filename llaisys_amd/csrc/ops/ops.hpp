@@ -14,6 +14,8 @@ void pagedKVAppend(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_
 void pagedKVGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t &k_pool, const tensor_t &v_pool,
                    const tensor_t &block_table, const tensor_t &cu_seqlens);
 
+void pagedKVCopyBlocks(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_t &pairs);
+
 void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_pool, const tensor_t &v_pool,
                     const tensor_t &block_table, const tensor_t &ctx_len, const tensor_t &cu_q /* null = decode */,
                     float scale);

@@ -19,6 +19,7 @@ from .llaisys_types import (
     llaisysMemcpyKind_t,
     llaisysStream_t,
 )
+from .kv_cache import load_kv_cache, llaisysKVBlockManager_t
 from .ops import load_ops
 from .runtime import LlaisysRuntimeAPI, load_runtime
 from .tensor import llaisysTensor_t, load_tensor
@@ -65,6 +66,7 @@ LIB_LLAISYS = load_shared_library()
 load_runtime(LIB_LLAISYS)
 load_tensor(LIB_LLAISYS)
 load_ops(LIB_LLAISYS)
+load_kv_cache(LIB_LLAISYS)
 
 
 class LlaisysError(RuntimeError):
@@ -88,6 +90,7 @@ __all__ = [
     "LlaisysRuntimeAPI",
     "llaisysStream_t",
     "llaisysTensor_t",
+    "llaisysKVBlockManager_t",
     "llaisysDataType_t",
     "DataType",
     "llaisysDeviceType_t",

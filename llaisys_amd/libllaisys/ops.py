@@ -20,6 +20,8 @@ def load_ops(lib):
         ("llaisysSelfAttention", [T, T, T, T, c_float]),
         # k_pool, v_pool, k_new, v_new, block_table, ctx_len, cu_new (nullable)
         ("llaisysPagedKVAppend", [T, T, T, T, T, T, T]),
+        # k_pool, v_pool, pairs [P, 2] (src, dst)
+        ("llaisysPagedKVCopyBlocks", [T, T, T]),
         # k_out, v_out, k_pool, v_pool, block_table, cu_seqlens
         ("llaisysPagedKVGather", [T, T, T, T, T, T]),
         # out, q, k_pool, v_pool, block_table, ctx_len, scale

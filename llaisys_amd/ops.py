@@ -77,6 +77,12 @@ class Ops:
         check_last_error()
 
     @staticmethod
+    def paged_kv_copy_blocks(k_pool: Tensor, v_pool: Tensor, pairs: Tensor):
+        """Copy whole blocks (src -> dst, pairs [P, 2] I32), e.g. for copy-on-write."""
+        LIB_LLAISYS.llaisysPagedKVCopyBlocks(_h(k_pool), _h(v_pool), _h(pairs))
+        check_last_error()
+
+    @staticmethod
     def paged_attention(out: Tensor, q: Tensor, k_pool: Tensor, v_pool: Tensor,
                         block_table: Tensor, ctx_len: Tensor, scale: float):
         """Batched decode attention over paged KV (one query per sequence)."""
