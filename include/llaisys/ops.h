@@ -3,11 +3,10 @@
  *
  * llaisysSelfAttention and the eight other reference ops keep the reference's
  * declarations (include/llaisys/ops.h:7-15) so python/llaisys/libllaisys/ops.py
- * binds unchanged. This library implements the KV-cache attention path only:
- * llaisysSelfAttention runs on LLAISYS_DEVICE_AMD tensors; the other eight ops
- * are exported so the reference's loader finds them, and fail with an
- * "outside this library's scope" error, as the reference's stubs fail with
- * TO_BE_IMPLEMENTED (src/ops/<op>/op.cpp:4-6).
+ * binds unchanged. All run on LLAISYS_DEVICE_AMD tensors (F32, F16, BF16;
+ * indices I64), contiguous unless stated; CPU tensors are rejected (the
+ * reference's CPU ops are TO_BE_IMPLEMENTED stubs, src/ops/<op>/op.cpp:4-6,
+ * except add). Contracts are the reference README's (README.md:157-292):
  *
  * The llaisysPagedKV* / llaisysPagedAttention* entry points are new. The
  * reference has no paged KV code; they follow its op conventions
@@ -34,14 +33,23 @@
 #include "tensor.h"
 
 __C {
-    /* Reference ops outside the KV path: exported, raise an error (ops.h:7-13,15). */
+    /* ops.h:7: c = a + b, one shape and dtype. */
     __export void llaisysAdd(llaisysTensor_t c, llaisysTensor_t a, llaisysTensor_t b);
+    /* ops.h:8: max over the last dim of vals; max_idx I64 and max_val (may be
+     * NULL) hold one element per row (1 for a 1-D vals, README.md:161-167). */
     __export void llaisysArgmax(llaisysTensor_t max_idx, llaisysTensor_t max_val, llaisysTensor_t vals);
+    /* ops.h:9: out[i] = weight[index[i]], index I64 (README.md:171-177). */
     __export void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index, llaisysTensor_t weight);
+    /* ops.h:10: out = in . weight^T + bias, weight [out, in], bias may be NULL
+     * (README.md:181-198); rocBLAS GEMM, fp32 accumulation. */
     __export void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, llaisysTensor_t bias);
+    /* ops.h:11: copy between equal shapes with any strides (README.md:286-292). */
     __export void llaisysRearrange(llaisysTensor_t out, llaisysTensor_t in);
+    /* ops.h:12: y = w * x / sqrt(mean(x^2) + eps) per row (README.md:202-217). */
     __export void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, float eps);
+    /* ops.h:13: rotary embedding of [seqlen, nhead, d] by pos_ids I64 (README.md:221-242). */
     __export void llaisysROPE(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t pos_ids, float theta);
+    /* ops.h:15: out = up * gate / (1 + exp(-gate)) (README.md:268-278). */
     __export void llaisysSwiGLU(llaisysTensor_t out, llaisysTensor_t gate, llaisysTensor_t up);
 
     /* Replaces include/llaisys/ops.h:14 (stub src/ops/self_attention/op.cpp:4-6;

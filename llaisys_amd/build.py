@@ -63,7 +63,9 @@ def build(verbose: bool = True) -> Path:
         objs = list(ex.map(_compile, srcs))
     LIB.parent.mkdir(exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    rocm_lib = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), f"-L{rocm_lib}", "-lrocblas",
+           "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

@@ -178,29 +178,35 @@ llaisysTensor_t tensorSlice(llaisysTensor_t t, size_t dim, size_t start, size_t 
 }
 
 // ---------------- ops.h
-void llaisysAdd(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t) {
-    guardedVoid([] { llaisys::ops::outOfScope("add"); });
+void llaisysAdd(llaisysTensor_t c, llaisysTensor_t a, llaisysTensor_t b) {
+    guardedVoid([&] { llaisys::ops::add(unbox(c, "add"), unbox(a, "add"), unbox(b, "add")); });
 }
-void llaisysArgmax(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t) {
-    guardedVoid([] { llaisys::ops::outOfScope("argmax"); });
+void llaisysArgmax(llaisysTensor_t max_idx, llaisysTensor_t max_val, llaisysTensor_t vals) {
+    guardedVoid([&] { llaisys::ops::argmax(unbox(max_idx, "argmax"), unboxOpt(max_val), unbox(vals, "argmax")); });
 }
-void llaisysEmbedding(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t) {
-    guardedVoid([] { llaisys::ops::outOfScope("embedding"); });
+void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index, llaisysTensor_t weight) {
+    guardedVoid([&] {
+        llaisys::ops::embedding(unbox(out, "embedding"), unbox(index, "embedding"), unbox(weight, "embedding"));
+    });
 }
-void llaisysLinear(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t, llaisysTensor_t) {
-    guardedVoid([] { llaisys::ops::outOfScope("linear"); });
+void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, llaisysTensor_t bias) {
+    guardedVoid([&] {
+        llaisys::ops::linear(unbox(out, "linear"), unbox(in, "linear"), unbox(weight, "linear"), unboxOpt(bias));
+    });
 }
-void llaisysRearrange(llaisysTensor_t, llaisysTensor_t) {
-    guardedVoid([] { llaisys::ops::outOfScope("rearrange"); });
+void llaisysRearrange(llaisysTensor_t out, llaisysTensor_t in) {
+    guardedVoid([&] { llaisys::ops::rearrange(unbox(out, "rearrange"), unbox(in, "rearrange")); });
 }
-void llaisysRmsNorm(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t, float) {
-    guardedVoid([] { llaisys::ops::outOfScope("rms_norm"); });
+void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, float eps) {
+    guardedVoid([&] {
+        llaisys::ops::rmsNorm(unbox(out, "rms_norm"), unbox(in, "rms_norm"), unbox(weight, "rms_norm"), eps);
+    });
 }
-void llaisysROPE(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t, float) {
-    guardedVoid([] { llaisys::ops::outOfScope("rope"); });
+void llaisysROPE(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t pos_ids, float theta) {
+    guardedVoid([&] { llaisys::ops::rope(unbox(out, "rope"), unbox(in, "rope"), unbox(pos_ids, "rope"), theta); });
 }
-void llaisysSwiGLU(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t) {
-    guardedVoid([] { llaisys::ops::outOfScope("swiglu"); });
+void llaisysSwiGLU(llaisysTensor_t out, llaisysTensor_t gate, llaisysTensor_t up) {
+    guardedVoid([&] { llaisys::ops::swiglu(unbox(out, "swiglu"), unbox(gate, "swiglu"), unbox(up, "swiglu")); });
 }
 
 void llaisysSelfAttention(llaisysTensor_t attn_val, llaisysTensor_t q, llaisysTensor_t k, llaisysTensor_t v,

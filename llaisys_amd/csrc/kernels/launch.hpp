@@ -63,4 +63,21 @@ void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_
                   int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
                   float *records, int *err, void *stream);
 
+// ---- model ops (model_ops.hip, linear.cpp)
+constexpr int kMaxDims = 8;
+void add(void *c, const void *a, const void *b, ElemType t, size_t n, void *stream);
+void swiglu(void *out, const void *gate, const void *up, ElemType t, size_t n, void *stream);
+void addBias(void *x, const void *bias, ElemType t, size_t rows, size_t cols, void *stream);
+void rmsNorm(void *out, const void *x, const void *w, ElemType t, size_t rows, int d, float eps, void *stream);
+void rope(void *out, const void *in, const int64_t *pos, ElemType t, size_t ntok, int nhead, int d, float theta,
+          void *stream);
+void embedding(void *out, const int64_t *idx, const void *weight, ElemType t, size_t rows, int64_t vocab, int d,
+               int *err, void *stream);
+// Row-wise argmax over the last dim: idx[rows] (first maximum), val[rows] (may be null).
+void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, int64_t n, void *stream);
+void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *shape, const int64_t *out_strides,
+               const int64_t *in_strides, void *stream);
+// Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]), row-major, fp32 accumulation.
+void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream);
+
 } // namespace llaisys::kernels

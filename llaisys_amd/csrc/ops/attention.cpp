@@ -90,11 +90,6 @@ int *errWord() { return core::context().runtime().errorWord(); }
 
 } // namespace
 
-void outOfScope(const char *op) {
-    LLAISYS_RAISE(op << ": not implemented by llaisys_amd, which provides the KV-cache attention path "
-                     "(self_attention and the paged KV ops) only");
-}
-
 // README.md:244-266: attn_val [L, nh, dv], q [L, nh, d], k [S, nkvh, d], v [S, nkvh, dv].
 void selfAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k, const tensor_t &v, float scale) {
     const char *op = "self_attention";

@@ -20,6 +20,14 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
                     const tensor_t &block_table, const tensor_t &ctx_len, const tensor_t &cu_q /* null = decode */,
                     float scale);
 
-[[noreturn]] void outOfScope(const char *op);
+// Model ops of the reference (README.md:145-292), AMD device.
+void add(const tensor_t &c, const tensor_t &a, const tensor_t &b);
+void argmax(const tensor_t &max_idx, const tensor_t &max_val, const tensor_t &vals);
+void embedding(const tensor_t &out, const tensor_t &index, const tensor_t &weight);
+void linear(const tensor_t &out, const tensor_t &in, const tensor_t &weight, const tensor_t &bias /* may be null */);
+void rearrange(const tensor_t &out, const tensor_t &in);
+void rmsNorm(const tensor_t &out, const tensor_t &in, const tensor_t &weight, float eps);
+void rope(const tensor_t &out, const tensor_t &in, const tensor_t &pos_ids, float theta);
+void swiglu(const tensor_t &out, const tensor_t &gate, const tensor_t &up);
 
 } // namespace llaisys::ops

@@ -29,25 +29,27 @@ LIB_PATH = Path(os.environ.get("LLAISYS_LIBRARY") or Path(__file__).resolve().pa
 
 
 def _share_hip_runtime():
-    """Map the HIP runtime this process should use before libllaisys.so binds one.
+    """Map the HIP runtime (and rocBLAS) this process should use before
+    libllaisys.so binds them.
 
-    libllaisys.so needs libamdhip64.so.7. PyTorch-ROCm ships its own copy of
-    that library; if libllaisys.so were loaded first it would pull in
-    /opt/rocm's copy and a later `import torch` would bring a second HIP
-    runtime into the process, whose device pointers the first cannot use.
-    So when torch is installed its copy is mapped first (by path, without
-    importing torch), making one runtime serve both. LLAISYS_HIP_RUNTIME
-    names another libamdhip64 to use instead.
+    libllaisys.so needs libamdhip64.so.7 and librocblas.so.5. PyTorch-ROCm
+    ships its own copies under the same sonames; if libllaisys.so were loaded
+    first it would pull in /opt/rocm's and a later `import torch` would bring
+    a second HIP runtime into the process, whose device pointers the first
+    cannot use. So when torch is installed its copies are mapped first (by
+    path, without importing torch), making one runtime serve both.
+    LLAISYS_HIP_RUNTIME names another libamdhip64 to use instead.
     """
     path = os.environ.get("LLAISYS_HIP_RUNTIME")
+    libs = [path] if path else []
     if not path:
         spec = importlib.util.find_spec("torch")
         if spec and spec.submodule_search_locations:
-            cand = Path(list(spec.submodule_search_locations)[0]) / "lib" / "libamdhip64.so"
-            if cand.is_file():
-                path = os.fspath(cand)
-    if path:
-        ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+            torch_lib = Path(list(spec.submodule_search_locations)[0]) / "lib"
+            # The GEMM library too: both share sonames with /opt/rocm's copies.
+            libs = [os.fspath(torch_lib / n) for n in ("libamdhip64.so", "librocblas.so") if (torch_lib / n).is_file()]
+    for lib in libs:
+        ctypes.CDLL(lib, mode=ctypes.RTLD_GLOBAL)
 
 
 def load_shared_library():
