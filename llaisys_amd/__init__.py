@@ -7,6 +7,7 @@ HIP, plus the paged KV ops and the host-side block manager.
 from .libllaisys import DataType, DeviceType, LlaisysError, MemcpyKind
 from .libllaisys import llaisysStream_t as Stream
 from .kv_cache import KVBlockManager
+from . import models
 from .ops import Ops
 from .runtime import RuntimeAPI, context_stream, device_error_flags, set_context_runtime, set_context_stream
 from .tensor import Tensor
@@ -20,6 +21,7 @@ __all__ = [
     "Tensor",
     "Ops",
     "KVBlockManager",
+    "models",
     "LlaisysError",
     "set_context_runtime",
     "context_stream",

@@ -4,6 +4,7 @@
 // the message is already on stderr, is kept for llaisysGetLastError(), and the
 // function returns its neutral value (NULL / 0 / nothing).
 #include "llaisys/kv_cache.h"
+#include "llaisys/models/qwen2.h"
 #include "llaisys/ops.h"
 #include "llaisys/runtime.h"
 #include "llaisys/tensor.h"
@@ -12,11 +13,14 @@
 #include "core/core.hpp"
 #include "device/runtime_api.hpp"
 #include "kvcache/block_manager.hpp"
+#include "models/qwen2.hpp"
 #include "ops/ops.hpp"
 #include "tensor/tensor.hpp"
 
 #include <algorithm>
+#include <memory>
 #include <string>
+#include <vector>
 
 struct LlaisysTensor {
     llaisys::tensor_t tensor;
@@ -24,6 +28,17 @@ struct LlaisysTensor {
 
 struct LlaisysKVBlockManager {
     llaisys::kvcache::BlockManager impl;
+};
+
+// The model plus the handle boxes of its weights. `orig` keeps the boxes the
+// model handed out, so handles a caller swapped into `w` can be detected and
+// copied into the model's own tensors.
+struct LlaisysQwen2Model {
+    std::unique_ptr<llaisys::models::Qwen2Model> impl;
+    LlaisysQwen2Weights w{};
+    LlaisysQwen2Weights orig{};
+    std::vector<std::unique_ptr<LlaisysTensor>> owned;
+    std::vector<std::vector<llaisysTensor_t>> arrays, orig_arrays; // 12 per-layer arrays
 };
 
 namespace {
@@ -56,6 +71,88 @@ llaisys::tensor_t unbox(llaisysTensor_t t, const char *what) {
     return t->tensor;
 }
 llaisys::tensor_t unboxOpt(llaisysTensor_t t) { return t ? t->tensor : nullptr; }
+
+// Per-layer weight slots of LlaisysQwen2Weights in declaration order.
+constexpr int kQwen2LayerSlots = 12;
+llaisysTensor_t *&layerSlot(LlaisysQwen2Weights &w, int k) {
+    llaisysTensor_t **slots[kQwen2LayerSlots] = {&w.attn_norm_w, &w.attn_q_w, &w.attn_q_b,  &w.attn_k_w,
+                                                 &w.attn_k_b,    &w.attn_v_w, &w.attn_v_b,  &w.attn_o_w,
+                                                 &w.mlp_norm_w,  &w.mlp_gate_w, &w.mlp_up_w, &w.mlp_down_w};
+    return *slots[k];
+}
+
+llaisys::tensor_t layerTensor(const llaisys::models::Qwen2LayerWeights &L, int k) {
+    const llaisys::tensor_t *t[kQwen2LayerSlots] = {&L.attn_norm, &L.q_w, &L.q_b, &L.k_w, &L.k_b, &L.v_w,
+                                                    &L.v_b,       &L.o_w, &L.mlp_norm, &L.gate_w, &L.up_w, &L.down_w};
+    return *t[k];
+}
+
+LlaisysQwen2Model *createQwen2(const LlaisysQwen2Meta *meta, llaisysDeviceType_t device, const int *device_ids,
+                               int ndevice, size_t num_blocks) {
+    LLAISYS_CHECK(meta, "qwen2: null meta");
+    LLAISYS_CHECK(device == LLAISYS_DEVICE_AMD, "qwen2: llaisys_amd runs the model on LLAISYS_DEVICE_AMD only");
+    LLAISYS_CHECK(ndevice == 1, "qwen2: one device per model (got " << ndevice << ")");
+    const int id = device_ids ? device_ids[0] : 0;
+    llaisys::models::Qwen2Config cfg{meta->dtype, meta->nlayer, meta->hs,     meta->nh,    meta->nkvh, meta->dh,
+                                     meta->di,    meta->maxseq, meta->voc,    meta->epsilon, meta->theta,
+                                     meta->end_token};
+    if (num_blocks == 0) num_blocks = (meta->maxseq + 15) / 16 + 1;
+    auto m = std::make_unique<LlaisysQwen2Model>();
+    m->impl = std::make_unique<llaisys::models::Qwen2Model>(cfg, id, num_blocks);
+    auto box = [&](const llaisys::tensor_t &t) {
+        m->owned.push_back(std::make_unique<LlaisysTensor>(LlaisysTensor{t}));
+        return m->owned.back().get();
+    };
+    m->w.in_embed = box(m->impl->inEmbed());
+    m->w.out_embed = box(m->impl->outEmbed());
+    m->w.out_norm_w = box(m->impl->outNorm());
+    m->arrays.assign(kQwen2LayerSlots, std::vector<llaisysTensor_t>(cfg.nlayer));
+    for (int k = 0; k < kQwen2LayerSlots; ++k) {
+        for (size_t l = 0; l < cfg.nlayer; ++l) m->arrays[k][l] = box(layerTensor(m->impl->layer(l), k));
+        layerSlot(m->w, k) = m->arrays[k].data();
+    }
+    m->orig = m->w;
+    m->orig_arrays = m->arrays;
+    return m.release();
+}
+
+// Copy a caller-supplied tensor into the model's own and restore the slot.
+void adopt(llaisysTensor_t &slot, llaisysTensor_t own) {
+    if (slot == own || slot == nullptr) {
+        slot = own;
+        return;
+    }
+    const auto &src = slot->tensor;
+    const auto &dst = own->tensor;
+    LLAISYS_CHECK(src->shape() == dst->shape() && src->dtype() == dst->dtype(),
+                  "qwen2: replaced weight " << src->info() << " does not match " << dst->info());
+    LLAISYS_CHECK(src->isContiguous(), "qwen2: replaced weight must be contiguous");
+    auto &ctx = llaisys::core::context();
+    ctx.setDevice(dst->deviceType(), dst->deviceId());
+    const size_t bytes = dst->numel() * dst->elementSize();
+    const auto kind = src->deviceType() == LLAISYS_DEVICE_CPU ? LLAISYS_MEMCPY_H2D : LLAISYS_MEMCPY_D2D;
+    if (bytes) ctx.runtime().api()->memcpy_sync(dst->data(), src->data(), bytes, kind);
+    slot = own;
+}
+
+void syncWeights(LlaisysQwen2Model &m) {
+    adopt(m.w.in_embed, m.orig.in_embed);
+    adopt(m.w.out_embed, m.orig.out_embed);
+    adopt(m.w.out_norm_w, m.orig.out_norm_w);
+    for (int k = 0; k < kQwen2LayerSlots; ++k) {
+        llaisysTensor_t *arr = layerSlot(m.w, k);
+        if (arr != m.arrays[k].data()) { // caller swapped the whole array
+            for (size_t l = 0; l < m.arrays[k].size(); ++l) m.arrays[k][l] = arr[l];
+            layerSlot(m.w, k) = m.arrays[k].data();
+        }
+        for (size_t l = 0; l < m.arrays[k].size(); ++l) adopt(m.arrays[k][l], m.orig_arrays[k][l]);
+    }
+}
+
+llaisys::models::Qwen2Model &model(LlaisysQwen2Model *m) {
+    LLAISYS_CHECK(m && m->impl, "qwen2: null model");
+    return *m->impl;
+}
 
 } // namespace
 
@@ -307,6 +404,71 @@ int llaisysKVSeqLength(llaisysKVBlockManager_t m, int64_t seq_id) {
 int llaisysKVBuildBlockTable(llaisysKVBlockManager_t m, const int64_t *seq_ids, size_t B, int32_t *table,
                              size_t max_pages, int32_t *ctx_len) {
     return guarded([&] { return mgr(m).buildTable(seq_ids, B, table, max_pages, ctx_len); }, -1);
+}
+
+// ---------------- models/qwen2.h
+LlaisysQwen2Model *llaisysQwen2ModelCreate(const LlaisysQwen2Meta *meta, llaisysDeviceType_t device, int *device_ids,
+                                           int ndevice) {
+    return guarded([&] { return createQwen2(meta, device, device_ids, ndevice, 0); },
+                   static_cast<LlaisysQwen2Model *>(nullptr));
+}
+
+LlaisysQwen2Model *llaisysQwen2ModelCreatePaged(const LlaisysQwen2Meta *meta, llaisysDeviceType_t device,
+                                                int *device_ids, int ndevice, size_t num_blocks) {
+    return guarded(
+        [&] {
+            LLAISYS_CHECK(num_blocks > 0, "qwen2: num_blocks must be positive");
+            return createQwen2(meta, device, device_ids, ndevice, num_blocks);
+        },
+        static_cast<LlaisysQwen2Model *>(nullptr));
+}
+
+void llaisysQwen2ModelDestroy(LlaisysQwen2Model *m) {
+    guardedVoid([&] { delete m; });
+}
+
+LlaisysQwen2Weights *llaisysQwen2ModelWeights(LlaisysQwen2Model *m) {
+    return guarded([&] { model(m); return &m->w; }, static_cast<LlaisysQwen2Weights *>(nullptr));
+}
+
+int64_t llaisysQwen2ModelInfer(LlaisysQwen2Model *m, int64_t *token_ids, size_t ntoken) {
+    return guarded([&] { auto &impl = model(m); syncWeights(*m); return impl.infer(token_ids, ntoken); }, int64_t(-1));
+}
+
+int64_t llaisysQwen2SeqCreate(LlaisysQwen2Model *m, const int64_t *tokens, size_t ntokens, size_t *reused) {
+    return guarded([&] { return model(m).seqCreate(tokens, ntokens, reused); }, int64_t(-1));
+}
+
+int64_t llaisysQwen2SeqFork(LlaisysQwen2Model *m, int64_t parent) {
+    return guarded([&] { return model(m).seqFork(parent); }, int64_t(-1));
+}
+
+int llaisysQwen2SeqFree(LlaisysQwen2Model *m, int64_t seq_id) {
+    return guarded([&] { model(m).seqFree(seq_id); return 0; }, -1);
+}
+
+int64_t llaisysQwen2SeqLength(LlaisysQwen2Model *m, int64_t seq_id) {
+    return guarded([&] { return int64_t(model(m).seqLength(seq_id)); }, int64_t(-1));
+}
+
+int64_t llaisysQwen2NumFreeBlocks(LlaisysQwen2Model *m) {
+    return guarded([&] { return int64_t(model(m).numFreeBlocks()); }, int64_t(-1));
+}
+
+int llaisysQwen2ModelStep(LlaisysQwen2Model *m, const int64_t *seq_ids, size_t nseq, const int64_t *token_ids,
+                          const size_t *ntokens, int64_t *next_tokens) {
+    return guarded(
+        [&] {
+            auto &impl = model(m);
+            syncWeights(*m);
+            impl.step(seq_ids, nseq, token_ids, ntokens, next_tokens);
+            return 0;
+        },
+        -1);
+}
+
+llaisysTensor_t llaisysQwen2ModelLogits(LlaisysQwen2Model *m) {
+    return guarded([&] { return new LlaisysTensor{model(m).lastLogits()}; }, static_cast<llaisysTensor_t>(nullptr));
 }
 
 } // extern "C"

@@ -78,6 +78,18 @@ void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, 
 void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *shape, const int64_t *out_strides,
                const int64_t *in_strides, void *stream);
 // Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]), row-major, fp32 accumulation.
-void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream);
+// accumulate: Y += X . W^T instead (a residual add folded into the GEMM).
+void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream,
+            bool accumulate = false);
+
+// ---- Qwen2 step glue (qwen2_step.hip), bf16
+// qkv [T, (nh + 2 nkvh) d] -> q [T, nh, d] and k [T, nkvh, d] rotated by pos, v [T, nkvh, d].
+void qkvRope(uint16_t *q, uint16_t *k, uint16_t *v, const uint16_t *qkv, const int64_t *pos, size_t T, int nh, int nkvh,
+             int d, float theta, void *stream);
+// act [T, di] = up * silu(gate) with gate_up rows [gate (di) | up (di)].
+void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *stream);
+// out [R, d] = rms_norm(x[rows[r]]) * w.
+void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
+                 void *stream);
 
 } // namespace llaisys::kernels

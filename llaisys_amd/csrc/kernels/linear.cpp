@@ -47,11 +47,12 @@ rocblas_datatype typeOf(ElemType t) {
 
 } // namespace
 
-void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream) {
+void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream,
+            bool accumulate) {
     if (M == 0 || N == 0) return;
     rocblas_handle h = handleFor();
     ROCBLAS_CHECK(rocblas_set_stream(h, static_cast<hipStream_t>(stream)));
-    const float alpha = 1.f, beta = 0.f;
+    const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
     const rocblas_datatype dt = typeOf(t);
     ROCBLAS_CHECK(rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, w, dt, K, x,
                                   dt, K, &beta, y, dt, N, y, dt, N, rocblas_datatype_f32_r, rocblas_gemm_algo_standard,

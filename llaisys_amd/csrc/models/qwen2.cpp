@@ -1,0 +1,294 @@
+// Qwen2 decoder step over the paged KV cache. Per layer, for the T new tokens
+// of a step (hf Qwen2DecoderLayer order):
+//   h = rms_norm(x) ; qkv = h Wqkv^T + b ; q,k = rope(q,k), v
+//   append k,v into the layer's pages ; a = paged_attention(q)
+//   x += a Wo^T                      (residual folded into the GEMM)
+//   h = rms_norm(x) ; gu = h [Wg;Wu]^T ; act = up * silu(gate)
+//   x += act Wd^T
+// then, for each sequence's last token: logits = rms_norm(x) Wlm^T, argmax.
+#include "qwen2.hpp"
+
+#include "../common.hpp"
+#include "../core/core.hpp"
+#include "../kernels/launch.hpp"
+#include "../ops/ops.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace llaisys::models {
+
+namespace K = llaisys::kernels;
+
+namespace {
+
+tensor_t dev(std::vector<size_t> shape, llaisysDataType_t dt, int id) {
+    return Tensor::create(shape, dt, LLAISYS_DEVICE_AMD, id);
+}
+uint16_t *u16(const tensor_t &t) { return reinterpret_cast<uint16_t *>(t->data()); }
+int64_t *i64(const tensor_t &t) { return reinterpret_cast<int64_t *>(t->data()); }
+tensor_t rows(const tensor_t &t, size_t n) { return t->slice(0, 0, n); }
+
+} // namespace
+
+Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
+    : cfg_(cfg), dev_(device_id), num_blocks_(num_blocks), blocks_(int(num_blocks)) {
+    LLAISYS_CHECK(cfg.dtype == LLAISYS_DTYPE_BF16, "qwen2: the paged KV path runs bf16 models (meta.dtype)");
+    LLAISYS_CHECK(cfg.dh == size_t(K::kHeadDim), "qwen2: head dim must be " << K::kHeadDim << ", got " << cfg.dh);
+    LLAISYS_CHECK(cfg.nlayer > 0 && cfg.hs > 0 && cfg.nh > 0 && cfg.nkvh > 0 && cfg.di > 0 && cfg.voc > 0,
+                  "qwen2: meta sizes must be positive");
+    LLAISYS_CHECK(cfg.nh % cfg.nkvh == 0 && cfg.nh / cfg.nkvh <= 16, "qwen2: need nh % nkvh == 0, nh / nkvh <= 16");
+    LLAISYS_CHECK(num_blocks > 0 && num_blocks < (size_t(1) << 31), "qwen2: bad KV block count " << num_blocks);
+    core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
+    const auto dt = cfg.dtype;
+    const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
+    in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
+    out_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
+    out_norm_ = dev({cfg.hs}, dt, dev_);
+    layers_.resize(cfg.nlayer);
+    for (auto &L : layers_) {
+        L.attn_norm = dev({cfg.hs}, dt, dev_);
+        L.qkv_w = dev({q + 2 * kv, cfg.hs}, dt, dev_);
+        L.qkv_b = dev({q + 2 * kv}, dt, dev_);
+        L.o_w = dev({cfg.hs, q}, dt, dev_);
+        L.mlp_norm = dev({cfg.hs}, dt, dev_);
+        L.gate_up_w = dev({2 * cfg.di, cfg.hs}, dt, dev_);
+        L.down_w = dev({cfg.hs, cfg.di}, dt, dev_);
+        L.q_w = L.qkv_w->slice(0, 0, q);
+        L.k_w = L.qkv_w->slice(0, q, q + kv);
+        L.v_w = L.qkv_w->slice(0, q + kv, q + 2 * kv);
+        L.q_b = L.qkv_b->slice(0, 0, q);
+        L.k_b = L.qkv_b->slice(0, q, q + kv);
+        L.v_b = L.qkv_b->slice(0, q + kv, q + 2 * kv);
+        L.gate_w = L.gate_up_w->slice(0, 0, cfg.di);
+        L.up_w = L.gate_up_w->slice(0, cfg.di, 2 * cfg.di);
+    }
+    for (size_t l = 0; l < cfg.nlayer; ++l) {
+        k_pool_.push_back(dev({num_blocks, cfg.nkvh, size_t(K::kPageTokens), cfg.dh}, LLAISYS_DTYPE_BF16, dev_));
+        v_pool_.push_back(dev({num_blocks, cfg.nkvh, size_t(K::kPageTokens), cfg.dh}, LLAISYS_DTYPE_BF16, dev_));
+    }
+}
+
+Qwen2Model::~Qwen2Model() = default;
+
+void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints64) {
+    auto &rt = core::context().runtime();
+    const auto dt = cfg_.dtype;
+    if (T > cap_T_) {
+        const size_t cap = std::max(T, cap_T_ * 2);
+        const size_t q = cfg_.nh * cfg_.dh, kv = cfg_.nkvh * cfg_.dh;
+        rt.api()->device_synchronize();
+        x_ = dev({cap, cfg_.hs}, dt, dev_);
+        h_ = dev({cap, cfg_.hs}, dt, dev_);
+        qkv_ = dev({cap, q + 2 * kv}, dt, dev_);
+        q_ = dev({cap, cfg_.nh, cfg_.dh}, dt, dev_);
+        k_ = dev({cap, cfg_.nkvh, cfg_.dh}, dt, dev_);
+        v_ = dev({cap, cfg_.nkvh, cfg_.dh}, dt, dev_);
+        attn_ = dev({cap, cfg_.nh, cfg_.dh}, dt, dev_);
+        gu_ = dev({cap, 2 * cfg_.di}, dt, dev_);
+        act_ = dev({cap, cfg_.di}, dt, dev_);
+        cap_T_ = cap;
+    }
+    if (B > cap_B_) {
+        const size_t cap = std::max(B, cap_B_ * 2);
+        rt.api()->device_synchronize();
+        hl_ = dev({cap, cfg_.hs}, dt, dev_);
+        logits_ = dev({cap, cfg_.voc}, dt, dev_);
+        next_ = dev({cap}, LLAISYS_DTYPE_I64, dev_);
+        cap_B_ = cap;
+    }
+    if (ints32 > cap_i32_) {
+        const size_t cap = std::max(ints32, cap_i32_ * 2);
+        rt.api()->device_synchronize();
+        dev_i32_ = dev({cap}, LLAISYS_DTYPE_I32, dev_);
+        host32_ = rt.allocateHostStorage(cap * sizeof(int32_t));
+        cap_i32_ = cap;
+    }
+    if (ints64 + B > cap_i64_) {
+        const size_t cap = std::max(ints64 + B, cap_i64_ * 2);
+        rt.api()->device_synchronize();
+        dev_i64_ = dev({cap}, LLAISYS_DTYPE_I64, dev_);
+        host64_ = rt.allocateHostStorage(cap * sizeof(int64_t));
+        cap_i64_ = cap;
+    }
+}
+
+void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, const size_t *ntokens, int64_t *next) {
+    LLAISYS_CHECK(nseq > 0, "qwen2 step: no sequences");
+    LLAISYS_CHECK(ids && tokens && ntokens && next, "qwen2 step: null argument");
+    core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
+    auto &rt = core::context().runtime();
+    const size_t B = nseq;
+    size_t T = 0;
+    for (size_t i = 0; i < B; ++i) {
+        LLAISYS_CHECK(ntokens[i] >= 1, "qwen2 step: sequence " << ids[i] << " appends no token");
+        LLAISYS_CHECK(size_t(blocks_.length(ids[i])) + ntokens[i] <= cfg_.maxseq,
+                      "qwen2 step: sequence " << ids[i] << " would exceed maxseq " << cfg_.maxseq);
+        for (size_t j = 0; j < i; ++j) LLAISYS_CHECK(ids[j] != ids[i], "qwen2 step: sequence " << ids[i] << " listed twice");
+        T += ntokens[i];
+    }
+    for (size_t i = 0; i < T; ++i)
+        LLAISYS_CHECK(tokens[i] >= 0 && size_t(tokens[i]) < cfg_.voc, "qwen2 step: token id " << tokens[i] << " out of vocabulary");
+
+    // Map the pages the new tokens go to (copy-on-write pairs for shared tails).
+    std::vector<int32_t> cow;
+    std::vector<int32_t> before(B);
+    try {
+        for (size_t i = 0; i < B; ++i) {
+            before[i] = blocks_.length(ids[i]);
+            int32_t pair[2];
+            if (blocks_.reserve(ids[i], int(ntokens[i]), pair, 1) == 1) cow.insert(cow.end(), pair, pair + 2);
+        }
+    } catch (...) {
+        // A sequence already switched to its private copy of a shared block
+        // must get that copy's contents even though this step fails.
+        if (!cow.empty()) {
+            auto pairs = Tensor::create({cow.size() / 2, 2}, LLAISYS_DTYPE_I32, LLAISYS_DEVICE_AMD, dev_);
+            pairs->load(cow.data());
+            for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], pairs);
+            rt.api()->stream_synchronize(rt.stream());
+        }
+        throw;
+    }
+    const size_t max_pages = size_t(std::max(1, blocks_.buildTable(ids, B, nullptr, 0, nullptr)));
+    const size_t ncow = cow.size() / 2;
+    const size_t n32 = B * max_pages + 3 * B + 1 + cow.size();
+    const size_t n64 = 2 * T + B;
+    ensureWorkspace(T, B, n32, n64);
+
+    // int32 staging: table | ctx_before | ctx_after | cu | cow pairs
+    int32_t *h32 = reinterpret_cast<int32_t *>(host32_->memory());
+    std::vector<int32_t> ctx_scratch(B);
+    blocks_.buildTable(ids, B, h32, max_pages, ctx_scratch.data());
+    int32_t *cb = h32 + B * max_pages, *ca = cb + B, *cu = ca + B;
+    cu[0] = 0;
+    for (size_t i = 0; i < B; ++i) {
+        cb[i] = before[i];
+        ca[i] = before[i] + int32_t(ntokens[i]);
+        cu[i + 1] = cu[i] + int32_t(ntokens[i]);
+    }
+    std::copy(cow.begin(), cow.end(), cu + B + 1);
+    // int64 staging: tokens | positions | last rows
+    int64_t *h64 = reinterpret_cast<int64_t *>(host64_->memory());
+    std::memcpy(h64, tokens, T * sizeof(int64_t));
+    for (size_t i = 0; i < B; ++i) {
+        for (size_t j = 0; j < ntokens[i]; ++j) h64[T + cu[i] + j] = before[i] + int64_t(j);
+        h64[2 * T + i] = cu[i + 1] - 1;
+    }
+    auto *api = rt.api();
+    api->memcpy_async(dev_i32_->data(), h32, n32 * sizeof(int32_t), LLAISYS_MEMCPY_H2D, rt.stream());
+    api->memcpy_async(dev_i64_->data(), h64, n64 * sizeof(int64_t), LLAISYS_MEMCPY_H2D, rt.stream());
+
+    table_ = dev_i32_->slice(0, 0, B * max_pages)->view({B, max_pages});
+    ctx_before_ = dev_i32_->slice(0, B * max_pages, B * max_pages + B);
+    ctx_after_ = dev_i32_->slice(0, B * max_pages + B, B * max_pages + 2 * B);
+    cu_ = dev_i32_->slice(0, B * max_pages + 2 * B, B * max_pages + 3 * B + 1);
+    cow_ = ncow ? dev_i32_->slice(0, B * max_pages + 3 * B + 1, n32)->view({ncow, 2}) : nullptr;
+    tok_ = dev_i64_->slice(0, 0, T);
+    pos_ = dev_i64_->slice(0, T, 2 * T);
+    last_ = dev_i64_->slice(0, 2 * T, 2 * T + B);
+
+    bool decode_only = T == B;
+    forward(T, B, decode_only);
+
+    // next tokens back to the host; the staging buffers are free after this.
+    int64_t *hnext = h64 + n64;
+    api->memcpy_async(hnext, next_->data(), B * sizeof(int64_t), LLAISYS_MEMCPY_D2H, rt.stream());
+    api->stream_synchronize(rt.stream());
+    const int flags = rt.takeErrorFlags();
+    LLAISYS_CHECK(flags == 0, "qwen2 step: kernels reported error flags " << flags);
+    std::memcpy(next, hnext, B * sizeof(int64_t));
+    last_B_ = B;
+    for (size_t i = 0; i < B; ++i) blocks_.commit(ids[i], int(ntokens[i]), tokens + cu[i]);
+}
+
+void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
+    auto &rt = core::context().runtime();
+    void *s = rt.stream();
+    const auto et = K::ElemType::BF16;
+    const int hs = int(cfg_.hs), di = int(cfg_.di);
+    const int q = int(cfg_.nh * cfg_.dh), kv = int(cfg_.nkvh * cfg_.dh);
+    const int M = int(T);
+    const float scale = 1.f / std::sqrt(float(cfg_.dh));
+
+    if (cow_)
+        for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], cow_);
+
+    K::embedding(x_->data(), i64(tok_), in_embed_->data(), et, T, int64_t(cfg_.voc), hs, rt.errorWord(), s);
+    const tensor_t q3 = rows(q_, T), k3 = rows(k_, T), v3 = rows(v_, T), a3 = rows(attn_, T);
+    for (size_t l = 0; l < cfg_.nlayer; ++l) {
+        const auto &L = layers_[l];
+        K::rmsNorm(h_->data(), x_->data(), L.attn_norm->data(), et, T, hs, cfg_.epsilon, s);
+        K::linear(qkv_->data(), h_->data(), L.qkv_w->data(), L.qkv_b->data(), et, M, q + 2 * kv, hs, s);
+        K::qkvRope(u16(q_), u16(k_), u16(v_), u16(qkv_), i64(pos_), T, int(cfg_.nh), int(cfg_.nkvh), int(cfg_.dh),
+                   cfg_.theta, s);
+        ops::pagedKVAppend(k_pool_[l], v_pool_[l], k3, v3, table_, ctx_before_, decode_only ? nullptr : cu_);
+        ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_, scale);
+        K::linear(x_->data(), attn_->data(), L.o_w->data(), nullptr, et, M, hs, q, s, true);
+        K::rmsNorm(h_->data(), x_->data(), L.mlp_norm->data(), et, T, hs, cfg_.epsilon, s);
+        K::linear(gu_->data(), h_->data(), L.gate_up_w->data(), nullptr, et, M, 2 * di, hs, s);
+        K::swigluRows(u16(act_), u16(gu_), T, di, s);
+        K::linear(x_->data(), act_->data(), L.down_w->data(), nullptr, et, M, hs, di, s, true);
+    }
+    K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);
+    K::linear(logits_->data(), hl_->data(), out_embed_->data(), nullptr, et, int(B), int(cfg_.voc), hs, s);
+    K::argmax(i64(next_), nullptr, logits_->data(), et, B, int64_t(cfg_.voc), s);
+}
+
+tensor_t Qwen2Model::lastLogits() const {
+    LLAISYS_CHECK(last_B_ > 0, "qwen2: no step has run yet");
+    return rows(logits_, last_B_);
+}
+
+int64_t Qwen2Model::infer(const int64_t *token_ids, size_t ntoken) {
+    LLAISYS_CHECK(token_ids && ntoken > 0, "qwen2 infer: no tokens");
+    const bool extends = have0_ && hist0_.size() < ntoken &&
+                         std::equal(hist0_.begin(), hist0_.end(), token_ids);
+    size_t start = hist0_.size();
+    if (!extends) {
+        if (have0_) blocks_.release(0);
+        have0_ = false;
+        hist0_.clear();
+        start = size_t(blocks_.create(0, token_ids, ntoken));
+        have0_ = true;
+        hist0_.assign(token_ids, token_ids + start);
+    }
+    const int64_t id = 0;
+    const size_t n = ntoken - start;
+    int64_t next = -1;
+    try {
+        step(&id, 1, token_ids + start, &n, &next);
+    } catch (...) {
+        // The sequence may hold reserved, uncommitted pages: start over next time.
+        blocks_.release(0);
+        have0_ = false;
+        hist0_.clear();
+        throw;
+    }
+    hist0_.assign(token_ids, token_ids + ntoken);
+    return next;
+}
+
+int64_t Qwen2Model::seqCreate(const int64_t *tokens, size_t ntokens, size_t *reused) {
+    const int64_t id = next_id_++;
+    const int r = blocks_.create(id, tokens, tokens ? ntokens : 0);
+    if (reused) *reused = size_t(r);
+    return id;
+}
+
+int64_t Qwen2Model::seqFork(int64_t parent) {
+    LLAISYS_CHECK(parent != 0, "qwen2: sequence 0 belongs to Infer");
+    const int64_t id = next_id_++;
+    blocks_.fork(parent, id);
+    return id;
+}
+
+void Qwen2Model::seqFree(int64_t id) {
+    LLAISYS_CHECK(id != 0, "qwen2: sequence 0 belongs to Infer");
+    blocks_.release(id);
+}
+
+size_t Qwen2Model::seqLength(int64_t id) const { return size_t(blocks_.length(id)); }
+
+} // namespace llaisys::models

@@ -1,0 +1,96 @@
+// Qwen2 decoder on the paged KV path (reference API: include/llaisys/models/
+// qwen2.h:7-40; the reference leaves the model unimplemented,
+// python/llaisys/models/qwen2.py:9-33).
+//
+// Layout choices:
+//  * q/k/v projections live in one fused [(nh + 2 nkvh) dh, hs] matrix and
+//    gate/up in one [2 di, hs] matrix; the reference's per-projection weight
+//    tensors are row slices of these, so loading them fills the fused ones and
+//    each layer runs one QKV GEMM and one gate-up GEMM;
+//  * the K/V cache is one paged pool pair per layer ([blocks, nkvh, 16, dh]
+//    bf16, the MI355X page format), shared by every sequence through a
+//    BlockManager (prefix cache, forks, copy-on-write);
+//  * a step is a varlen batch: each sequence appends n_i >= 1 tokens (prefill
+//    chunks and single-token decodes mix freely), and the LM head runs on each
+//    sequence's last position only.
+#pragma once
+
+#include "../kvcache/block_manager.hpp"
+#include "../tensor/tensor.hpp"
+
+#include <cstdint>
+#include <vector>
+
+namespace llaisys::models {
+
+struct Qwen2Config {
+    llaisysDataType_t dtype;
+    size_t nlayer, hs, nh, nkvh, dh, di, maxseq, voc;
+    float epsilon, theta;
+    int64_t end_token;
+};
+
+struct Qwen2LayerWeights {
+    tensor_t attn_norm, qkv_w, qkv_b, o_w, mlp_norm, gate_up_w, down_w;
+    // reference-named slices of the fused tensors
+    tensor_t q_w, k_w, v_w, q_b, k_b, v_b, gate_w, up_w;
+};
+
+class Qwen2Model {
+public:
+    Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks);
+    ~Qwen2Model();
+
+    const Qwen2Config &config() const { return cfg_; }
+    tensor_t inEmbed() const { return in_embed_; }
+    tensor_t outEmbed() const { return out_embed_; }
+    tensor_t outNorm() const { return out_norm_; }
+    const Qwen2LayerWeights &layer(size_t i) const { return layers_.at(i); }
+
+    // The reference's single-sequence Infer: token_ids is the whole token
+    // history. The KV cache of the previous call is kept when it is a prefix
+    // of token_ids (only the new tokens are computed); otherwise the sequence
+    // restarts, reusing cached full blocks of a matching prefix.
+    int64_t infer(const int64_t *token_ids, size_t ntoken);
+
+    // Sequences of the batched API. create() maps the cached prefix of tokens
+    // (may be null) and returns how many leading tokens it already covers.
+    int64_t seqCreate(const int64_t *tokens, size_t ntokens, size_t *reused);
+    int64_t seqFork(int64_t parent);
+    void seqFree(int64_t id);
+    size_t seqLength(int64_t id) const;
+    size_t numFreeBlocks() const { return size_t(blocks_.numFree()); }
+
+    // One step: sequence ids[i] appends ntokens[i] >= 1 tokens (concatenated
+    // in tokens); next[i] is the argmax of the logits at its last position.
+    void step(const int64_t *ids, size_t nseq, const int64_t *tokens, const size_t *ntokens, int64_t *next);
+
+    // Logits [nseq, voc] of the last step (a view of the step workspace).
+    tensor_t lastLogits() const;
+
+private:
+    void ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints64);
+    void forward(size_t T, size_t B, bool decode_only);
+
+    Qwen2Config cfg_;
+    int dev_;
+    size_t num_blocks_;
+    kvcache::BlockManager blocks_;
+    int64_t next_id_ = 1;
+    std::vector<int64_t> hist0_; // token history of the Infer sequence (id 0)
+    bool have0_ = false;
+
+    tensor_t in_embed_, out_embed_, out_norm_;
+    std::vector<Qwen2LayerWeights> layers_;
+    std::vector<tensor_t> k_pool_, v_pool_;
+
+    // step workspace (grow-only)
+    size_t cap_T_ = 0, cap_B_ = 0, cap_i32_ = 0, cap_i64_ = 0;
+    tensor_t x_, h_, qkv_, q_, k_, v_, attn_, gu_, act_, hl_, logits_, next_;
+    tensor_t dev_i32_, dev_i64_;     // per-step indices, uploaded in one copy each
+    core::storage_t host32_, host64_; // pinned staging of the same
+    tensor_t table_, ctx_before_, ctx_after_, cu_, cow_, tok_, pos_, last_; // views of dev_i32_/dev_i64_
+    size_t last_B_ = 0;
+};
+
+} // namespace llaisys::models

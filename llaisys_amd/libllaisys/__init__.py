@@ -20,6 +20,7 @@ from .llaisys_types import (
     llaisysStream_t,
 )
 from .kv_cache import load_kv_cache, llaisysKVBlockManager_t
+from .qwen2 import LlaisysQwen2Meta, LlaisysQwen2Weights, llaisysQwen2Model_t, load_qwen2
 from .ops import load_ops
 from .runtime import LlaisysRuntimeAPI, load_runtime
 from .tensor import llaisysTensor_t, load_tensor
@@ -69,6 +70,7 @@ load_runtime(LIB_LLAISYS)
 load_tensor(LIB_LLAISYS)
 load_ops(LIB_LLAISYS)
 load_kv_cache(LIB_LLAISYS)
+load_qwen2(LIB_LLAISYS)
 
 
 class LlaisysError(RuntimeError):
@@ -93,6 +95,9 @@ __all__ = [
     "llaisysStream_t",
     "llaisysTensor_t",
     "llaisysKVBlockManager_t",
+    "LlaisysQwen2Meta",
+    "LlaisysQwen2Weights",
+    "llaisysQwen2Model_t",
     "llaisysDataType_t",
     "DataType",
     "llaisysDeviceType_t",

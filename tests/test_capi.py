@@ -101,3 +101,11 @@ def test_one_hip_runtime_whatever_the_import_order():
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=str(ROOT))
     assert r.returncode == 0, r.stderr
     assert r.stdout.strip() == "1 1"
+
+
+def test_qwen2_create_rejects_cpu_and_non_bf16():
+    from llaisys_amd.models import Qwen2, Qwen2Meta
+
+    meta = Qwen2Meta(nlayer=1, hs=64, nh=2, nkvh=1, di=64, voc=32)
+    with pytest.raises(L.LlaisysError, match="AMD"):
+        Qwen2(meta=meta, device=L.DeviceType.CPU)

@@ -1,0 +1,179 @@
+"""The Qwen2 model C-API (include/llaisys/models/qwen2.h) on the AMD device
+against transformers' Qwen2ForCausalLM (the model the reference's
+test/test_infer.py:17-34 compares with), run in fp32 from the same bf16
+weights, on small random-init shapes (no checkpoint is available offline).
+
+Tolerance: logits within 3% of the reference logits' max magnitude (the
+library keeps activations in bf16 between kernels, as the reference's bf16
+model does); greedy tokens must agree wherever the reference's top-2 margin
+exceeds that tolerance."""
+import numpy as np
+import pytest
+import torch
+
+import llaisys_amd as L
+from llaisys_amd.models import Qwen2, Qwen2Meta
+from utils import to_torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+REL_TOL = 3e-2
+
+SHAPES = {
+    "tiny": dict(nlayer=2, hs=256, nh=4, nkvh=2, di=512, voc=1000),
+    "gqa12": dict(nlayer=1, hs=384, nh=12, nkvh=2, di=768, voc=777),
+}
+
+
+def build(shape, seed=0, num_blocks=0, maxseq=1024):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    s = SHAPES[shape]
+    meta = Qwen2Meta(**s, maxseq=maxseq, epsilon=1e-6, theta=10000.0, end_token=-1)
+    cfg = Qwen2Config(vocab_size=s["voc"], hidden_size=s["hs"], intermediate_size=s["di"],
+                      num_hidden_layers=s["nlayer"], num_attention_heads=s["nh"], num_key_value_heads=s["nkvh"],
+                      head_dim=128, max_position_embeddings=4096, rms_norm_eps=1e-6, rope_theta=10000.0,
+                      tie_word_embeddings=False, attn_implementation="eager")
+    torch.manual_seed(seed)
+    hf = Qwen2ForCausalLM(cfg)
+    with torch.no_grad():
+        for n, p in hf.named_parameters():
+            if n.endswith("norm.weight"):
+                p.copy_(1 + 0.1 * torch.randn_like(p))
+            else:
+                p.copy_(0.05 * torch.randn_like(p))
+            p.copy_(p.to(torch.bfloat16).float())  # the values both models hold
+    hf = hf.to(DEV).eval()
+    model = Qwen2(meta=meta, num_blocks=num_blocks)
+    params = dict(hf.named_parameters())
+    for name in model.weight_names():
+        t = params[name].detach().to(torch.bfloat16).cpu().contiguous()
+        model.load_weight(name, t.data_ptr())
+    return model, hf
+
+
+def hf_logits(hf, tokens):
+    with torch.no_grad():
+        out = hf(torch.tensor([tokens], device=DEV)).logits[0]
+    return out.float()
+
+
+def check_logits(got, ref):
+    got, ref = got.float(), ref.float()
+    tol = REL_TOL * ref.abs().max().item()
+    err = (got - ref).abs().max().item()
+    assert err <= tol, f"max |logit diff| {err:.4g} > {tol:.4g}"
+    return tol
+
+
+def check_token(tok, ref_row, tol):
+    best = int(ref_row.argmax())
+    if tok != best:
+        top2 = ref_row.topk(2).values
+        assert (ref_row[best] - ref_row[tok]).item() <= 2 * tol, f"token {tok} vs reference {best}"
+
+
+def prompt(n, voc, seed):
+    return np.random.default_rng(seed).integers(0, voc, n).tolist()
+
+
+@pytest.mark.parametrize("shape", list(SHAPES))
+def test_infer_prefill_then_decode_matches_transformers(shape):
+    model, hf = build(shape)
+    toks = prompt(37, model.meta.voc, 1)
+    for step in range(6):
+        nxt = model.infer(toks)
+        ref = hf_logits(hf, toks)[-1]
+        got = to_torch(model.logits())[0]
+        tol = check_logits(got, ref)
+        check_token(nxt, ref, tol)
+        assert nxt == int(got.float().argmax())
+        toks = toks + [int(ref.argmax())]  # teacher-forced on the reference's choice
+
+
+def test_infer_restarts_on_a_new_history_and_reuses_cached_blocks():
+    model, hf = build("tiny")
+    a = prompt(50, model.meta.voc, 2)
+    model.infer(a)
+    b = a[:40] + prompt(5, model.meta.voc, 3)  # shares 2 full blocks with a
+    model.infer(b)
+    check_logits(to_torch(model.logits())[0], hf_logits(hf, b)[-1])
+    model.infer(a)  # back to a: its blocks may have been reclaimed or reused
+    check_logits(to_torch(model.logits())[0], hf_logits(hf, a)[-1])
+
+
+def test_batched_mixed_steps_match_single_sequence_reference():
+    model, hf = build("tiny", num_blocks=256)
+    prompts = [prompt(n, model.meta.voc, 10 + n) for n in (1, 17, 33, 64)]
+    ids = [model.create_sequence()[0] for _ in prompts]
+    # step 1: three prompts prefill together, the fourth starts later
+    nxt = model.step(ids[:3], prompts[:3])
+    logits = to_torch(model.logits())
+    hist = {i: list(p) for i, p in zip(ids, prompts)}
+    for r, i in enumerate(ids[:3]):
+        ref = hf_logits(hf, hist[i])[-1]
+        check_token(nxt[r], ref, check_logits(logits[r], ref))
+        hist[i].append(nxt[r])
+    # steps 2..5: decodes of the first three mixed with the fourth's prefill chunks
+    chunks = [prompts[3][:30], prompts[3][30:31], prompts[3][31:]]
+    fourth = []
+    for s in range(4):
+        seqs = ids[:3] + ([ids[3]] if s < len(chunks) else [])
+        toks = [[hist[i][-1]] for i in ids[:3]] + ([chunks[s]] if s < len(chunks) else [])
+        nxt = model.step(seqs, toks)
+        logits = to_torch(model.logits())
+        if s < len(chunks):
+            fourth += chunks[s]
+        for r, i in enumerate(seqs):
+            h = hist[i] if r < 3 else fourth
+            ref = hf_logits(hf, h)[-1]
+            check_token(nxt[r], ref, check_logits(logits[r], ref))
+            if r < 3:
+                hist[i].append(nxt[r])
+    for i in ids[:3]:
+        assert model.length(i) == len(hist[i]) - 1
+    assert model.length(ids[3]) == 64
+
+
+def test_fork_copy_on_write_and_prefix_reuse():
+    model, hf = build("tiny", num_blocks=128)
+    p = prompt(40, model.meta.voc, 5)  # ends inside a block: forks share a partial tail
+    a, _ = model.create_sequence()
+    model.step([a], [p])
+    b = model.fork(a)
+    na, nb = model.step([a, b], [[7], [9]])
+    logits = to_torch(model.logits())
+    check_logits(logits[0], hf_logits(hf, p + [7])[-1])
+    check_logits(logits[1], hf_logits(hf, p + [9])[-1])
+    # a fresh sequence with the same prompt maps a's cached full blocks
+    c, reused = model.create_sequence(p + [7])
+    assert reused == 32
+    model.step([c], [(p + [7])[reused:]])
+    check_logits(to_torch(model.logits())[0], hf_logits(hf, p + [7])[-1])
+    for s in (a, b, c):
+        model.free(s)
+    assert model.num_free_blocks() == 128
+
+
+def test_step_errors_leave_the_model_usable():
+    model, hf = build("tiny", num_blocks=8)
+    s, _ = model.create_sequence()
+    with pytest.raises(L.LlaisysError, match="vocabulary"):
+        model.step([s], [[model.meta.voc]])
+    with pytest.raises(L.LlaisysError, match="out of blocks"):
+        model.step([s], [prompt(200, model.meta.voc, 6)])
+    model.free(s)
+    s, _ = model.create_sequence()
+    p = prompt(20, model.meta.voc, 7)
+    model.step([s], [p])
+    check_logits(to_torch(model.logits())[0], hf_logits(hf, p)[-1])
+
+
+def test_random_init_builds_on_gpu():
+    meta = Qwen2Meta(nlayer=2, hs=256, nh=4, nkvh=2, di=512, voc=1000, maxseq=256)
+    model = Qwen2.random(meta, seed=3, num_blocks=64)
+    ids = [model.create_sequence()[0] for _ in range(3)]
+    nxt = model.step(ids, [[1, 2, 3], [4], [5, 6]])
+    assert all(0 <= t < 1000 for t in nxt)
+    assert model.generate([1, 2, 3], max_new_tokens=4)[:3] == [1, 2, 3]
