@@ -39,9 +39,9 @@ SCALE = 1.0 / 128 ** 0.5
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy"])
+    p.add_argument("--steps", type=int, default=None, help="timed steps (default: 200; qwen2: 64)")
+    p.add_argument("--warmup", type=int, default=None, help="untimed steps (default: 20; qwen2: 4)")
+    p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy", "qwen2"])
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=0)
@@ -282,6 +282,87 @@ def run_mixed(args):
     }
 
 
+QWEN2_1_5B = dict(nlayer=28, hs=1536, nh=12, nkvh=2, di=8960, voc=151936, epsilon=1e-6, theta=10000.0)
+
+
+def qwen2_step_bytes(meta, ctx_total, B):
+    """Algorithmic HBM bytes of one batched decode step: every weight once
+    (the input embedding only for the B rows looked up), each layer's K/V of
+    every context token once, the new K/V written once; activations are
+    O(B * hidden) and left out."""
+    hs, q, kv, di, voc = meta.hs, meta.nh * meta.dh, meta.nkvh * meta.dh, meta.di, meta.voc
+    per_layer = 2 * ((q + 2 * kv) * hs + (q + 2 * kv) + hs * q + 2 * di * hs + hs * di + 2 * hs)
+    weights = meta.nlayer * per_layer + 2 * voc * hs + 2 * hs + 2 * B * hs
+    kv_bytes = meta.nlayer * 2 * kv * 2 * (ctx_total + B)
+    return weights + kv_bytes, weights, kv_bytes
+
+
+def run_qwen2(args):
+    """random-init Qwen2-1.5B shape, 128 sequences with a
+    2048-token paged context each (built by batched prefill steps through the
+    model), then greedy decode steps of the whole batch. One step = one
+    llaisysQwen2ModelStep (all 28 layers, LM head, argmax, next tokens back on
+    the host)."""
+    import numpy as np
+    import torch
+
+    from llaisys_amd.models import Qwen2, Qwen2Meta
+
+    B, ctx0 = 128, 2048
+    meta = Qwen2Meta(**QWEN2_1_5B, maxseq=ctx0 + args.warmup + args.steps + 16)
+    blocks = B * ((meta.maxseq + 15) // 16) + 16
+    t0 = time.perf_counter()
+    model = Qwen2.random(meta, seed=args.seed, std=0.02, num_blocks=blocks)
+    ids = np.array([model.create_sequence()[0] for _ in range(B)], np.int64)
+    prompts = np.random.default_rng(args.seed).integers(0, meta.voc, (B, ctx0), dtype=np.int64)
+    nxt = np.zeros(B, np.int64)
+    torch.cuda.synchronize()
+    t_init = time.perf_counter() - t0
+    chunk = 16  # sequences per prefill step: 32768 tokens
+    t0 = time.perf_counter()
+    for c in range(0, B, chunk):
+        out = np.zeros(chunk, np.int64)
+        model.step_arrays(ids[c:c + chunk], np.ascontiguousarray(prompts[c:c + chunk].reshape(-1)),
+                          np.full(chunk, ctx0, np.uint64), out)
+        nxt[c:c + chunk] = out
+    t_prefill = time.perf_counter() - t0
+    ones = np.ones(B, np.uint64)
+    cur = nxt.copy()
+
+    def step(_):
+        model.step_arrays(ids, cur, ones, nxt)
+        cur[:] = nxt
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ctx_start = int(sum(model.length(int(i)) for i in ids))
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # mean context over the timed steps (it grows by one token per step)
+    ctx_mean_total = ctx_start + B * (args.steps - 1) / 2
+    nbytes, wbytes, kvbytes = qwen2_step_bytes(meta, ctx_mean_total, B)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "paged decode attention achieved HBM GB/s (% of peak) + decode tokens/s, 1 GPU",
+        "value": round(B / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init bf16 weights ~ N(0,0.02), seeded random prompts)",
+        "config": {"workload": "BASELINE config 5: Qwen2-1.5B-shape greedy decode step", "batch": B,
+                   "context_at_start": ctx0, **QWEN2_1_5B, "head_dim": 128, "block_size": 16,
+                   "prefill_tokens_per_s": round(B * ctx0 / t_prefill, 1), "setup_s": round(t_init, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": int(nbytes), "weight_bytes": int(wbytes),
+                     "kv_bytes": int(kvbytes)},
+    }
+
+
 def run_append_gather(args):
     import numpy as np
     import torch
@@ -437,6 +518,9 @@ def traffic_from_profiles(kernel_tag):
 
 def main():
     args = parse()
+    small = args.workload == "qwen2"
+    args.steps = args.steps if args.steps is not None else (64 if small else 200)
+    args.warmup = args.warmup if args.warmup is not None else (4 if small else 20)
     if args.summarize:
         summarize(args)
         return
@@ -447,8 +531,8 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
-    line = {"decode": run_decode, "mixed": run_mixed, "append_gather": run_append_gather, "copy": run_copy}[
-        args.workload](args)
+    line = {"decode": run_decode, "mixed": run_mixed, "append_gather": run_append_gather, "copy": run_copy,
+            "qwen2": run_qwen2}[args.workload](args)
     print(json.dumps(line), flush=True)
 
 

@@ -68,13 +68,18 @@ constexpr int kMaxDims = 8;
 void add(void *c, const void *a, const void *b, ElemType t, size_t n, void *stream);
 void swiglu(void *out, const void *gate, const void *up, ElemType t, size_t n, void *stream);
 void addBias(void *x, const void *bias, ElemType t, size_t rows, size_t cols, void *stream);
+// x[r, c] = row[c] for every row r.
+void fillRows(void *x, const void *row, ElemType t, size_t rows, size_t cols, void *stream);
 void rmsNorm(void *out, const void *x, const void *w, ElemType t, size_t rows, int d, float eps, void *stream);
 void rope(void *out, const void *in, const int64_t *pos, ElemType t, size_t ntok, int nhead, int d, float theta,
           void *stream);
 void embedding(void *out, const int64_t *idx, const void *weight, ElemType t, size_t rows, int64_t vocab, int d,
                int *err, void *stream);
-// Row-wise argmax over the last dim: idx[rows] (first maximum), val[rows] (may be null).
-void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, int64_t n, void *stream);
+// Row-wise argmax over the last dim: idx[rows] (first maximum; NaN counts as
+// the largest value), val[rows] (may be null); workspace of argmaxWorkspaceBytes().
+size_t argmaxWorkspaceBytes(size_t rows, int64_t n);
+void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, int64_t n, void *workspace,
+            void *stream);
 void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *shape, const int64_t *out_strides,
                const int64_t *in_strides, void *stream);
 // Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]), row-major, fp32 accumulation.
@@ -83,10 +88,15 @@ void linear(void *y, const void *x, const void *w, const void *bias, ElemType t,
             bool accumulate = false);
 
 // ---- Qwen2 step glue (qwen2_step.hip), bf16
-// qkv [T, (nh + 2 nkvh) d] -> q [T, nh, d] and k [T, nkvh, d] rotated by pos, v [T, nkvh, d].
-void qkvRope(uint16_t *q, uint16_t *k, uint16_t *v, const uint16_t *qkv, const int64_t *pos, size_t T, int nh, int nkvh,
-             int d, float theta, void *stream);
-// act [T, di] = up * silu(gate) with gate_up rows [gate (di) | up (di)].
+// qkv [T, (nh + 2 nkvh) d] + bias -> q [T, nh, d] rotated by position, and k
+// (rotated) and v written
+// into the paged pool at each token's position (decode: cu == null, T == B;
+// else row r belongs to the sequence b with cu[b] <= r < cu[b+1]);
+// ctx = lengths before the append. Error bits 1 (bad block), 2 (past table).
+void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv, const uint16_t *bias,
+                   const int32_t *table, const int32_t *ctx, const int32_t *cu, int T, int B, int nh, int nkvh, int d,
+                   int max_pages, int num_blocks, float theta, int *err, void *stream);
+// act [T, di] = up * silu(gate) with gate_up rows [gate (di) | up (di)]; di % 8 == 0.
 void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *stream);
 // out [R, d] = rms_norm(x[rows[r]]) * w.
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,

@@ -52,12 +52,19 @@ void linear(void *y, const void *x, const void *w, const void *bias, ElemType t,
     if (M == 0 || N == 0) return;
     rocblas_handle h = handleFor();
     ROCBLAS_CHECK(rocblas_set_stream(h, static_cast<hipStream_t>(stream)));
-    const float alpha = 1.f, beta = accumulate ? 1.f : 0.f;
+    // The bias enters as C (Y preset to bias, beta = 1) so the result is rounded once.
+    if (bias) {
+        if (accumulate) {
+            addBias(y, bias, t, size_t(M), size_t(N), stream);
+        } else {
+            fillRows(y, bias, t, size_t(M), size_t(N), stream);
+        }
+    }
+    const float alpha = 1.f, beta = (accumulate || bias) ? 1.f : 0.f;
     const rocblas_datatype dt = typeOf(t);
     ROCBLAS_CHECK(rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &alpha, w, dt, K, x,
                                   dt, K, &beta, y, dt, N, y, dt, N, rocblas_datatype_f32_r, rocblas_gemm_algo_standard,
                                   0, 0));
-    if (bias) addBias(y, bias, t, size_t(M), size_t(N), stream);
 }
 
 } // namespace llaisys::kernels

@@ -50,6 +50,12 @@ template <typename T> __global__ void biasKernel(T *x, const T *bias, size_t row
         st(x, i, ld(x, i) + ld(bias, i % cols));
 }
 
+template <typename T> __global__ void fillRowsKernel(T *x, const T *row, size_t rows, size_t cols) {
+    const size_t n = rows * cols;
+    for (size_t i = blockIdx.x * size_t(kThreads) + threadIdx.x; i < n; i += size_t(gridDim.x) * kThreads)
+        x[i] = row[i % cols];
+}
+
 __device__ float blockSum(float v, float *red) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -62,7 +68,8 @@ __device__ float blockSum(float v, float *red) {
     return s;
 }
 
-// One block per row: y = x * w / sqrt(mean(x^2) + eps).
+// One block per row: y = x * w / sqrt(mean(x^2) + eps). Rows of 2-byte
+// elements with d % 8 == 0 move as 16 B vectors.
 template <typename T> __global__ void __launch_bounds__(kThreads) rmsNormKernel(T *out, const T *x, const T *w, int d, float eps) {
     __shared__ float red[kThreads / 64];
     const size_t row = blockIdx.x;
@@ -73,6 +80,43 @@ template <typename T> __global__ void __launch_bounds__(kThreads) rmsNormKernel(
     }
     const float inv = rsqrtf(blockSum(ss, red) / float(d) + eps);
     for (int c = threadIdx.x; c < d; c += kThreads) st(out, row * d + c, ld(x, row * d + c) * inv * ld(w, c));
+}
+
+template <typename T> __device__ __forceinline__ float half8(const uint4 &v, int e) {
+    const uint16_t h = uint16_t((&v.x)[e >> 1] >> ((e & 1) * 16));
+    return ld(reinterpret_cast<const T *>(&h), 0);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads) rmsNormVecKernel(T *out, const T *x, const T *w, int d, float eps) {
+    __shared__ float red[kThreads / 64];
+    const size_t row = blockIdx.x;
+    const uint4 *xr = reinterpret_cast<const uint4 *>(x + row * d);
+    const int nv = d / 8;
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < nv; c += kThreads) {
+        const uint4 v = xr[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = half8<T>(v, e);
+            ss += f * f;
+        }
+    }
+    const float inv = rsqrtf(blockSum(ss, red) / float(d) + eps);
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w);
+    uint4 *orow = reinterpret_cast<uint4 *>(out + row * d);
+    for (int c = threadIdx.x; c < nv; c += kThreads) {
+        const uint4 v = xr[c], g = wr[c];
+        uint4 o;
+        uint16_t *oh = reinterpret_cast<uint16_t *>(&o);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            T r;
+            st(&r, 0, half8<T>(v, e) * inv * half8<T>(g, e));
+            oh[e] = *reinterpret_cast<const uint16_t *>(&r);
+        }
+        orow[c] = o;
+    }
 }
 
 // Rotate halves: for j < d/2, phi = pos / theta^(2j/d) computed in fp32 as the
@@ -105,41 +149,62 @@ __global__ void embeddingKernel(T *out, const int64_t *idx, const T *weight, int
     for (int c = threadIdx.x; c < d; c += kThreads) out[r * d + c] = weight[size_t(i) * d + c];
 }
 
-// One block per row: the first index of the maximum (NaN compares false, as
-// a plain > scan would).
+// argmax over the last dim, split over columns: stage 1 reduces chunks of
+// kArgmaxChunk columns of one row to a 64-bit key, stage 2 reduces a row's
+// chunk keys. key = order-preserving bits of the value (NaN above +inf, as
+// torch.max propagates NaN) << 32 | ~column, so the maximum key is the
+// largest value at its first column.
+constexpr int kArgmaxChunk = 4096;
+
+__device__ __forceinline__ uint64_t argmaxKey(float v, int64_t col) {
+    uint32_t u = __float_as_uint(v);
+    if (v != v) u = 0x7fc00000u; // any NaN: the canonical positive NaN
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (uint64_t(ord) << 32) | uint32_t(~uint32_t(col));
+}
+
+__device__ __forceinline__ uint64_t waveMax(uint64_t k) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t o = __shfl_xor(k, off);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+// grid (chunks, rows): keys[row * chunks + chunk]
 template <typename T>
-__global__ void __launch_bounds__(kThreads) argmaxKernel(int64_t *idx, T *val, const T *vals, int64_t n) {
-    __shared__ float sv[kThreads];
-    __shared__ int64_t si[kThreads];
-    const size_t row = blockIdx.x;
-    float best = -INFINITY;
-    int64_t bi = -1;
-    for (int64_t c = threadIdx.x; c < n; c += kThreads) {
-        const float v = ld(vals, row * n + c);
-        if (bi < 0 || v > best) {
-            best = v;
-            bi = c;
-        }
+__global__ void __launch_bounds__(kThreads) argmaxChunkKernel(uint64_t *keys, const T *vals, int64_t n, int chunks) {
+    __shared__ uint64_t red[kThreads / 64];
+    const size_t row = blockIdx.y;
+    const int64_t c0 = int64_t(blockIdx.x) * kArgmaxChunk;
+    const int64_t c1 = min(n, c0 + kArgmaxChunk);
+    uint64_t best = 0;
+    for (int64_t c = c0 + threadIdx.x; c < c1; c += kThreads) {
+        const uint64_t k = argmaxKey(ld(vals, row * n + c), c);
+        best = k > best ? k : best;
     }
-    sv[threadIdx.x] = best;
-    si[threadIdx.x] = bi;
+    best = waveMax(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
     __syncthreads();
-    for (int s = kThreads / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            const float ov = sv[threadIdx.x + s];
-            const int64_t oi = si[threadIdx.x + s];
-            const float mv = sv[threadIdx.x];
-            const int64_t mi = si[threadIdx.x];
-            if (oi >= 0 && (mi < 0 || ov > mv || (ov == mv && oi < mi))) {
-                sv[threadIdx.x] = ov;
-                si[threadIdx.x] = oi;
-            }
-        }
-        __syncthreads();
-    }
     if (threadIdx.x == 0) {
-        idx[row] = si[0];
-        if (val) st(val, row, sv[0]);
+        for (int w = 1; w < kThreads / 64; ++w) best = red[w] > best ? red[w] : best;
+        keys[row * chunks + blockIdx.x] = best;
+    }
+}
+
+// one wave per row
+template <typename T>
+__global__ void __launch_bounds__(64) argmaxFinishKernel(int64_t *idx, T *val, const uint64_t *keys, const T *vals,
+                                                        int64_t n, int chunks) {
+    const size_t row = blockIdx.x;
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < chunks; c += 64) best = keys[row * chunks + c] > best ? keys[row * chunks + c] : best;
+    best = waveMax(best);
+    if (threadIdx.x == 0) {
+        const int64_t col = int64_t(~uint32_t(best & 0xffffffffu));
+        idx[row] = col;
+        if (val) val[row] = vals[row * n + col];
     }
 }
 
@@ -191,9 +256,21 @@ template <typename T> struct BiasL {
             hipLaunchKernelGGL(biasKernel<T>, dim3(gridFor(rows * cols)), dim3(kThreads), 0, s, (T *)x, (const T *)b, rows, cols);
     }
 };
+template <typename T> struct FillRowsL {
+    static void run(void *x, const void *r, size_t rows, size_t cols, hipStream_t s) {
+        if (rows * cols)
+            hipLaunchKernelGGL(fillRowsKernel<T>, dim3(gridFor(rows * cols)), dim3(kThreads), 0, s, (T *)x, (const T *)r, rows, cols);
+    }
+};
 template <typename T> struct RmsL {
     static void run(void *o, const void *x, const void *w, size_t rows, int d, float eps, hipStream_t s) {
-        if (rows) hipLaunchKernelGGL(rmsNormKernel<T>, dim3(rows), dim3(kThreads), 0, s, (T *)o, (const T *)x, (const T *)w, d, eps);
+        if (!rows) return;
+        const bool vec = sizeof(T) == 2 && d % 8 == 0 && (reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(x) |
+                                                          reinterpret_cast<uintptr_t>(w)) % 16 == 0;
+        if (vec)
+            hipLaunchKernelGGL(rmsNormVecKernel<T>, dim3(rows), dim3(kThreads), 0, s, (T *)o, (const T *)x, (const T *)w, d, eps);
+        else
+            hipLaunchKernelGGL(rmsNormKernel<T>, dim3(rows), dim3(kThreads), 0, s, (T *)o, (const T *)x, (const T *)w, d, eps);
     }
 };
 template <typename T> struct RopeL {
@@ -207,8 +284,11 @@ template <typename T> struct EmbL {
     }
 };
 template <typename T> struct ArgmaxL {
-    static void run(int64_t *idx, void *val, const void *vals, size_t rows, int64_t n, hipStream_t s) {
-        if (rows) hipLaunchKernelGGL(argmaxKernel<T>, dim3(rows), dim3(kThreads), 0, s, idx, (T *)val, (const T *)vals, n);
+    static void run(int64_t *idx, void *val, const void *vals, size_t rows, int64_t n, uint64_t *keys, hipStream_t s) {
+        if (!rows) return;
+        const int chunks = int((n + kArgmaxChunk - 1) / kArgmaxChunk);
+        hipLaunchKernelGGL(argmaxChunkKernel<T>, dim3(chunks, unsigned(rows)), dim3(kThreads), 0, s, keys, (const T *)vals, n, chunks);
+        hipLaunchKernelGGL(argmaxFinishKernel<T>, dim3(unsigned(rows)), dim3(64), 0, s, idx, (T *)val, keys, (const T *)vals, n, chunks);
     }
 };
 
@@ -226,6 +306,10 @@ void addBias(void *x, const void *bias, ElemType t, size_t rows, size_t cols, vo
     byType<BiasL>(t, x, bias, rows, cols, static_cast<hipStream_t>(stream));
     HIP_CHECK(hipGetLastError());
 }
+void fillRows(void *x, const void *row, ElemType t, size_t rows, size_t cols, void *stream) {
+    byType<FillRowsL>(t, x, row, rows, cols, static_cast<hipStream_t>(stream));
+    HIP_CHECK(hipGetLastError());
+}
 void rmsNorm(void *out, const void *x, const void *w, ElemType t, size_t rows, int d, float eps, void *stream) {
     byType<RmsL>(t, out, x, w, rows, d, eps, static_cast<hipStream_t>(stream));
     HIP_CHECK(hipGetLastError());
@@ -240,8 +324,12 @@ void embedding(void *out, const int64_t *idx, const void *weight, ElemType t, si
     byType<EmbL>(t, out, idx, weight, rows, vocab, d, err, static_cast<hipStream_t>(stream));
     HIP_CHECK(hipGetLastError());
 }
-void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, int64_t n, void *stream) {
-    byType<ArgmaxL>(t, idx, val, vals, rows, n, static_cast<hipStream_t>(stream));
+size_t argmaxWorkspaceBytes(size_t rows, int64_t n) {
+    return rows * size_t((n + kArgmaxChunk - 1) / kArgmaxChunk) * sizeof(uint64_t);
+}
+void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, int64_t n, void *workspace,
+            void *stream) {
+    byType<ArgmaxL>(t, idx, val, vals, rows, n, static_cast<uint64_t *>(workspace), static_cast<hipStream_t>(stream));
     HIP_CHECK(hipGetLastError());
 }
 void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *shape, const int64_t *out_strides,

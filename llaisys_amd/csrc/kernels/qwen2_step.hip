@@ -1,14 +1,17 @@
 // Fused glue kernels of the Qwen2 decode/prefill step (bf16 activations,
 // fp32 math, one rounding per output):
-//  * qkvRope: split the fused QKV projection rows into q [T, nh, d] and
-//    k/v [T, nkvh, d], rotating q and k by the token's position (the
-//    reference's rope formula, test/ops/rope.py:11-33);
+//  * qkvRopeAppend: split the fused QKV projection rows (plus bias) into q
+//    [T, nh, d] and k/v, rotating q and k by the token's position (the
+//    reference's rope formula, test/ops/rope.py:11-33), with k/v written
+//    straight into their slots of the paged pool (the append of paged_kv.hip
+//    fused in);
 //  * swigluRows: act = up * silu(gate) over fused [gate | up] rows
 //    (test/ops/swiglu.py:11-12);
 //  * rmsNormRows: rms_norm of selected rows only (the last position of each
 //    sequence before the LM head; test/ops/rms_norm.py:11-17).
 #include "launch.hpp"
 
+#include "../common.hpp"
 #include "../device/hip_check.hpp"
 
 #include <hip/hip_bf16.h>
@@ -24,36 +27,88 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ float f(bf16 v) { return __bfloat162float(v); }
 
-// One block per token. Rotation pairs (j, j + d/2), angle pos / theta^(2j/d).
-__global__ void __launch_bounds__(kThreads) qkvRopeKernel(bf16 *q, bf16 *k, bf16 *v, const bf16 *qkv, const int64_t *pos,
-                                                          int nh, int nkvh, int d, float theta) {
-    const size_t t = blockIdx.x;
+// 8 columns per thread (di % 8 == 0): 16 B loads of gate and up, one 16 B store.
+__global__ void swigluRowsKernel(bf16 *act, const bf16 *gu, size_t T, int di) {
+    const int nv = di / 8;
+    const size_t n = T * size_t(nv);
+    for (size_t i = blockIdx.x * size_t(kThreads) + threadIdx.x; i < n; i += size_t(gridDim.x) * kThreads) {
+        const size_t r = i / nv, c = i - r * nv;
+        const uint4 g = reinterpret_cast<const uint4 *>(gu + r * 2 * di)[c];
+        const uint4 u = reinterpret_cast<const uint4 *>(gu + r * 2 * di + di)[c];
+        uint4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t gw = (&g.x)[e], uw = (&u.x)[e];
+            const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
+            const float u0 = __uint_as_float(uw << 16), u1 = __uint_as_float(uw & 0xffff0000u);
+            const uint32_t lo = __builtin_bit_cast(uint16_t, __float2bfloat16(u0 * g0 / (1.f + expf(-g0))));
+            const uint32_t hi = __builtin_bit_cast(uint16_t, __float2bfloat16(u1 * g1 / (1.f + expf(-g1))));
+            (&o.x)[e] = lo | (hi << 16);
+        }
+        reinterpret_cast<uint4 *>(act + r * size_t(di))[c] = o;
+    }
+}
+
+__device__ __forceinline__ int kPageIndex(int t, int d) { return (d >> 3) * 128 + t * 8 + (d & 7); }
+__device__ __forceinline__ int vPageIndex(int t, int d) {
+    return (d >> 5) * 512 + (t >> 2) * 128 + (d & 15) * 8 + ((d >> 4) & 1) * 4 + (t & 3);
+}
+
+// One block per token row r of sequence b (cu: varlen offsets, else r == b),
+// position pos = ctx[b] + (r - cu[b]). Error bits as the append kernel: 1 bad
+// block id, 2 position past the block table.
+__global__ void __launch_bounds__(kThreads) qkvRopeAppendKernel(
+    bf16 *q, uint16_t *k_pool, uint16_t *v_pool, const bf16 *qkv, const bf16 *bias, const int32_t *table,
+    const int32_t *ctx, const int32_t *cu, int B, int nh, int nkvh, int d, int max_pages, int num_blocks, float theta,
+    int *err) {
+    const int r = blockIdx.x;
+    int b = r;
+    if (cu) {
+        int lo = 0, hi = B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (cu[mid] <= r) lo = mid; else hi = mid - 1;
+        }
+        b = lo;
+    }
+    const int pos = ctx[b] + (cu ? r - cu[b] : 0);
+    const int page = pos >> 4, slot = pos & 15;
+    bool ok = pos >= 0 && page < max_pages;
+    int blk = ok ? table[size_t(b) * max_pages + page] : -1;
+    if (!ok) {
+        if (threadIdx.x == 0) atomicOr(err, 2);
+    } else if (blk < 0 || blk >= num_blocks) {
+        if (threadIdx.x == 0) atomicOr(err, 1);
+        ok = false;
+    }
     const int half = d / 2;
     const int width = (nh + 2 * nkvh) * d;
-    const bf16 *row = qkv + t * size_t(width);
-    const float p = float(pos[t]);
-    // rotated heads: nh query heads then nkvh key heads, half-pairs each
+    const bf16 *row = qkv + size_t(r) * width;
+    const float p = float(pos);
     for (int i = threadIdx.x; i < (nh + nkvh) * half; i += kThreads) {
         const int h = i / half, j = i - h * half;
         const float phi = p / powf(theta, float(2 * j) / float(d));
-        float s, c;
-        sincosf(phi, &s, &c);
-        const bf16 *src = row + h * d;
-        const float a = f(src[j]), b = f(src[j + half]);
-        bf16 *dst = h < nh ? q + (t * nh + h) * size_t(d) : k + (t * nkvh + (h - nh)) * size_t(d);
-        dst[j] = __float2bfloat16(a * c - b * s);
-        dst[j + half] = __float2bfloat16(b * c + a * s);
+        float sn, cs;
+        sincosf(phi, &sn, &cs);
+        const int c = h * d + j;
+        const float a = f(row[c]) + f(bias[c]), bb = f(row[c + half]) + f(bias[c + half]);
+        const bf16 ra = __float2bfloat16(a * cs - bb * sn), rb = __float2bfloat16(bb * cs + a * sn);
+        if (h < nh) {
+            bf16 *dst = q + (size_t(r) * nh + h) * d;
+            dst[j] = ra;
+            dst[j + half] = rb;
+        } else if (ok) {
+            uint16_t *pg = k_pool + (size_t(blk) * nkvh + (h - nh)) * kPageElems;
+            pg[kPageIndex(slot, j)] = __builtin_bit_cast(uint16_t, ra);
+            pg[kPageIndex(slot, j + half)] = __builtin_bit_cast(uint16_t, rb);
+        }
     }
-    const bf16 *vsrc = row + (nh + nkvh) * d;
-    for (int i = threadIdx.x; i < nkvh * d; i += kThreads) v[t * size_t(nkvh) * d + i] = vsrc[i];
-}
-
-__global__ void swigluRowsKernel(bf16 *act, const bf16 *gu, size_t T, int di) {
-    const size_t n = T * size_t(di);
-    for (size_t i = blockIdx.x * size_t(kThreads) + threadIdx.x; i < n; i += size_t(gridDim.x) * kThreads) {
-        const size_t r = i / di, c = i - r * di;
-        const float g = f(gu[r * 2 * di + c]), u = f(gu[r * 2 * di + di + c]);
-        act[i] = __float2bfloat16(u * g / (1.f + expf(-g)));
+    if (!ok) return;
+    for (int i = threadIdx.x; i < nkvh * d; i += kThreads) {
+        const int h = i / d, dd = i - h * d;
+        const int c = (nh + nkvh) * d + i;
+        const bf16 v = __float2bfloat16(f(row[c]) + f(bias[c]));
+        v_pool[(size_t(blk) * nkvh + h) * kPageElems + vPageIndex(slot, dd)] = __builtin_bit_cast(uint16_t, v);
     }
 }
 
@@ -76,17 +131,20 @@ __global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(bf16 *out, const b
 
 } // namespace
 
-void qkvRope(uint16_t *q, uint16_t *k, uint16_t *v, const uint16_t *qkv, const int64_t *pos, size_t T, int nh, int nkvh,
-             int d, float theta, void *stream) {
+void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv, const uint16_t *bias,
+                   const int32_t *table, const int32_t *ctx, const int32_t *cu, int T, int B, int nh, int nkvh, int d,
+                   int max_pages, int num_blocks, float theta, int *err, void *stream) {
     if (!T) return;
-    hipLaunchKernelGGL(qkvRopeKernel, dim3(unsigned(T)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                       reinterpret_cast<bf16 *>(q), reinterpret_cast<bf16 *>(k), reinterpret_cast<bf16 *>(v),
-                       reinterpret_cast<const bf16 *>(qkv), pos, nh, nkvh, d, theta);
+    hipLaunchKernelGGL(qkvRopeAppendKernel, dim3(unsigned(T)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<bf16 *>(q), k_pool, v_pool, reinterpret_cast<const bf16 *>(qkv),
+                       reinterpret_cast<const bf16 *>(bias), table, ctx, cu, B, nh, nkvh, d, max_pages, num_blocks,
+                       theta, err);
     HIP_CHECK(hipGetLastError());
 }
 
 void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *stream) {
-    const size_t n = T * size_t(di);
+    LLAISYS_CHECK(di % 8 == 0, "swigluRows: di must be a multiple of 8, got " << di);
+    const size_t n = T * size_t(di / 8);
     if (!n) return;
     const unsigned grid = unsigned(std::min<size_t>((n + kThreads - 1) / kThreads, 65536));
     hipLaunchKernelGGL(swigluRowsKernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),

@@ -1,7 +1,7 @@
 // Qwen2 decoder step over the paged KV cache. Per layer, for the T new tokens
 // of a step (hf Qwen2DecoderLayer order):
-//   h = rms_norm(x) ; qkv = h Wqkv^T + b ; q,k = rope(q,k), v
-//   append k,v into the layer's pages ; a = paged_attention(q)
+//   h = rms_norm(x) ; qkv = h Wqkv^T ; q,k = rope(q+bq, k+bk), v+bv
+//   k,v written into the layer's pages (same kernel) ; a = paged_attention(q)
 //   x += a Wo^T                      (residual folded into the GEMM)
 //   h = rms_norm(x) ; gu = h [Wg;Wu]^T ; act = up * silu(gate)
 //   x += act Wd^T
@@ -28,7 +28,15 @@ tensor_t dev(std::vector<size_t> shape, llaisysDataType_t dt, int id) {
 }
 uint16_t *u16(const tensor_t &t) { return reinterpret_cast<uint16_t *>(t->data()); }
 int64_t *i64(const tensor_t &t) { return reinterpret_cast<int64_t *>(t->data()); }
+int32_t *i32(const tensor_t &t) { return reinterpret_cast<int32_t *>(t->data()); }
 tensor_t rows(const tensor_t &t, size_t n) { return t->slice(0, 0, n); }
+
+// Y[M, N] = X W^T (+ bias) (+ Y) through the library GEMM.
+void gemm(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &bias, int M, int N, int K,
+          bool accumulate, void *s) {
+    K::linear(y->data(), x->data(), w->data(), bias ? bias->data() : nullptr, K::ElemType::BF16, M, N, K, s,
+              accumulate);
+}
 
 } // namespace
 
@@ -39,6 +47,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     LLAISYS_CHECK(cfg.nlayer > 0 && cfg.hs > 0 && cfg.nh > 0 && cfg.nkvh > 0 && cfg.di > 0 && cfg.voc > 0,
                   "qwen2: meta sizes must be positive");
     LLAISYS_CHECK(cfg.nh % cfg.nkvh == 0 && cfg.nh / cfg.nkvh <= 16, "qwen2: need nh % nkvh == 0, nh / nkvh <= 16");
+    LLAISYS_CHECK(cfg.di % 8 == 0 && cfg.hs % 8 == 0, "qwen2: hs and di must be multiples of 8");
     LLAISYS_CHECK(num_blocks > 0 && num_blocks < (size_t(1) << 31), "qwen2: bad KV block count " << num_blocks);
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     const auto dt = cfg.dtype;
@@ -83,8 +92,6 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
         h_ = dev({cap, cfg_.hs}, dt, dev_);
         qkv_ = dev({cap, q + 2 * kv}, dt, dev_);
         q_ = dev({cap, cfg_.nh, cfg_.dh}, dt, dev_);
-        k_ = dev({cap, cfg_.nkvh, cfg_.dh}, dt, dev_);
-        v_ = dev({cap, cfg_.nkvh, cfg_.dh}, dt, dev_);
         attn_ = dev({cap, cfg_.nh, cfg_.dh}, dt, dev_);
         gu_ = dev({cap, 2 * cfg_.di}, dt, dev_);
         act_ = dev({cap, cfg_.di}, dt, dev_);
@@ -154,7 +161,7 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     const size_t max_pages = size_t(std::max(1, blocks_.buildTable(ids, B, nullptr, 0, nullptr)));
     const size_t ncow = cow.size() / 2;
     const size_t n32 = B * max_pages + 3 * B + 1 + cow.size();
-    const size_t n64 = 2 * T + B;
+    const size_t n64 = T + B;
     ensureWorkspace(T, B, n32, n64);
 
     // int32 staging: table | ctx_before | ctx_after | cu | cow pairs
@@ -169,13 +176,10 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
         cu[i + 1] = cu[i] + int32_t(ntokens[i]);
     }
     std::copy(cow.begin(), cow.end(), cu + B + 1);
-    // int64 staging: tokens | positions | last rows
+    // int64 staging: tokens | last row of each sequence
     int64_t *h64 = reinterpret_cast<int64_t *>(host64_->memory());
     std::memcpy(h64, tokens, T * sizeof(int64_t));
-    for (size_t i = 0; i < B; ++i) {
-        for (size_t j = 0; j < ntokens[i]; ++j) h64[T + cu[i] + j] = before[i] + int64_t(j);
-        h64[2 * T + i] = cu[i + 1] - 1;
-    }
+    for (size_t i = 0; i < B; ++i) h64[T + i] = cu[i + 1] - 1;
     auto *api = rt.api();
     api->memcpy_async(dev_i32_->data(), h32, n32 * sizeof(int32_t), LLAISYS_MEMCPY_H2D, rt.stream());
     api->memcpy_async(dev_i64_->data(), h64, n64 * sizeof(int64_t), LLAISYS_MEMCPY_H2D, rt.stream());
@@ -186,8 +190,7 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     cu_ = dev_i32_->slice(0, B * max_pages + 2 * B, B * max_pages + 3 * B + 1);
     cow_ = ncow ? dev_i32_->slice(0, B * max_pages + 3 * B + 1, n32)->view({ncow, 2}) : nullptr;
     tok_ = dev_i64_->slice(0, 0, T);
-    pos_ = dev_i64_->slice(0, T, 2 * T);
-    last_ = dev_i64_->slice(0, 2 * T, 2 * T + B);
+    last_ = dev_i64_->slice(0, T, T + B);
 
     bool decode_only = T == B;
     forward(T, B, decode_only);
@@ -216,24 +219,25 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
         for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], cow_);
 
     K::embedding(x_->data(), i64(tok_), in_embed_->data(), et, T, int64_t(cfg_.voc), hs, rt.errorWord(), s);
-    const tensor_t q3 = rows(q_, T), k3 = rows(k_, T), v3 = rows(v_, T), a3 = rows(attn_, T);
+    const tensor_t q3 = rows(q_, T), a3 = rows(attn_, T);
     for (size_t l = 0; l < cfg_.nlayer; ++l) {
         const auto &L = layers_[l];
         K::rmsNorm(h_->data(), x_->data(), L.attn_norm->data(), et, T, hs, cfg_.epsilon, s);
-        K::linear(qkv_->data(), h_->data(), L.qkv_w->data(), L.qkv_b->data(), et, M, q + 2 * kv, hs, s);
-        K::qkvRope(u16(q_), u16(k_), u16(v_), u16(qkv_), i64(pos_), T, int(cfg_.nh), int(cfg_.nkvh), int(cfg_.dh),
-                   cfg_.theta, s);
-        ops::pagedKVAppend(k_pool_[l], v_pool_[l], k3, v3, table_, ctx_before_, decode_only ? nullptr : cu_);
+        gemm(qkv_, h_, L.qkv_w, nullptr, M, q + 2 * kv, hs, false, s);
+        K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
+                         i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh), int(cfg_.nkvh),
+                         int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), s);
         ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_, scale);
-        K::linear(x_->data(), attn_->data(), L.o_w->data(), nullptr, et, M, hs, q, s, true);
+        gemm(x_, attn_, L.o_w, nullptr, M, hs, q, true, s);
         K::rmsNorm(h_->data(), x_->data(), L.mlp_norm->data(), et, T, hs, cfg_.epsilon, s);
-        K::linear(gu_->data(), h_->data(), L.gate_up_w->data(), nullptr, et, M, 2 * di, hs, s);
+        gemm(gu_, h_, L.gate_up_w, nullptr, M, 2 * di, hs, false, s);
         K::swigluRows(u16(act_), u16(gu_), T, di, s);
-        K::linear(x_->data(), act_->data(), L.down_w->data(), nullptr, et, M, hs, di, s, true);
+        gemm(x_, act_, L.down_w, nullptr, M, hs, di, true, s);
     }
     K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);
-    K::linear(logits_->data(), hl_->data(), out_embed_->data(), nullptr, et, int(B), int(cfg_.voc), hs, s);
-    K::argmax(i64(next_), nullptr, logits_->data(), et, B, int64_t(cfg_.voc), s);
+    gemm(logits_, hl_, out_embed_, nullptr, int(B), int(cfg_.voc), hs, false, s);
+    K::argmax(i64(next_), nullptr, logits_->data(), et, B, int64_t(cfg_.voc),
+              rt.scratch(K::argmaxWorkspaceBytes(B, int64_t(cfg_.voc))), s);
 }
 
 tensor_t Qwen2Model::lastLogits() const {

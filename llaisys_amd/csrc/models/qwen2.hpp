@@ -86,10 +86,10 @@ private:
 
     // step workspace (grow-only)
     size_t cap_T_ = 0, cap_B_ = 0, cap_i32_ = 0, cap_i64_ = 0;
-    tensor_t x_, h_, qkv_, q_, k_, v_, attn_, gu_, act_, hl_, logits_, next_;
+    tensor_t x_, h_, qkv_, q_, attn_, gu_, act_, hl_, logits_, next_;
     tensor_t dev_i32_, dev_i64_;     // per-step indices, uploaded in one copy each
     core::storage_t host32_, host64_; // pinned staging of the same
-    tensor_t table_, ctx_before_, ctx_after_, cu_, cow_, tok_, pos_, last_; // views of dev_i32_/dev_i64_
+    tensor_t table_, ctx_before_, ctx_after_, cu_, cow_, tok_, last_; // views of dev_i32_/dev_i64_
     size_t last_B_ = 0;
 };
 

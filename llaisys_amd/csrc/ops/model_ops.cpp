@@ -74,8 +74,9 @@ void argmax(const tensor_t &max_idx, const tensor_t &max_val, const tensor_t &va
                       op << ": max_val must match vals' dtype with one element per row");
     }
     onAmd(op, {&max_idx, &max_val, &vals});
+    void *ws = core::context().runtime().scratch(K::argmaxWorkspaceBytes(rows, int64_t(n)));
     K::argmax(reinterpret_cast<int64_t *>(max_idx->data()), max_val ? max_val->data() : nullptr, vals->data(),
-              floatType(vals, op), rows, int64_t(n), stream());
+              floatType(vals, op), rows, int64_t(n), ws, stream());
 }
 
 void embedding(const tensor_t &out, const tensor_t &index, const tensor_t &weight) {

@@ -166,3 +166,25 @@ def test_model_ops_reject_cpu_tensors():
     a = L.Tensor((4,), dtype=DataType.F32, device=DeviceType.CPU)
     with pytest.raises(L.LlaisysError, match="AMD device"):
         L.Ops.add(a, a, a)
+
+
+SKINNY = [(1, 1, 64), (3, 7, 64), (5, 15, 128), (16, 16, 192), (17, 33, 1536), (64, 2048, 1536), (100, 1536, 8960),
+          (128, 17920, 1536), (128, 2049, 192), (128, 151936, 128), (128, 1536, 8960), (2, 3, 8), (128, 100, 264)]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY, ids=[f"{m}x{n}x{k}" for m, n, k in SKINNY])
+@pytest.mark.parametrize("use_bias", [True, False])
+def test_linear_bf16_decode_batches(M, N, K, use_bias):
+    # Decode-sized batches: fp32 sums of exact bf16 products, bias entering
+    # before the single rounding to bf16.
+    x, w = rnd((M, K), torch.bfloat16, 0.5, seed=M + K), rnd((N, K), torch.bfloat16, 0.05, seed=N)
+    b = rnd((N,), torch.bfloat16, seed=17) if use_bias else None
+    out = to_llaisys(torch.zeros(M, N, dtype=torch.bfloat16, device=DEV))
+    L.Ops.linear(out, to_llaisys(x), to_llaisys(w), to_llaisys(b) if use_bias else None)
+    ref = x.double() @ w.double().T
+    if use_bias:
+        ref += b.double()
+    got = to_torch(out).double()
+    # one bf16 rounding (2^-9 relative) plus fp32 accumulation of K products
+    bound = ref.abs() * 2.0 ** -8 + 1e-6 * (x.double().abs() @ w.double().abs().T) * K ** 0.5 + 1e-30
+    assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
