@@ -5,7 +5,7 @@ llaisys_amd/_build/ and links llaisys_amd/libllaisys/libllaisys.so, the
 library the ctypes layer loads (the reference loads libllaisys.so from its
 package dir the same way, python/llaisys/libllaisys/__init__.py:17-40).
 
-Run: python -m llaisys_amd.build   (or __graft_entry__.build()).
+Run: python llaisys_amd/build.py   (or __graft_entry__.build()).
 """
 from __future__ import annotations
 

@@ -7,7 +7,7 @@
 //    fused in);
 //  * swigluRows: act = up * silu(gate) over fused [gate | up] rows
 //    (test/ops/swiglu.py:11-12);
-//  * rmsNormRows: rms_norm of selected rows only (the last position of each
+//  * rmsNormRows: rms_norm of all or selected rows (the last position of each
 //    sequence before the LM head; test/ops/rms_norm.py:11-17).
 #include "launch.hpp"
 
@@ -45,7 +45,7 @@ __global__ void swigluRowsKernel(bf16 *act, const bf16 *gu, size_t T, int di) {
             const uint32_t hi = __builtin_bit_cast(uint16_t, __float2bfloat16(u1 * g1 / (1.f + expf(-g1))));
             (&o.x)[e] = lo | (hi << 16);
         }
-        reinterpret_cast<uint4 *>(act + r * size_t(di))[c] = o;
+        reinterpret_cast<uint4 *>(act)[r * nv + c] = o;
     }
 }
 
@@ -112,12 +112,24 @@ __global__ void __launch_bounds__(kThreads) qkvRopeAppendKernel(
     }
 }
 
-__global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(bf16 *out, const bf16 *x, const int64_t *rows, const bf16 *w,
-                                                              int d, float eps) {
+// One block per output row r (source row rows[r], or r), 8 columns per thread-step.
+__global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(uint16_t *out, const bf16 *x, const int64_t *rows,
+                                                              const bf16 *w, int d, float eps) {
     __shared__ float red[kThreads / 64];
-    const bf16 *src = x + size_t(rows[blockIdx.x]) * d;
+    const int r = blockIdx.x;
+    const uint4 *src = reinterpret_cast<const uint4 *>(x + size_t(rows ? rows[r] : r) * d);
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w);
+    const int nv = d / 8;
     float ss = 0.f;
-    for (int c = threadIdx.x; c < d; c += kThreads) ss += f(src[c]) * f(src[c]);
+    for (int c = threadIdx.x; c < nv; c += kThreads) {
+        const uint4 v = src[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t u = (&v.x)[e];
+            const float lo = __uint_as_float(u << 16), hi = __uint_as_float(u & 0xffff0000u);
+            ss += lo * lo + hi * hi;
+        }
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
@@ -125,8 +137,20 @@ __global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(bf16 *out, const b
     float tot = 0.f;
     for (int i = 0; i < kThreads / 64; ++i) tot += red[i];
     const float inv = rsqrtf(tot / float(d) + eps);
-    for (int c = threadIdx.x; c < d; c += kThreads)
-        out[size_t(blockIdx.x) * d + c] = __float2bfloat16(f(src[c]) * inv * f(w[c]));
+    for (int c = threadIdx.x; c < nv; c += kThreads) {
+        const uint4 v = src[c], g = wr[c];
+        uint4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t u = (&v.x)[e], gw = (&g.x)[e];
+            const uint32_t lo = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(u << 16) * inv *
+                                                                               __uint_as_float(gw << 16)));
+            const uint32_t hi = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(u & 0xffff0000u) * inv *
+                                                                               __uint_as_float(gw & 0xffff0000u)));
+            (&o.x)[e] = lo | (hi << 16);
+        }
+        reinterpret_cast<uint4 *>(out)[size_t(r) * nv + c] = o;
+    }
 }
 
 } // namespace
@@ -154,10 +178,10 @@ void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *
 
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
                  void *stream) {
+    LLAISYS_CHECK(d % 8 == 0, "rmsNormRows: d must be a multiple of 8, got " << d);
     if (!R) return;
-    hipLaunchKernelGGL(rmsNormRowsKernel, dim3(unsigned(R)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                       reinterpret_cast<bf16 *>(out), reinterpret_cast<const bf16 *>(x), rows,
-                       reinterpret_cast<const bf16 *>(w), d, eps);
+    hipLaunchKernelGGL(rmsNormRowsKernel, dim3(unsigned(R)), dim3(kThreads), 0, static_cast<hipStream_t>(stream), out,
+                       reinterpret_cast<const bf16 *>(x), rows, reinterpret_cast<const bf16 *>(w), d, eps);
     HIP_CHECK(hipGetLastError());
 }
 

@@ -222,14 +222,14 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     const tensor_t q3 = rows(q_, T), a3 = rows(attn_, T);
     for (size_t l = 0; l < cfg_.nlayer; ++l) {
         const auto &L = layers_[l];
-        K::rmsNorm(h_->data(), x_->data(), L.attn_norm->data(), et, T, hs, cfg_.epsilon, s);
+        K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
         gemm(qkv_, h_, L.qkv_w, nullptr, M, q + 2 * kv, hs, false, s);
         K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
                          i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh), int(cfg_.nkvh),
                          int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), s);
         ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_, scale);
         gemm(x_, attn_, L.o_w, nullptr, M, hs, q, true, s);
-        K::rmsNorm(h_->data(), x_->data(), L.mlp_norm->data(), et, T, hs, cfg_.epsilon, s);
+        K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
         gemm(gu_, h_, L.gate_up_w, nullptr, M, 2 * di, hs, false, s);
         K::swigluRows(u16(act_), u16(gu_), T, di, s);
         gemm(x_, act_, L.down_w, nullptr, M, hs, di, true, s);

@@ -58,7 +58,7 @@ def load_shared_library():
         raise RuntimeError("llaisys_amd targets Linux with ROCm only")
     if not LIB_PATH.is_file():
         raise FileNotFoundError(
-            f"{LIB_PATH} is missing: build it with `python -m llaisys_amd.build` "
+            f"{LIB_PATH} is missing: build it with `python llaisys_amd/build.py` "
             "(the HIP kernels have no fallback)"
         )
     _share_hip_runtime()

@@ -23,6 +23,8 @@ REL_TOL = 3e-2
 SHAPES = {
     "tiny": dict(nlayer=2, hs=256, nh=4, nkvh=2, di=512, voc=1000),
     "gqa12": dict(nlayer=1, hs=384, nh=12, nkvh=2, di=768, voc=777),
+    # vocab >= 16384: the LM head runs the 8-wave decode GEMM
+    "widehead": dict(nlayer=1, hs=256, nh=2, nkvh=1, di=384, voc=20000),
 }
 
 
@@ -80,6 +82,7 @@ def prompt(n, voc, seed):
 
 @pytest.mark.parametrize("shape", list(SHAPES))
 def test_infer_prefill_then_decode_matches_transformers(shape):
+    # 37-token prefill and 1-token decodes: the packed decode GEMMs (mt 1, 4)
     model, hf = build(shape)
     toks = prompt(37, model.meta.voc, 1)
     for step in range(6):
@@ -90,6 +93,33 @@ def test_infer_prefill_then_decode_matches_transformers(shape):
         check_token(nxt, ref, tol)
         assert nxt == int(got.float().argmax())
         toks = toks + [int(ref.argmax())]  # teacher-forced on the reference's choice
+
+
+def test_long_prefill_uses_library_gemm_and_matches():
+    # 150 tokens in one step: the row-major library GEMM path; then decodes.
+    model, hf = build("tiny")
+    toks = prompt(150, model.meta.voc, 21)
+    for _ in range(3):
+        nxt = model.infer(toks)
+        ref = hf_logits(hf, toks)[-1]
+        check_token(nxt, ref, check_logits(to_torch(model.logits())[0], ref))
+        toks = toks + [int(ref.argmax())]
+
+
+@pytest.mark.parametrize("nseq", [100, 130])
+def test_wide_decode_batches_match(nseq):
+    # 100 sequences: packed GEMMs with 8 row tiles; 130: the LM head (and the
+    # layers) back on the library GEMM.
+    model, hf = build("tiny", num_blocks=nseq * 2 + 8)
+    prompts = [prompt(3 + (i % 5), model.meta.voc, 100 + i) for i in range(nseq)]
+    ids = [model.create_sequence()[0] for _ in prompts]
+    nxt = model.step(ids, prompts)
+    hist = [p + [t] for p, t in zip(prompts, nxt)]
+    nxt = model.step(ids, [[h[-1]] for h in hist])
+    logits = to_torch(model.logits())
+    for r in range(0, nseq, 9):
+        ref = hf_logits(hf, hist[r])[-1]
+        check_token(nxt[r], ref, check_logits(logits[r], ref))
 
 
 def test_infer_restarts_on_a_new_history_and_reuses_cached_blocks():
