@@ -12,13 +12,15 @@ finds the previous step's KV in the 256 MB MALL.
 
 Printed (rank 0, one JSON line): the metric of BASELINE.json = achieved HBM
 GB/s of the attention kernel (algorithmic bytes / average kernel time from HIP
-events on the stream the kernel runs on), with tokens/s, the roofline
-fraction against 8 TB/s and a CPU baseline (the C oracle on host cores, a
-bounded sample of the same workload).
+events on the stream the kernel runs on), with the roofline fraction against
+8 TB/s, a CPU baseline (the C oracle on host cores, a bounded sample of the
+same workload) and, as "decode_tokens_per_s", the other half of the metric:
+greedy decode of the whole random-init Qwen2-1.5B-shape model (config 5,
+batch 128 x 2048-token paged contexts; --no-model skips it).
 
 Other workloads (parity configs, for measurement): --workload append_gather
-(config 2), mixed (config 4), copy (plain device copy, for rocprof counter
-calibration).
+(config 2), mixed (config 4), qwen2 (config 5 alone: value = tokens/s), copy
+(plain device copy, for rocprof counter calibration).
 """
 from __future__ import annotations
 
@@ -44,11 +46,17 @@ def parse():
     p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy", "qwen2"])
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-model", action="store_true",
+                   help="decode workload only: skip the Qwen2 config-5 tokens/s measurement")
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--summarize", nargs=6, metavar=("STATS", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE", "TAG"),
                    help="summarise rocprofv3 output directories into profiles/TAG.md and profiles/TAG_traffic.json")
-    p.add_argument("--profiled-args", default="--no-cpu --steps 200", help="bench arguments of the kernel-trace run")
-    p.add_argument("--pmc-args", default="--no-cpu --steps 20 --warmup 5", help="bench arguments of the PMC runs")
+    p.add_argument("--summarize-step", nargs=2, metavar=("TRACE_DIR", "TAG"),
+                   help="per-step kernel table of a --workload qwen2 kernel trace into profiles/TAG.md")
+    p.add_argument("--profiled-args", default="--no-cpu --no-model --steps 200",
+                   help="bench arguments of the kernel-trace run")
+    p.add_argument("--pmc-args", default="--no-cpu --no-model --steps 20 --warmup 5",
+                   help="bench arguments of the PMC runs")
     return p.parse_args()
 
 
@@ -250,6 +258,18 @@ def run_decode(args):
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode(insts[0], args.cpu_seconds)
+    if not args.no_model:
+        # The "+ decode tokens/s" half of the metric: config 5 on the same GPU.
+        del insts
+        torch.cuda.empty_cache()
+        margs = argparse.Namespace(**vars(args))
+        margs.steps, margs.warmup = 64, 4
+        m = run_qwen2(margs)
+        line["decode_tokens_per_s"] = m["value"]
+        line["model"] = {"workload": m["config"]["workload"], "tokens_per_s": m["value"],
+                         "ms_per_step": m["ms_per_step"], "steps": m["steps"], "warmup": m["warmup"],
+                         "batch": m["config"]["batch"], "context_at_start": m["config"]["context_at_start"],
+                         "prefill_tokens_per_s": m["config"]["prefill_tokens_per_s"], "roofline": m["roofline"]}
     return line
 
 
@@ -505,6 +525,61 @@ def summarize(args):
     (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
 
 
+def summarize_step(args):
+    """Per-step kernel table of a --workload qwen2 kernel trace.
+
+    --summarize-step TRACE_DIR TAG: reads the *kernel_trace.csv of
+    `rocprofv3 --kernel-trace --output-format csv`, takes the dispatches of the
+    last --steps decode steps (a step ends with the argmax finish kernel) and
+    writes profiles/TAG.md: per kernel (name and grid), dispatches and time per
+    step, and the step's span on the GPU clock.
+    """
+    import csv
+    import glob
+    from collections import defaultdict
+
+    trace_dir, tag = args.summarize_step
+    rows = []
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            grid = r.get("Grid_Size_X") or r.get("Grid_Size") or "?"
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], grid))
+    rows.sort()
+    ends = [i for i, r in enumerate(rows) if "argmaxFinish" in r[2]]
+    k = args.steps
+    sel = rows[ends[-k - 1] + 1: ends[-1] + 1]
+    span_us = (sel[-1][1] - sel[0][0]) / 1e3 / k
+
+    def short(name):
+        import re
+
+        if name.startswith("Cijk_"):  # library GEMM (Tensile): keep the macro tile
+            tile = re.search(r"MT\d+x\d+x\d+", name)
+            return "rocBLAS GEMM " + (tile.group(0) if tile else name[:40])
+        name = name.replace("(anonymous namespace)::", "").replace("void ", "").replace("llaisys::kernels::", "")
+        return name.split("(")[0]
+
+    agg = defaultdict(lambda: [0, 0.0])
+    for st, en, name, grid in sel:
+        key = (short(name), grid)
+        agg[key][0] += 1
+        agg[key][1] += (en - st) / 1e3
+    busy = sum(v[1] for v in agg.values()) / k
+    lines = [f"# {tag}: one decode step of the Qwen2-1.5B-shape model (rocprofv3 kernel trace)", "",
+             "Command (from the repo root, on the MI355X box):", "", "```",
+             f"rocprofv3 --kernel-trace --output-format csv -d {trace_dir} -o run -- python3 bench.py --workload qwen2 "
+             f"--steps {k} --warmup 2 --no-cpu",
+             f"python3 bench.py --summarize-step {trace_dir} {tag} --steps {k}", "```", "",
+             f"Last {k} steps: GPU span {span_us:.1f} us per step, kernels busy {busy:.1f} us per step "
+             f"({len(sel) / k:.0f} dispatches per step).", "",
+             "| kernel | grid (work-items) | per step | us per step | avg us |", "|---|---|---|---|---|"]
+    for (name, grid), (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        lines.append(f"| `{name}` | {grid} | {n / k:.0f} | {t / k:.1f} | {t / n:.2f} |")
+    print("\n".join(lines))
+    (ROOT / "profiles").mkdir(exist_ok=True)
+    (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
+
+
 def traffic_from_profiles(kernel_tag):
     """HBM bytes per launch measured by rocprofv3 PMC, if a summary is committed under profiles/."""
     f = ROOT / "profiles" / f"{kernel_tag}_traffic.json"
@@ -523,6 +598,9 @@ def main():
     args.warmup = args.warmup if args.warmup is not None else (4 if small else 20)
     if args.summarize:
         summarize(args)
+        return
+    if args.summarize_step:
+        summarize_step(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the KV-cache path "
