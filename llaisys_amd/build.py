@@ -64,7 +64,7 @@ def build(verbose: bool = True) -> Path:
     LIB.parent.mkdir(exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
     rocm_lib = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), f"-L{rocm_lib}", "-lrocblas",
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), f"-L{rocm_lib}", "-lrocblas", "-lhipblaslt",
            "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

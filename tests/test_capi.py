@@ -87,7 +87,7 @@ def test_last_error_is_cleared_after_read():
 
 def test_one_hip_runtime_whatever_the_import_order():
     # Importing llaisys_amd before torch must not map a second libamdhip64
-    # (nor a second librocblas, which carries its own device code objects).
+    # (nor a second rocBLAS / hipBLASLt, which carry their own device code objects).
     import subprocess
     import sys
 
@@ -96,11 +96,12 @@ def test_one_hip_runtime_whatever_the_import_order():
         "maps = open(f'/proc/{os.getpid()}/maps').read().splitlines()\n"
         "hip = {l.split()[-1] for l in maps if 'amdhip64' in l and 'r-xp' in l}\n"
         "blas = {l.split()[-1] for l in maps if 'librocblas' in l and 'r-xp' in l}\n"
-        "print(len(hip), len(blas))\n"
+        "lt = {l.split()[-1] for l in maps if 'libhipblaslt.so' in l and 'r-xp' in l}\n"
+        "print(len(hip), len(blas), len(lt))\n"
     )
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=str(ROOT))
     assert r.returncode == 0, r.stderr
-    assert r.stdout.strip() == "1 1"
+    assert r.stdout.strip() == "1 1 1"
 
 
 def test_qwen2_create_rejects_cpu_and_non_bf16():
