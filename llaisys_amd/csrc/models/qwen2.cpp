@@ -11,10 +11,14 @@
 #include "../common.hpp"
 #include "../core/core.hpp"
 #include "../kernels/launch.hpp"
+#include "../device/hip_check.hpp"
 #include "../ops/ops.hpp"
+
+#include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 namespace llaisys::models {
@@ -50,6 +54,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     LLAISYS_CHECK(cfg.di % 8 == 0 && cfg.hs % 8 == 0, "qwen2: hs and di must be multiples of 8");
     LLAISYS_CHECK(num_blocks > 0 && num_blocks < (size_t(1) << 31), "qwen2: bad KV block count " << num_blocks);
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
+    if (const char *e = std::getenv("LLAISYS_QWEN2_GRAPHS")) use_graphs_ = e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -79,7 +84,49 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     }
 }
 
-Qwen2Model::~Qwen2Model() = default;
+Qwen2Model::~Qwen2Model() {
+    for (auto &kv : graphs_)
+        if (kv.second.exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(kv.second.exec));
+}
+
+// Decode steps of one batch size replay a captured graph of forward(): same
+// kernels, same arguments, the per-step indices read from the same device
+// buffers. A graph is (re)captured when the table width, any workspace buffer
+// or the runtime's split workspace moved; the step that captures runs eagerly
+// first (so library GEMM tuning and workspace growth happen outside the
+// capture) and its results are the eager ones.
+void Qwen2Model::decodeGraph(size_t B, size_t width) {
+    auto &rt = core::context().runtime();
+    auto s = static_cast<hipStream_t>(rt.stream());
+    DecodeGraph &g = graphs_[B];
+    if (g.exec && g.width == width && g.gen == ws_gen_ && g.scratch == rt.scratch(0)) {
+        HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(g.exec), s));
+        return;
+    }
+    if (g.exec) {
+        HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(g.exec)));
+        g.exec = nullptr;
+    }
+    forward(B, B, true);
+    hipGraph_t graph = nullptr;
+    HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    try {
+        forward(B, B, true);
+    } catch (...) {
+        (void)hipStreamEndCapture(s, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    HIP_CHECK(hipStreamEndCapture(s, &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIP_CHECK(e);
+    g.exec = exec;
+    g.width = width;
+    g.gen = ws_gen_;
+    g.scratch = rt.scratch(0);
+}
 
 void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints64) {
     auto &rt = core::context().runtime();
@@ -96,6 +143,7 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
         gu_ = dev({cap, 2 * cfg_.di}, dt, dev_);
         act_ = dev({cap, cfg_.di}, dt, dev_);
         cap_T_ = cap;
+        ++ws_gen_;
     }
     if (B > cap_B_) {
         const size_t cap = std::max(B, cap_B_ * 2);
@@ -104,6 +152,7 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
         logits_ = dev({cap, cfg_.voc}, dt, dev_);
         next_ = dev({cap}, LLAISYS_DTYPE_I64, dev_);
         cap_B_ = cap;
+        ++ws_gen_;
     }
     if (ints32 > cap_i32_) {
         const size_t cap = std::max(ints32, cap_i32_ * 2);
@@ -111,6 +160,7 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
         dev_i32_ = dev({cap}, LLAISYS_DTYPE_I32, dev_);
         host32_ = rt.allocateHostStorage(cap * sizeof(int32_t));
         cap_i32_ = cap;
+        ++ws_gen_;
     }
     if (ints64 + B > cap_i64_) {
         const size_t cap = std::max(ints64 + B, cap_i64_ * 2);
@@ -118,6 +168,7 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
         dev_i64_ = dev({cap}, LLAISYS_DTYPE_I64, dev_);
         host64_ = rt.allocateHostStorage(cap * sizeof(int64_t));
         cap_i64_ = cap;
+        ++ws_gen_;
     }
 }
 
@@ -158,7 +209,10 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
         }
         throw;
     }
-    const size_t max_pages = size_t(std::max(1, blocks_.buildTable(ids, B, nullptr, 0, nullptr)));
+    // Table width rounded up to 32 pages, so it (and a captured decode graph)
+    // changes once per 512 tokens of the longest sequence, not every page.
+    const size_t used_pages = size_t(std::max(1, blocks_.buildTable(ids, B, nullptr, 0, nullptr)));
+    const size_t max_pages = (used_pages + 31) / 32 * 32;
     const size_t ncow = cow.size() / 2;
     const size_t n32 = B * max_pages + 3 * B + 1 + cow.size();
     const size_t n64 = T + B;
@@ -192,8 +246,14 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     tok_ = dev_i64_->slice(0, 0, T);
     last_ = dev_i64_->slice(0, T, T + B);
 
-    bool decode_only = T == B;
-    forward(T, B, decode_only);
+    if (cow_)
+        for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], cow_);
+    const bool decode_only = T == B;
+    if (decode_only && use_graphs_) {
+        decodeGraph(B, max_pages);
+    } else {
+        forward(T, B, decode_only);
+    }
 
     // next tokens back to the host; the staging buffers are free after this.
     int64_t *hnext = h64 + n64;
@@ -214,9 +274,6 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     const int q = int(cfg_.nh * cfg_.dh), kv = int(cfg_.nkvh * cfg_.dh);
     const int M = int(T);
     const float scale = 1.f / std::sqrt(float(cfg_.dh));
-
-    if (cow_)
-        for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], cow_);
 
     K::embedding(x_->data(), i64(tok_), in_embed_->data(), et, T, int64_t(cfg_.voc), hs, rt.errorWord(), s);
     const tensor_t q3 = rows(q_, T), a3 = rows(attn_, T);

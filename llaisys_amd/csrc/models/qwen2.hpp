@@ -19,6 +19,7 @@
 #include "../tensor/tensor.hpp"
 
 #include <cstdint>
+#include <map>
 #include <vector>
 
 namespace llaisys::models {
@@ -71,6 +72,7 @@ public:
 private:
     void ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints64);
     void forward(size_t T, size_t B, bool decode_only);
+    void decodeGraph(size_t B, size_t width);
 
     Qwen2Config cfg_;
     int dev_;
@@ -91,6 +93,17 @@ private:
     core::storage_t host32_, host64_; // pinned staging of the same
     tensor_t table_, ctx_before_, ctx_after_, cu_, cow_, tok_, last_; // views of dev_i32_/dev_i64_
     size_t last_B_ = 0;
+
+    // Captured decode steps per batch size (LLAISYS_QWEN2_GRAPHS=0 disables).
+    struct DecodeGraph {
+        void *exec = nullptr; // hipGraphExec_t
+        size_t width = 0;     // block-table width it was captured with
+        uint64_t gen = 0;     // workspace generation it was captured with
+        void *scratch = nullptr;
+    };
+    bool use_graphs_ = true;
+    uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
+    std::map<size_t, DecodeGraph> graphs_;
 };
 
 } // namespace llaisys::models

@@ -207,3 +207,29 @@ def test_random_init_builds_on_gpu():
     nxt = model.step(ids, [[1, 2, 3], [4], [5, 6]])
     assert all(0 <= t < 1000 for t in nxt)
     assert model.generate([1, 2, 3], max_new_tokens=4)[:3] == [1, 2, 3]
+
+
+def test_decode_graph_replays_match_eager(monkeypatch):
+    # Decode steps replay a captured graph; results must equal eager execution
+    # bit for bit, across re-captures (table width 32 -> 64 pages at 512 tokens,
+    # a fork changing the batch, copy-on-write copies before the replay).
+    models = {}
+    for graphs in ("1", "0"):
+        monkeypatch.setenv("LLAISYS_QWEN2_GRAPHS", graphs)
+        models[graphs] = build("tiny", num_blocks=512)[0]
+    runs = {}
+    for key, model in models.items():
+        ids = [model.create_sequence()[0] for _ in range(3)]
+        prompts = [prompt(n, model.meta.voc, 40 + n) for n in (490, 500, 505)]
+        nxt = model.step(ids, prompts)
+        out = []
+        for step in range(24):
+            if step == 8:
+                ids.append(model.fork(ids[0]))
+                nxt = list(nxt) + [nxt[0]]
+            nxt = model.step(ids, [[t] for t in nxt])
+            out.append((list(nxt), to_torch(model.logits()).cpu()))
+        runs[key] = out
+    for (ta, la), (tb, lb) in zip(runs["1"], runs["0"]):
+        assert ta == tb
+        assert torch.equal(la, lb)
