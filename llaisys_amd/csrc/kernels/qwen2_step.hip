@@ -54,14 +54,16 @@ __device__ __forceinline__ int vPageIndex(int t, int d) {
     return (d >> 5) * 512 + (t >> 2) * 128 + (d & 15) * 8 + ((d >> 4) & 1) * 4 + (t & 3);
 }
 
-// One block per token row r of sequence b (cu: varlen offsets, else r == b),
-// position pos = ctx[b] + (r - cu[b]). Error bits as the append kernel: 1 bad
-// block id, 2 position past the block table.
-__global__ void __launch_bounds__(kThreads) qkvRopeAppendKernel(
+// One 64-lane block per (token row r, head h) over the nh query, nkvh key and
+// nkvh value heads; row r belongs to sequence b (cu: varlen offsets, else
+// r == b) at position pos = ctx[b] + (r - cu[b]). Lane j rotates the pair
+// (j, j + d/2) of a q or k head, or moves dims 2j, 2j+1 of a v head. Error
+// bits as the append kernel: 1 bad block id, 2 position past the block table.
+__global__ void __launch_bounds__(64) qkvRopeAppendKernel(
     bf16 *q, uint16_t *k_pool, uint16_t *v_pool, const bf16 *qkv, const bf16 *bias, const int32_t *table,
     const int32_t *ctx, const int32_t *cu, int B, int nh, int nkvh, int d, int max_pages, int num_blocks, float theta,
     int *err) {
-    const int r = blockIdx.x;
+    const int r = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
     int b = r;
     if (cu) {
         int lo = 0, hi = B - 1;
@@ -72,22 +74,10 @@ __global__ void __launch_bounds__(kThreads) qkvRopeAppendKernel(
         b = lo;
     }
     const int pos = ctx[b] + (cu ? r - cu[b] : 0);
-    const int page = pos >> 4, slot = pos & 15;
-    bool ok = pos >= 0 && page < max_pages;
-    int blk = ok ? table[size_t(b) * max_pages + page] : -1;
-    if (!ok) {
-        if (threadIdx.x == 0) atomicOr(err, 2);
-    } else if (blk < 0 || blk >= num_blocks) {
-        if (threadIdx.x == 0) atomicOr(err, 1);
-        ok = false;
-    }
     const int half = d / 2;
-    const int width = (nh + 2 * nkvh) * d;
-    const bf16 *row = qkv + size_t(r) * width;
-    const float p = float(pos);
-    for (int i = threadIdx.x; i < (nh + nkvh) * half; i += kThreads) {
-        const int h = i / half, j = i - h * half;
-        const float phi = p / powf(theta, float(2 * j) / float(d));
+    const bf16 *row = qkv + size_t(r) * (nh + 2 * nkvh) * d;
+    if (h < nh + nkvh) {
+        const float phi = float(pos) / powf(theta, float(2 * j) / float(d));
         float sn, cs;
         sincosf(phi, &sn, &cs);
         const int c = h * d + j;
@@ -97,22 +87,41 @@ __global__ void __launch_bounds__(kThreads) qkvRopeAppendKernel(
             bf16 *dst = q + (size_t(r) * nh + h) * d;
             dst[j] = ra;
             dst[j + half] = rb;
-        } else if (ok) {
-            uint16_t *pg = k_pool + (size_t(blk) * nkvh + (h - nh)) * kPageElems;
-            pg[kPageIndex(slot, j)] = __builtin_bit_cast(uint16_t, ra);
-            pg[kPageIndex(slot, j + half)] = __builtin_bit_cast(uint16_t, rb);
+            return;
         }
     }
-    if (!ok) return;
-    for (int i = threadIdx.x; i < nkvh * d; i += kThreads) {
-        const int h = i / d, dd = i - h * d;
-        const int c = (nh + nkvh) * d + i;
-        const bf16 v = __float2bfloat16(f(row[c]) + f(bias[c]));
-        v_pool[(size_t(blk) * nkvh + h) * kPageElems + vPageIndex(slot, dd)] = __builtin_bit_cast(uint16_t, v);
+    // k or v head: find the page slot
+    const int page = pos >> 4, slot = pos & 15;
+    const bool in_table = pos >= 0 && page < max_pages;
+    const int blk = in_table ? table[size_t(b) * max_pages + page] : -1;
+    if (!in_table || blk < 0 || blk >= num_blocks) {
+        if (j == 0 && h == nh) atomicOr(err, in_table ? 1 : 2);
+        return;
+    }
+    if (h < nh + nkvh) {
+        const int c = h * d + j;
+        const float a = f(row[c]) + f(bias[c]), bb = f(row[c + half]) + f(bias[c + half]);
+        const float phi = float(pos) / powf(theta, float(2 * j) / float(d));
+        float sn, cs;
+        sincosf(phi, &sn, &cs);
+        uint16_t *pg = k_pool + (size_t(blk) * nkvh + (h - nh)) * kPageElems;
+        pg[kPageIndex(slot, j)] = __builtin_bit_cast(uint16_t, __float2bfloat16(a * cs - bb * sn));
+        pg[kPageIndex(slot, j + half)] = __builtin_bit_cast(uint16_t, __float2bfloat16(bb * cs + a * sn));
+    } else {
+        const int hv = h - nh - nkvh;
+        uint16_t *pg = v_pool + (size_t(blk) * nkvh + hv) * kPageElems;
+        for (int dd = 2 * j; dd < 2 * j + 2; ++dd) {
+            const int c = (nh + nkvh) * d + hv * d + dd;
+            pg[vPageIndex(slot, dd)] = __builtin_bit_cast(uint16_t, __float2bfloat16(f(row[c]) + f(bias[c])));
+        }
     }
 }
 
-// One block per output row r (source row rows[r], or r), 8 columns per thread-step.
+// One block per output row r (source row rows[r], or r), 8 columns per
+// thread-step; rows of up to kRowVecs * 256 * 8 elements are read once and
+// kept in registers between the sum of squares and the scaling.
+constexpr int kRowVecs = 4;
+
 __global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(uint16_t *out, const bf16 *x, const int64_t *rows,
                                                               const bf16 *w, int d, float eps) {
     __shared__ float red[kThreads / 64];
@@ -120,12 +129,15 @@ __global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(uint16_t *out, con
     const uint4 *src = reinterpret_cast<const uint4 *>(x + size_t(rows ? rows[r] : r) * d);
     const uint4 *wr = reinterpret_cast<const uint4 *>(w);
     const int nv = d / 8;
+    uint4 v[kRowVecs];
     float ss = 0.f;
-    for (int c = threadIdx.x; c < nv; c += kThreads) {
-        const uint4 v = src[c];
+#pragma unroll
+    for (int i = 0; i < kRowVecs; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        v[i] = c < nv ? src[c] : uint4{0, 0, 0, 0};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t u = (&v.x)[e];
+            const uint32_t u = (&v[i].x)[e];
             const float lo = __uint_as_float(u << 16), hi = __uint_as_float(u & 0xffff0000u);
             ss += lo * lo + hi * hi;
         }
@@ -137,12 +149,15 @@ __global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(uint16_t *out, con
     float tot = 0.f;
     for (int i = 0; i < kThreads / 64; ++i) tot += red[i];
     const float inv = rsqrtf(tot / float(d) + eps);
-    for (int c = threadIdx.x; c < nv; c += kThreads) {
-        const uint4 v = src[c], g = wr[c];
+#pragma unroll
+    for (int i = 0; i < kRowVecs; ++i) {
+        const int c = threadIdx.x + i * kThreads;
+        if (c >= nv) break;
+        const uint4 g = wr[c];
         uint4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t u = (&v.x)[e], gw = (&g.x)[e];
+            const uint32_t u = (&v[i].x)[e], gw = (&g.x)[e];
             const uint32_t lo = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(u << 16) * inv *
                                                                                __uint_as_float(gw << 16)));
             const uint32_t hi = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(u & 0xffff0000u) * inv *
@@ -159,7 +174,9 @@ void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16
                    const int32_t *table, const int32_t *ctx, const int32_t *cu, int T, int B, int nh, int nkvh, int d,
                    int max_pages, int num_blocks, float theta, int *err, void *stream) {
     if (!T) return;
-    hipLaunchKernelGGL(qkvRopeAppendKernel, dim3(unsigned(T)), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+    LLAISYS_CHECK(d == 128, "qkvRopeAppend: head dim must be 128, got " << d);
+    hipLaunchKernelGGL(qkvRopeAppendKernel, dim3(unsigned(T), unsigned(nh + 2 * nkvh)), dim3(d / 2), 0,
+                       static_cast<hipStream_t>(stream),
                        reinterpret_cast<bf16 *>(q), k_pool, v_pool, reinterpret_cast<const bf16 *>(qkv),
                        reinterpret_cast<const bf16 *>(bias), table, ctx, cu, B, nh, nkvh, d, max_pages, num_blocks,
                        theta, err);
@@ -178,7 +195,8 @@ void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *
 
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
                  void *stream) {
-    LLAISYS_CHECK(d % 8 == 0, "rmsNormRows: d must be a multiple of 8, got " << d);
+    LLAISYS_CHECK(d % 8 == 0 && d <= kRowVecs * kThreads * 8,
+                  "rmsNormRows: d must be a multiple of 8 and at most " << kRowVecs * kThreads * 8 << ", got " << d);
     if (!R) return;
     hipLaunchKernelGGL(rmsNormRowsKernel, dim3(unsigned(R)), dim3(kThreads), 0, static_cast<hipStream_t>(stream), out,
                        reinterpret_cast<const bf16 *>(x), rows, reinterpret_cast<const bf16 *>(w), d, eps);
