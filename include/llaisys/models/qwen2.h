@@ -86,7 +86,14 @@ __C {
      * the sequence's last position. Returns 0, or -1 on failure. */
     __export int llaisysQwen2ModelStep(struct LlaisysQwen2Model * model, const int64_t *seq_ids, size_t nseq, const int64_t *token_ids, const size_t *ntokens, int64_t *next_tokens);
 
-    /* Logits [nseq, voc] (meta.dtype) of the last Infer/Step: a new handle the
+    /* nsteps greedy decode steps of nseq distinct sequences in one call, the
+     * next token fed back on the device (no host round trip between steps):
+     * sequence seq_ids[i] appends first_tokens[i], then its own greedy tokens.
+     * out_tokens[s * nseq + i] receives the greedy token after step s. Same
+     * results as nsteps calls of llaisysQwen2ModelStep. Returns 0, or -1. */
+    __export int llaisysQwen2ModelDecode(struct LlaisysQwen2Model * model, const int64_t *seq_ids, size_t nseq, const int64_t *first_tokens, size_t nsteps, int64_t *out_tokens);
+
+    /* Logits [nseq, voc] (meta.dtype) of the last Infer/Step/Decode step: a new handle the
      * caller destroys; its contents change at the next call. */
     __export llaisysTensor_t llaisysQwen2ModelLogits(struct LlaisysQwen2Model * model);
 }

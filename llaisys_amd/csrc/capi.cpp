@@ -467,6 +467,18 @@ int llaisysQwen2ModelStep(LlaisysQwen2Model *m, const int64_t *seq_ids, size_t n
         -1);
 }
 
+int llaisysQwen2ModelDecode(LlaisysQwen2Model *m, const int64_t *seq_ids, size_t nseq, const int64_t *first_tokens,
+                            size_t nsteps, int64_t *out_tokens) {
+    return guarded(
+        [&] {
+            auto &impl = model(m);
+            syncWeights(*m);
+            impl.decode(seq_ids, nseq, first_tokens, nsteps, out_tokens);
+            return 0;
+        },
+        -1);
+}
+
 llaisysTensor_t llaisysQwen2ModelLogits(LlaisysQwen2Model *m) {
     return guarded([&] { return new LlaisysTensor{model(m).lastLogits()}; }, static_cast<llaisysTensor_t>(nullptr));
 }

@@ -98,6 +98,12 @@ void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16
                    int max_pages, int num_blocks, float theta, int *err, void *stream);
 // act [T, di] = up * silu(gate) with gate_up rows [gate (di) | up (di)]; di % 8 == 0.
 void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *stream);
+// Multi-step decode bookkeeping on the device (s = *counter): before a step,
+// ctx_before = base + s, ctx_after = base + s + 1, tok = s ? next : first;
+// after it, history[s][:] = next and *counter = s + 1.
+void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, const int32_t *base, const int64_t *first,
+                   const int64_t *next, const int32_t *counter, int B, void *stream);
+void decodeRecord(int64_t *history, const int64_t *next, int32_t *counter, int B, void *stream);
 // out [R, d] = rms_norm(x[rows ? rows[r] : r]) * w; d % 8 == 0.
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
                  void *stream);

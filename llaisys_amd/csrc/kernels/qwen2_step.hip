@@ -168,7 +168,43 @@ __global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(uint16_t *out, con
     }
 }
 
+// Multi-step decode: step s reads s from a device counter. Before the step:
+// lengths = base + s (before) and base + s + 1 (after), tokens = first at
+// s = 0 else the previous step's argmax. After it: history[s] = argmax, s + 1.
+// One block each (the counter is read by every thread before it moves).
+__global__ void __launch_bounds__(kThreads) decodeAdvanceKernel(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok,
+                                                                const int32_t *base, const int64_t *first,
+                                                                const int64_t *next, const int32_t *counter, int B) {
+    const int s = *counter;
+    for (int b = threadIdx.x; b < B; b += kThreads) {
+        ctx_before[b] = base[b] + s;
+        ctx_after[b] = base[b] + s + 1;
+        tok[b] = s == 0 ? first[b] : next[b];
+    }
+}
+
+__global__ void __launch_bounds__(kThreads) decodeRecordKernel(int64_t *history, const int64_t *next, int32_t *counter,
+                                                               int B) {
+    const int s = *counter;
+    for (int b = threadIdx.x; b < B; b += kThreads) history[size_t(s) * B + b] = next[b];
+    __syncthreads();
+    if (threadIdx.x == 0) *counter = s + 1;
+}
+
 } // namespace
+
+void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, const int32_t *base, const int64_t *first,
+                   const int64_t *next, const int32_t *counter, int B, void *stream) {
+    hipLaunchKernelGGL(decodeAdvanceKernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), ctx_before,
+                       ctx_after, tok, base, first, next, counter, B);
+    HIP_CHECK(hipGetLastError());
+}
+
+void decodeRecord(int64_t *history, const int64_t *next, int32_t *counter, int B, void *stream) {
+    hipLaunchKernelGGL(decodeRecordKernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), history, next,
+                       counter, B);
+    HIP_CHECK(hipGetLastError());
+}
 
 void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv, const uint16_t *bias,
                    const int32_t *table, const int32_t *ctx, const int32_t *cu, int T, int B, int nh, int nkvh, int d,

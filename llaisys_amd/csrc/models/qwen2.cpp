@@ -85,8 +85,9 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
 }
 
 Qwen2Model::~Qwen2Model() {
-    for (auto &kv : graphs_)
-        if (kv.second.exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(kv.second.exec));
+    for (auto *m : {&graphs_, &multi_graphs_})
+        for (auto &kv : *m)
+            if (kv.second.exec) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(kv.second.exec));
 }
 
 // Decode steps of one batch size replay a captured graph of forward(): same
@@ -95,6 +96,31 @@ Qwen2Model::~Qwen2Model() {
 // or the runtime's split workspace moved; the step that captures runs eagerly
 // first (so library GEMM tuning and workspace growth happen outside the
 // capture) and its results are the eager ones.
+Qwen2Model::DecodeGraph Qwen2Model::capture(const std::function<void()> &work, size_t width) {
+    auto &rt = core::context().runtime();
+    auto s = static_cast<hipStream_t>(rt.stream());
+    hipGraph_t graph = nullptr;
+    HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    try {
+        work();
+    } catch (...) {
+        (void)hipStreamEndCapture(s, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+    }
+    HIP_CHECK(hipStreamEndCapture(s, &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    HIP_CHECK(e);
+    DecodeGraph g;
+    g.exec = exec;
+    g.width = width;
+    g.gen = ws_gen_;
+    g.scratch = rt.scratch(0);
+    return g;
+}
+
 void Qwen2Model::decodeGraph(size_t B, size_t width) {
     auto &rt = core::context().runtime();
     auto s = static_cast<hipStream_t>(rt.stream());
@@ -108,24 +134,7 @@ void Qwen2Model::decodeGraph(size_t B, size_t width) {
         g.exec = nullptr;
     }
     forward(B, B, true);
-    hipGraph_t graph = nullptr;
-    HIP_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    try {
-        forward(B, B, true);
-    } catch (...) {
-        (void)hipStreamEndCapture(s, &graph);
-        if (graph) (void)hipGraphDestroy(graph);
-        throw;
-    }
-    HIP_CHECK(hipStreamEndCapture(s, &graph));
-    hipGraphExec_t exec = nullptr;
-    const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    HIP_CHECK(e);
-    g.exec = exec;
-    g.width = width;
-    g.gen = ws_gen_;
-    g.scratch = rt.scratch(0);
+    g = capture([&] { forward(B, B, true); }, width);
 }
 
 void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints64) {
@@ -172,6 +181,32 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
     }
 }
 
+// Map the pages positions [len, len + n_i) of each sequence land in; returns
+// the copy-on-write (src, dst) block pairs to copy before writing, and the
+// lengths before. If a reservation fails, copies already decided are made.
+std::vector<int32_t> Qwen2Model::reserveAll(const int64_t *ids, size_t B, const size_t *n, std::vector<int32_t> &before) {
+    auto &rt = core::context().runtime();
+    std::vector<int32_t> cow;
+    try {
+        for (size_t i = 0; i < B; ++i) {
+            before[i] = blocks_.length(ids[i]);
+            int32_t pair[2];
+            if (blocks_.reserve(ids[i], int(n[i]), pair, 1) == 1) cow.insert(cow.end(), pair, pair + 2);
+        }
+    } catch (...) {
+        // A sequence already switched to its private copy of a shared block
+        // must get that copy's contents even though this call fails.
+        if (!cow.empty()) {
+            auto pairs = Tensor::create({cow.size() / 2, 2}, LLAISYS_DTYPE_I32, LLAISYS_DEVICE_AMD, dev_);
+            pairs->load(cow.data());
+            for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], pairs);
+            rt.api()->stream_synchronize(rt.stream());
+        }
+        throw;
+    }
+    return cow;
+}
+
 void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, const size_t *ntokens, int64_t *next) {
     LLAISYS_CHECK(nseq > 0, "qwen2 step: no sequences");
     LLAISYS_CHECK(ids && tokens && ntokens && next, "qwen2 step: null argument");
@@ -189,26 +224,8 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     for (size_t i = 0; i < T; ++i)
         LLAISYS_CHECK(tokens[i] >= 0 && size_t(tokens[i]) < cfg_.voc, "qwen2 step: token id " << tokens[i] << " out of vocabulary");
 
-    // Map the pages the new tokens go to (copy-on-write pairs for shared tails).
-    std::vector<int32_t> cow;
     std::vector<int32_t> before(B);
-    try {
-        for (size_t i = 0; i < B; ++i) {
-            before[i] = blocks_.length(ids[i]);
-            int32_t pair[2];
-            if (blocks_.reserve(ids[i], int(ntokens[i]), pair, 1) == 1) cow.insert(cow.end(), pair, pair + 2);
-        }
-    } catch (...) {
-        // A sequence already switched to its private copy of a shared block
-        // must get that copy's contents even though this step fails.
-        if (!cow.empty()) {
-            auto pairs = Tensor::create({cow.size() / 2, 2}, LLAISYS_DTYPE_I32, LLAISYS_DEVICE_AMD, dev_);
-            pairs->load(cow.data());
-            for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], pairs);
-            rt.api()->stream_synchronize(rt.stream());
-        }
-        throw;
-    }
+    const std::vector<int32_t> cow = reserveAll(ids, B, ntokens, before);
     // Table width rounded up to 32 pages, so it (and a captured decode graph)
     // changes once per 512 tokens of the longest sequence, not every page.
     const size_t used_pages = size_t(std::max(1, blocks_.buildTable(ids, B, nullptr, 0, nullptr)));
@@ -264,6 +281,110 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     std::memcpy(next, hnext, B * sizeof(int64_t));
     last_B_ = B;
     for (size_t i = 0; i < B; ++i) blocks_.commit(ids[i], int(ntokens[i]), tokens + cu[i]);
+}
+
+
+// Multi-step greedy decode: nsteps single-token steps of the batch with the
+// next token fed back on the device. Pages for all steps are reserved up
+// front and the table is uploaded once; each step is decodeAdvance (lengths,
+// tokens from a device step counter), forward(), decodeRecord (argmax into
+// the history, counter + 1) - one captured graph replayed nsteps times.
+void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, size_t nsteps, int64_t *out) {
+    LLAISYS_CHECK(nseq > 0 && nsteps > 0, "qwen2 decode: no sequences or no steps");
+    LLAISYS_CHECK(ids && first && out, "qwen2 decode: null argument");
+    core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
+    auto &rt = core::context().runtime();
+    const size_t B = nseq;
+    for (size_t i = 0; i < B; ++i) {
+        LLAISYS_CHECK(size_t(blocks_.length(ids[i])) + nsteps <= cfg_.maxseq,
+                      "qwen2 decode: sequence " << ids[i] << " would exceed maxseq " << cfg_.maxseq);
+        for (size_t j = 0; j < i; ++j)
+            LLAISYS_CHECK(ids[j] != ids[i], "qwen2 decode: sequence " << ids[i] << " listed twice");
+        LLAISYS_CHECK(first[i] >= 0 && size_t(first[i]) < cfg_.voc,
+                      "qwen2 decode: token id " << first[i] << " out of vocabulary");
+    }
+    std::vector<int32_t> before(B);
+    const std::vector<size_t> counts(B, nsteps);
+    const std::vector<int32_t> cow = reserveAll(ids, B, counts.data(), before);
+    const size_t used_pages = size_t(std::max(1, blocks_.buildTable(ids, B, nullptr, 0, nullptr)));
+    const size_t width = (used_pages + 31) / 32 * 32;
+    const size_t ncow = cow.size() / 2;
+    // int32: table | ctx_before | ctx_after | cu | base | counter | cow ; int64: tok | last | first | history
+    const size_t o_cb = B * width, o_ca = o_cb + B, o_cu = o_ca + B, o_base = o_cu + B + 1, o_cnt = o_base + B;
+    const size_t n32 = o_cnt + 1 + cow.size();
+    const size_t n64 = 3 * B + nsteps * B;
+    ensureWorkspace(B, B, n32, n64);
+    int32_t *h32 = reinterpret_cast<int32_t *>(host32_->memory());
+    std::vector<int32_t> ctx_scratch(B);
+    blocks_.buildTable(ids, B, h32, width, ctx_scratch.data());
+    for (size_t i = 0; i < B; ++i) {
+        h32[o_cb + i] = before[i];
+        h32[o_ca + i] = before[i] + 1;
+        h32[o_cu + i] = int32_t(i);
+        h32[o_base + i] = before[i];
+    }
+    h32[o_cu + B] = int32_t(B);
+    h32[o_cnt] = 0;
+    std::copy(cow.begin(), cow.end(), h32 + o_cnt + 1);
+    int64_t *h64 = reinterpret_cast<int64_t *>(host64_->memory());
+    for (size_t i = 0; i < B; ++i) {
+        h64[i] = first[i];
+        h64[B + i] = int64_t(i);
+        h64[2 * B + i] = first[i];
+    }
+    auto *api = rt.api();
+    api->memcpy_async(dev_i32_->data(), h32, n32 * sizeof(int32_t), LLAISYS_MEMCPY_H2D, rt.stream());
+    api->memcpy_async(dev_i64_->data(), h64, 3 * B * sizeof(int64_t), LLAISYS_MEMCPY_H2D, rt.stream());
+
+    table_ = dev_i32_->slice(0, 0, B * width)->view({B, width});
+    ctx_before_ = dev_i32_->slice(0, o_cb, o_cb + B);
+    ctx_after_ = dev_i32_->slice(0, o_ca, o_ca + B);
+    cu_ = dev_i32_->slice(0, o_cu, o_cu + B + 1);
+    cow_ = ncow ? dev_i32_->slice(0, o_cnt + 1, n32)->view({ncow, 2}) : nullptr;
+    tok_ = dev_i64_->slice(0, 0, B);
+    last_ = dev_i64_->slice(0, B, 2 * B);
+    auto *base = reinterpret_cast<int32_t *>(dev_i32_->data()) + o_base;
+    auto *counter = reinterpret_cast<int32_t *>(dev_i32_->data()) + o_cnt;
+    auto *first_d = reinterpret_cast<int64_t *>(dev_i64_->data()) + 2 * B;
+    auto *history = reinterpret_cast<int64_t *>(dev_i64_->data()) + 3 * B;
+    if (cow_)
+        for (size_t l = 0; l < cfg_.nlayer; ++l) ops::pagedKVCopyBlocks(k_pool_[l], v_pool_[l], cow_);
+
+    void *s = rt.stream();
+    auto oneStep = [&] {
+        K::decodeAdvance(i32(ctx_before_), i32(ctx_after_), i64(tok_), base, first_d, i64(next_), counter, int(B), s);
+        forward(B, B, true);
+        K::decodeRecord(history, i64(next_), counter, int(B), s);
+    };
+    size_t done = 0;
+    if (use_graphs_) {
+        DecodeGraph &g = multi_graphs_[B];
+        const bool valid = g.exec && g.width == width && g.gen == ws_gen_ && g.scratch == rt.scratch(0);
+        if (!valid) {
+            if (g.exec) HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(g.exec)));
+            g.exec = nullptr;
+            oneStep(); // eager: library tuning and workspace growth stay outside the capture
+            done = 1;
+            g = capture(oneStep, width);
+        }
+        for (; done < nsteps; ++done) HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(g.exec), static_cast<hipStream_t>(s)));
+    } else {
+        for (; done < nsteps; ++done) oneStep();
+    }
+
+    int64_t *hout = h64 + 3 * B;
+    api->memcpy_async(hout, history, nsteps * B * sizeof(int64_t), LLAISYS_MEMCPY_D2H, s);
+    api->stream_synchronize(s);
+    const int flags = rt.takeErrorFlags();
+    LLAISYS_CHECK(flags == 0, "qwen2 decode: kernels reported error flags " << flags);
+    std::memcpy(out, hout, nsteps * B * sizeof(int64_t));
+    last_B_ = B;
+    std::vector<int64_t> fed(nsteps);
+    for (size_t i = 0; i < B; ++i) {
+        fed[0] = first[i];
+        for (size_t t = 1; t < nsteps; ++t) fed[t] = out[(t - 1) * B + i];
+        blocks_.commit(ids[i], int(nsteps), fed.data());
+    }
 }
 
 void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {

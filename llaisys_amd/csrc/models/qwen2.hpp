@@ -19,6 +19,7 @@
 #include "../tensor/tensor.hpp"
 
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <vector>
 
@@ -66,6 +67,11 @@ public:
     // in tokens); next[i] is the argmax of the logits at its last position.
     void step(const int64_t *ids, size_t nseq, const int64_t *tokens, const size_t *ntokens, int64_t *next);
 
+    // nsteps greedy single-token steps of the batch with the next token fed
+    // back on the device: sequence ids[i] appends first[i], then its own
+    // greedy tokens; out[s * nseq + i] = the greedy token after step s.
+    void decode(const int64_t *ids, size_t nseq, const int64_t *first, size_t nsteps, int64_t *out);
+
     // Logits [nseq, voc] of the last step (a view of the step workspace).
     tensor_t lastLogits() const;
 
@@ -73,6 +79,7 @@ private:
     void ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints64);
     void forward(size_t T, size_t B, bool decode_only);
     void decodeGraph(size_t B, size_t width);
+    std::vector<int32_t> reserveAll(const int64_t *ids, size_t B, const size_t *n, std::vector<int32_t> &before);
 
     Qwen2Config cfg_;
     int dev_;
@@ -101,9 +108,11 @@ private:
         uint64_t gen = 0;     // workspace generation it was captured with
         void *scratch = nullptr;
     };
+    DecodeGraph capture(const std::function<void()> &work, size_t width);
     bool use_graphs_ = true;
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
-    std::map<size_t, DecodeGraph> graphs_;
+    std::map<size_t, DecodeGraph> graphs_;       // one step (step())
+    std::map<size_t, DecodeGraph> multi_graphs_; // advance + step + record (decode())
 };
 
 } // namespace llaisys::models

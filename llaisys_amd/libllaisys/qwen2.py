@@ -72,5 +72,8 @@ def load_qwen2(lib):
     lib.llaisysQwen2ModelStep.argtypes = [M, POINTER(c_int64), c_size_t, POINTER(c_int64), POINTER(c_size_t),
                                           POINTER(c_int64)]
     lib.llaisysQwen2ModelStep.restype = c_int
+    lib.llaisysQwen2ModelDecode.argtypes = [M, POINTER(c_int64), c_size_t, POINTER(c_int64), c_size_t,
+                                            POINTER(c_int64)]
+    lib.llaisysQwen2ModelDecode.restype = c_int
     lib.llaisysQwen2ModelLogits.argtypes = [M]
     lib.llaisysQwen2ModelLogits.restype = llaisysTensor_t

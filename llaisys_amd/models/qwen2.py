@@ -12,7 +12,8 @@ weights into the tensors the library hands out and marshals token arrays:
   tests;
 * `create_sequence / step / fork / free` drive the batched API: one step
   appends any number of tokens per sequence (prefill chunks and decodes
-  mix) and returns each sequence's greedy next token.
+  mix) and returns each sequence's greedy next token; `decode` runs many
+  greedy steps of a batch in one call.
 """
 from __future__ import annotations
 
@@ -247,6 +248,18 @@ class Qwen2:
             flat_tokens.ctypes.data_as(POINTER(c_int64)), counts.ctypes.data_as(POINTER(c_size_t)),
             out.ctypes.data_as(POINTER(c_int64)))
         check_last_error()
+
+    def decode(self, seq_ids: Sequence[int], first_tokens: Sequence[int], nsteps: int) -> np.ndarray:
+        """nsteps greedy steps in one call (tokens fed back on the device).
+        Returns int64 [nsteps, nseq]: row s = each sequence's token after step s."""
+        ids = np.ascontiguousarray(np.asarray(seq_ids, dtype=np.int64))
+        first = np.ascontiguousarray(np.asarray(first_tokens, dtype=np.int64))
+        out = np.zeros((nsteps, ids.size), np.int64)
+        LIB_LLAISYS.llaisysQwen2ModelDecode(self._model, ids.ctypes.data_as(POINTER(c_int64)), ids.size,
+                                            first.ctypes.data_as(POINTER(c_int64)), nsteps,
+                                            out.ctypes.data_as(POINTER(c_int64)))
+        check_last_error()
+        return out
 
     def logits(self) -> Tensor:
         """[nseq, voc] logits of the last infer/step (a view; copy before the next call)."""

@@ -233,3 +233,32 @@ def test_decode_graph_replays_match_eager(monkeypatch):
     for (ta, la), (tb, lb) in zip(runs["1"], runs["0"]):
         assert ta == tb
         assert torch.equal(la, lb)
+
+
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_multi_step_decode_equals_single_steps(monkeypatch, graphs):
+    # decode(n) == n single steps: same tokens, same final logits (bit for bit),
+    # across a page boundary and a forked sequence sharing a partial block.
+    monkeypatch.setenv("LLAISYS_QWEN2_GRAPHS", graphs)
+    a_model = build("tiny", num_blocks=256)[0]
+    b_model = build("tiny", num_blocks=256)[0]
+    seqs = {}
+    for key, model in (("a", a_model), ("b", b_model)):
+        ids = [model.create_sequence()[0] for _ in range(3)]
+        prompts = [prompt(n, model.meta.voc, 60 + n) for n in (5, 14, 30)]
+        first = model.step(ids, prompts)
+        ids.append(model.fork(ids[1]))
+        first = list(first) + [first[1]]
+        seqs[key] = (model, ids, first)
+    model, ids, first = seqs["a"]
+    multi = model.decode(ids, first, 20)
+    multi_logits = to_torch(model.logits()).cpu()
+    model, ids, first = seqs["b"]
+    cur, single = list(first), []
+    for _ in range(20):
+        cur = model.step(ids, [[t] for t in cur])
+        single.append(cur)
+    assert multi.tolist() == single
+    assert torch.equal(multi_logits, to_torch(model.logits()).cpu())
+    for i in ids:
+        assert seqs["a"][0].length(i) == model.length(i)
