@@ -125,8 +125,11 @@ template <int NSTAGE> struct Ring {
     u32x4 q[NSTAGE][4];
 };
 
+// Two stages fit 256 registers (two waves per SIMD); three need the whole
+// register file (one wave per SIMD) to avoid spilling.
 template <bool OUT_F32, int NSTAGE>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) decodeKernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64)
+    __attribute__((amdgpu_waves_per_eu(NSTAGE == 2 ? 2 : 1, NSTAGE == 2 ? 2 : 1))) decodeKernel(DecodeArgs a) {
     extern __shared__ int lds[];
     int *S = lds;
     int *C = lds + a.B + 1;
