@@ -53,6 +53,8 @@ def parse():
                    help="summarise rocprofv3 output directories into profiles/TAG.md and profiles/TAG_traffic.json")
     p.add_argument("--summarize-step", nargs=2, metavar=("TRACE_DIR", "TAG"),
                    help="per-step kernel table of a --workload qwen2 kernel trace into profiles/TAG.md")
+    p.add_argument("--summarize-mfma", nargs=4, metavar=("STATS_DIR", "UTIL_DIR", "MOPS_DIR", "TAG"),
+                   help="per-kernel MFMA use from a kernel trace and two counter runs into profiles/TAG.md")
     p.add_argument("--profiled-args", default="--no-cpu --no-model --steps 200",
                    help="bench arguments of the kernel-trace run")
     p.add_argument("--pmc-args", default="--no-cpu --no-model --steps 20 --warmup 5",
@@ -595,6 +597,63 @@ def summarize_step(args):
     (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
 
 
+def summarize_mfma(args):
+    """MFMA use per kernel of a workload from three rocprofv3 runs.
+
+    --summarize-mfma STATS_DIR UTIL_DIR MOPS_DIR TAG: STATS_DIR holds a
+    --kernel-trace --stats run (average duration per kernel), UTIL_DIR a
+    `--pmc MfmaUtil` run (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs,
+    percent), MOPS_DIR a `--pmc SQ_INSTS_VALU_MFMA_MOPS_BF16` run (bf16 MFMA
+    math ops / 512 per dispatch). Writes profiles/TAG.md with, per kernel, the
+    MFMA-busy percentage, the bf16 MFMA FLOP per dispatch and FLOP/s over the
+    average duration, against the 2.5 PFLOP/s dense bf16 peak.
+    """
+    import csv
+    import glob
+    from collections import defaultdict
+
+    stats_dir, util_dir, mops_dir, tag = args.summarize_mfma
+
+    def counters(d):
+        acc = defaultdict(list)
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                acc[(r["Kernel_Name"], r["Counter_Name"])].append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+    def short(name):
+        return name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+
+    durations = {}
+    for f in glob.glob(os.path.join(stats_dir, "**", "*kernel_stats.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            durations[r["Name"]] = float(r["AverageNs"])
+    util, mops = counters(util_dir), counters(mops_dir)
+    cmd = f"python3 bench.py {args.profiled_args}"
+    lines = [f"# {tag}: MFMA use (rocprofv3 counters)", "", "Commands (from the repo root, on the MI355X box):", "",
+             "```",
+             f"rocprofv3 --kernel-trace --stats --output-format csv -d {stats_dir} -o run -- {cmd}",
+             f"rocprofv3 --pmc MfmaUtil --output-format csv -d {util_dir} -o run -- {cmd}",
+             f"rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16 --output-format csv -d {mops_dir} -o run -- {cmd}",
+             f"python3 bench.py --summarize-mfma {' '.join(args.summarize_mfma)} --profiled-args '{args.profiled_args}'",
+             "```", "",
+             "| kernel | avg us | MFMA busy % | bf16 MFMA GFLOP / dispatch | TFLOP/s | % of 2.5 PFLOP/s |",
+             "|---|---|---|---|---|---|"]
+    for name, ns in sorted(durations.items(), key=lambda kv: -kv[1]):
+        if "llaisys" not in name:
+            continue
+        u = util.get((name, "MfmaUtil"))
+        m = mops.get((name, "SQ_INSTS_VALU_MFMA_MOPS_BF16"))
+        flop = m * 512 if m is not None else None
+        tf = flop / ns / 1e3 if flop else None
+        lines.append(f"| `{short(name)}` | {ns / 1e3:.2f} | {'' if u is None else f'{u:.1f}'} | "
+                     f"{'' if flop is None else f'{flop / 1e9:.2f}'} | {'' if tf is None else f'{tf:.1f}'} | "
+                     f"{'' if tf is None else f'{100 * tf / 2500:.1f}'} |")
+    print("\n".join(lines))
+    (ROOT / "profiles").mkdir(exist_ok=True)
+    (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
+
+
 def traffic_from_profiles(kernel_tag):
     """HBM bytes per launch measured by rocprofv3 PMC, if a summary is committed under profiles/."""
     f = ROOT / "profiles" / f"{kernel_tag}_traffic.json"
@@ -616,6 +675,9 @@ def main():
         return
     if args.summarize_step:
         summarize_step(args)
+        return
+    if args.summarize_mfma:
+        summarize_mfma(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the KV-cache path "
