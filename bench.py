@@ -361,6 +361,13 @@ def run_qwen2(args):
 
     for i in range(args.warmup):
         step(i)
+    torch.cuda.synchronize()
+    # For reference: K single-step calls (next tokens back on the host each time).
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    single_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     cur[:] = model.decode(ids, cur, args.warmup)[-1]
     torch.cuda.synchronize()
     ctx_start = int(sum(model.length(int(i)) for i in ids))
@@ -371,12 +378,6 @@ def run_qwen2(args):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     cur[:] = toks[-1]
-    # For reference: the same number of single-step calls (host round trip each).
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
-    single_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     # mean context over the timed steps (it grows by one token per step)
     ctx_mean_total = ctx_start + B * (args.steps - 1) / 2
     nbytes, wbytes, kvbytes = qwen2_step_bytes(meta, ctx_mean_total, B)
@@ -570,9 +571,9 @@ def summarize_step(args):
     def short(name):
         import re
 
-        if name.startswith("Cijk_"):  # library GEMM (Tensile): keep the macro tile
+        if name.startswith("Cijk_"):  # library GEMM (Tensile kernels of hipBLASLt): keep the macro tile
             tile = re.search(r"MT\d+x\d+x\d+", name)
-            return "rocBLAS GEMM " + (tile.group(0) if tile else name[:40])
+            return "hipBLASLt GEMM " + (tile.group(0) if tile else name[:40])
         name = name.replace("(anonymous namespace)::", "").replace("void ", "").replace("llaisys::kernels::", "")
         return name.split("(")[0]
 
