@@ -51,8 +51,10 @@ void pagedCopyBlocks(uint16_t *k_pool, uint16_t *v_pool, const int32_t *pairs, i
                      int *err, void *stream);
 
 struct PagedAttentionPlan {
-    int units;           // (query tile, kv head) work units (upper bound)
-    int units_padded;    // rounded up to a multiple of the XCD count
+    int units;           // (query group, kv head) record units (upper bound)
+    int units_padded;    // same (kept for callers sizing by it)
+    int block_units;     // (block of groups, kv head) workgroup units (upper bound)
+    int block_units_padded; // rounded up to a multiple of the XCD count
     int max_splits;      // split-KV partitions per unit
     int pages_per_split;
     size_t partial_bytes; // workspace for split records

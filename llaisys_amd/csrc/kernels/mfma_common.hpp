@@ -75,18 +75,23 @@ struct Acc {
     }
 };
 
-// Consume one page pair. first_key = key position of page A's token 0;
-// pos = last key this lane's column may see (-1: none); ctx = keys in cache
-// (keys >= ctx are stale bytes and get zeroed V); hasB = page B exists.
-// SPLIT_P: P enters P.V as hi + lo bf16 parts (fp32-accurate) or as one bf16.
+// P of one page pair for one lane's column, as bf16 (hi, and lo when SPLIT_P).
+struct PairP {
+    bf16x8 hi, lo;
+};
+
+// Scores of one page pair (K pages a, b) against the lane's column, online
+// softmax update of acc (max, sum, rescaled O) and the pair's P. first_key =
+// key position of page A's token 0; pos = last key this lane's column may
+// see (-1: none); hasB = page B exists.
 template <bool SPLIT_P>
-__device__ __forceinline__ void consumePair(Acc &acc, PagePair &r, const u32x4 (&qop)[4], int first_key, int pos,
-                                           int ctx, bool hasB, int grp, float scale_log2) {
+__device__ __forceinline__ PairP scorePair(Acc &acc, const u32x4 (&ka)[4], const u32x4 (&kb)[4], const u32x4 (&qop)[4],
+                                          int first_key, int pos, bool hasB, int grp, float scale_log2) {
     f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        sa = mfma(asBf16(r.ka[s]), asBf16(qop[s]), sa);
-        sb = mfma(asBf16(r.kb[s]), asBf16(qop[s]), sb);
+        sa = mfma(asBf16(ka[s]), asBf16(qop[s]), sa);
+        sb = mfma(asBf16(kb[s]), asBf16(qop[s]), sb);
     }
     const int kbase = first_key + grp * 4;
     float sv[8];
@@ -115,38 +120,58 @@ __device__ __forceinline__ void consumePair(Acc &acc, PagePair &r, const u32x4 (
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc.o[i] *= alpha;
 
-    bf16x8 phi, plo;
+    PairP P;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const __bf16 hi = (__bf16)p[i];
-        phi[i] = hi;
-        if constexpr (SPLIT_P) plo[i] = (__bf16)(p[i] - (float)hi);
+        P.hi[i] = hi;
+        if constexpr (SPLIT_P) P.lo[i] = (__bf16)(p[i] - (float)hi);
     }
+    return P;
+}
 
-    // Keys at or past ctx may hold stale bytes (even NaN patterns): zero their
-    // V so 0 * V stays 0. Only a sequence's last pair has any.
+// Keys at or past ctx may hold stale bytes (even NaN patterns): zero their V
+// so 0 * V stays 0. Only a sequence's last pair has any.
+__device__ __forceinline__ void maskStaleV(u32x4 (&va)[4], u32x4 (&vb)[4], int first_key, int ctx, bool hasB, int grp) {
     if (first_key + 32 > ctx || !hasB) {
+        const int kbase = first_key + grp * 4;
         const uint32_t ma01 = keepPair(kbase < ctx, kbase + 1 < ctx);
         const uint32_t ma23 = keepPair(kbase + 2 < ctx, kbase + 3 < ctx);
         const uint32_t mb01 = hasB ? keepPair(kbase + 16 < ctx, kbase + 17 < ctx) : 0u;
         const uint32_t mb23 = hasB ? keepPair(kbase + 18 < ctx, kbase + 19 < ctx) : 0u;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            r.va[s] &= u32x4{ma01, ma23, ma01, ma23};
-            r.vb[s] &= u32x4{mb01, mb23, mb01, mb23};
+            va[s] &= u32x4{ma01, ma23, ma01, ma23};
+            vb[s] &= u32x4{mb01, mb23, mb01, mb23};
         }
     }
+}
+
+// O^T += V^T . P^T for one page pair (V pages a, b already masked).
+template <bool SPLIT_P>
+__device__ __forceinline__ void accumulatePV(Acc &acc, const u32x4 (&va)[4], const u32x4 (&vb)[4], const PairP &P) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const bf16x8 v0 = asBf16(u32x4{r.va[s][0], r.va[s][1], r.vb[s][0], r.vb[s][1]});
-        const bf16x8 v1 = asBf16(u32x4{r.va[s][2], r.va[s][3], r.vb[s][2], r.vb[s][3]});
-        acc.o[2 * s] = mfma(v0, phi, acc.o[2 * s]);
-        acc.o[2 * s + 1] = mfma(v1, phi, acc.o[2 * s + 1]);
+        const bf16x8 v0 = asBf16(u32x4{va[s][0], va[s][1], vb[s][0], vb[s][1]});
+        const bf16x8 v1 = asBf16(u32x4{va[s][2], va[s][3], vb[s][2], vb[s][3]});
+        acc.o[2 * s] = mfma(v0, P.hi, acc.o[2 * s]);
+        acc.o[2 * s + 1] = mfma(v1, P.hi, acc.o[2 * s + 1]);
         if constexpr (SPLIT_P) {
-            acc.o[2 * s] = mfma(v0, plo, acc.o[2 * s]);
-            acc.o[2 * s + 1] = mfma(v1, plo, acc.o[2 * s + 1]);
+            acc.o[2 * s] = mfma(v0, P.lo, acc.o[2 * s]);
+            acc.o[2 * s + 1] = mfma(v1, P.lo, acc.o[2 * s + 1]);
         }
     }
+}
+
+// Consume one page pair: scores, online softmax and P.V (see scorePair for
+// the arguments; ctx = keys in cache, whose later slots get zeroed V).
+// SPLIT_P: P enters P.V as hi + lo bf16 parts (fp32-accurate) or as one bf16.
+template <bool SPLIT_P>
+__device__ __forceinline__ void consumePair(Acc &acc, PagePair &r, const u32x4 (&qop)[4], int first_key, int pos,
+                                           int ctx, bool hasB, int grp, float scale_log2) {
+    const PairP P = scorePair<SPLIT_P>(acc, r.ka, r.kb, qop, first_key, pos, hasB, grp, scale_log2);
+    maskStaleV(r.va, r.vb, first_key, ctx, hasB, grp);
+    accumulatePV<SPLIT_P>(acc, r.va, r.vb, P);
 }
 
 // Output dims of lane (n, grp) for block i: 16*i + 4*grp + {0..3}.

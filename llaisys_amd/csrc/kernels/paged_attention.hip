@@ -4,21 +4,24 @@
 // Work unit = (query group, kv head). A query tile is 16 "columns"; column n
 // of tile t is the (query row, query head) pair number t*16+n of its
 // sequence, pairs ordered query-major: pair = qi*G + g, G = nh/nkvh query
-// heads per kv head. A group is kTiles adjacent tiles: one wave carries all of
-// them, so each K/V page pair it loads feeds kTiles x 24 MFMAs (the kernel is
-// otherwise bound by re-streaming the same pages from L2 per tile).
+// heads per kv head. A group is kTiles adjacent tiles carried by one wave.
+// A workgroup is kWaves waves on kWaves adjacent groups of one sequence and
+// kv head ("block"): each K/V page pair is read from L2 once per workgroup
+// into LDS (double buffered, one barrier per pair) and feeds kWaves x kTiles
+// x 24 MFMAs, and the waves hold no private K/V ring.
 // Query qi of a sequence with Lq new tokens sits at position ctx - Lq + qi
 // and sees keys at positions <= that (bottom-right causal alignment). A
-// unit's visible pages are cut into splits of `pages_per_split` pages; one
-// wave (one 64-lane workgroup) runs one (unit, split), streaming page pairs
-// through a two-stage register ring (loads never conditional) into the MFMA
-// step of mfma_common.hpp. A unit with one split writes its normalised
+// block's visible pages (up to its last query) are cut into splits of
+// `pages_per_split` pages; one workgroup runs one (block, split): the next
+// pair is loaded into registers while the current one is consumed from LDS
+// (loads never conditional: past the end they re-read the last pair), into
+// the MFMA step of mfma_common.hpp. A unit with one split writes its normalised
 // output; with more, each split writes a record (O, m, l) and the combine
 // kernel launched next merges them (the kernel boundary orders the records;
 // no fences, no waiting between waves).
 //
-// Workgroup ids are split-major over units padded to a multiple of 8, so all
-// splits of a unit run on one XCD and share its L2 for the unit's K/V pages.
+// Workgroup ids are split-major over blocks padded to a multiple of 8, so all
+// splits of a block run on one XCD and share its L2 for the block's K/V pages.
 #include "mfma_common.hpp"
 
 #include "../device/hip_check.hpp"
@@ -34,6 +37,7 @@ using namespace mfma;
 
 constexpr int kXcds = 8;
 constexpr int kTiles = 2;                                    // query tiles per wave
+constexpr int kWaves = 4;                                    // waves (groups) per workgroup
 constexpr int kRecordFloats = kTiles * 16 * (kHeadDim + 2); // O for the group's columns, then (m, l)
 
 struct Args {
@@ -46,87 +50,104 @@ struct Args {
     const int32_t *cu_q;
     float *records;
     int *err;
-    int B, T, nh, nkvh, G, max_pages, num_blocks, pps, max_splits, units, units_padded;
+    int B, T, nh, nkvh, G, max_pages, num_blocks, pps, max_splits, units, block_units, block_units_padded;
     float scale_log2;
 };
 
-// Sequence and group of unit-row `group_global`: groups are numbered sequence
-// by sequence, ceil(ceil(Lq*G/16)/kTiles) for each sequence with Lq >= 2
-// queries. Returns false past the last group. One wave.
-__device__ bool locateGroup(const Args &a, int group_global, int &b, int &group) {
+__device__ __forceinline__ int groupsOf(const Args &a, int bb) {
+    const int lq = a.cu_q[bb + 1] - a.cu_q[bb];
+    return lq >= 2 ? (((lq * a.G + 15) >> 4) + kTiles - 1) / kTiles : 0;
+}
+
+// Item `index` of the list where each sequence with Lq >= 2 contributes its
+// groups (blocks == false) or its blocks of kWaves groups (blocks == true):
+// its sequence b, index within the sequence, and the number of groups of the
+// sequences before b. Returns false past the last item. One wave.
+__device__ bool locate(const Args &a, int index, bool blocks, int &b, int &local, int &group_base) {
     const int lane = threadIdx.x & 63;
-    int remaining = group_global;
+    int remaining = index, groups_before = 0;
     for (int base = 0; base < a.B; base += 64) {
         const int bb = base + lane;
-        int nt = 0;
-        if (bb < a.B) {
-            const int lq = a.cu_q[bb + 1] - a.cu_q[bb];
-            nt = lq >= 2 ? (((lq * a.G + 15) >> 4) + kTiles - 1) / kTiles : 0;
-        }
-        int incl = nt;
+        const int ng = bb < a.B ? groupsOf(a, bb) : 0;
+        const int ni = blocks ? (ng + kWaves - 1) / kWaves : ng;
+        int incl = ni, gincl = ng;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(incl, off);
-            if (lane >= off) incl += y;
+            const int y = __shfl_up(incl, off), gy = __shfl_up(gincl, off);
+            if (lane >= off) {
+                incl += y;
+                gincl += gy;
+            }
         }
         const int total = __shfl(incl, 63);
         if (remaining < total) {
             const unsigned long long hit = __ballot(incl > remaining);
             const int first = __ffsll(hit) - 1;
             b = base + first;
-            group = remaining - (__shfl(incl, first) - __shfl(nt, first));
+            local = remaining - (__shfl(incl, first) - __shfl(ni, first));
+            group_base = groups_before + __shfl(gincl, first) - __shfl(ng, first);
             return true;
         }
         remaining -= total;
+        groups_before += __shfl(gincl, 63);
     }
     return false;
 }
 
-// Per-unit geometry shared by the attention and combine kernels.
+// Per-unit geometry shared by the attention and combine kernels. The visible
+// pages are those of the last query of the group's block, the same for every
+// group of a workgroup (their splits line up).
 struct TileGeom {
     int b, group, q0, Lq, ctx, npages, nsplit;
 };
 
-__device__ bool tileGeom(const Args &a, int group_global, TileGeom &t, bool report) {
-    if (!locateGroup(a, group_global, t.b, t.group)) return false;
-    t.q0 = a.cu_q[t.b];
-    t.Lq = a.cu_q[t.b + 1] - t.q0;
-    t.ctx = a.ctx[t.b];
+__device__ bool blockGeom(const Args &a, int b, int block, TileGeom &t, bool report) {
+    t.b = b;
+    t.q0 = a.cu_q[b];
+    t.Lq = a.cu_q[b + 1] - t.q0;
+    t.ctx = a.ctx[b];
     if (t.q0 < 0 || t.q0 + t.Lq > a.T || t.ctx > a.max_pages * 16 || t.Lq > t.ctx) {
         if (report && (threadIdx.x & 63) == 0) atomicOr(a.err, kErrTooLong);
         return false;
     }
-    const int qi_max = min(t.Lq - 1, ((t.group + 1) * kTiles * 16 - 1) / a.G);
-    const int kv_len = t.ctx - t.Lq + qi_max + 1; // keys some column of the group sees
+    const int qi_max = min(t.Lq - 1, ((block + 1) * kWaves * kTiles * 16 - 1) / a.G);
+    const int kv_len = t.ctx - t.Lq + qi_max + 1; // keys some column of the block sees
     t.npages = (kv_len + 15) >> 4;
     t.nsplit = (t.npages + a.pps - 1) / a.pps;
     return true;
 }
 
-template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillKernel(Args a) {
-    const int lane = threadIdx.x;
+template <bool OUT_F32>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) prefillKernel(Args a) {
+    __shared__ u32x4 kvs[2][16 * 64]; // one page pair: K a, K b, V a, V b quarters
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int n = lane & 15;
     const int grp = lane >> 4;
-    const int split = blockIdx.x / a.units_padded;
-    const int unit = blockIdx.x - split * a.units_padded;
-    if (unit >= a.units) return;
-    const int h = unit % a.nkvh;
+    const int split = blockIdx.x / a.block_units_padded;
+    const int wunit = blockIdx.x - split * a.block_units_padded;
+    if (wunit >= a.block_units) return;
+    const int h = wunit % a.nkvh;
+    int b, block, group_base;
+    if (!locate(a, wunit / a.nkvh, true, b, block, group_base)) return;
     TileGeom t;
-    if (!tileGeom(a, unit / a.nkvh, t, split == 0)) return;
+    if (!blockGeom(a, b, block, t, split == 0 && wave == 0)) return;
     const int G = a.G;
     const int p0 = split * a.pps;
     if (p0 >= t.npages) return;
     const int p1 = min(t.npages, p0 + a.pps);
+    const int group = block * kWaves + wave;        // this wave's group in the sequence
+    const bool active = group < groupsOf(a, b);
 
-    // Columns of the group's tiles.
+    // Columns of the wave's tiles.
     int qi[kTiles], g[kTiles], pos[kTiles];
     bool col_ok[kTiles];
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
-        const int pair = (t.group * kTiles + k) * 16 + n;
+        const int pair = (group * kTiles + k) * 16 + n;
         qi[k] = pair / G;
         g[k] = pair - qi[k] * G;
-        col_ok[k] = qi[k] < t.Lq;
+        col_ok[k] = active && qi[k] < t.Lq;
         pos[k] = col_ok[k] ? t.ctx - t.Lq + qi[k] : -1;
     }
 
@@ -148,9 +169,14 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillKernel(Args
     const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
     bool bad_block = false;
     const int last_pair = p0 + ((p1 - 1 - p0) & ~1);
-    // Loads for the pair starting at page pp (clamped: past the end it
-    // re-reads the last pair, so loads are never conditional).
-    auto issue = [&](PagePair &r, int pp) {
+    // The pair is 16 one-KiB quarters: slot q = page part (q / 4: K a, K b,
+    // V a, V b) and quarter (q % 4). Wave w stages slots w, w + kWaves, ...
+    // Clamped: past the end it re-reads the last pair, so loads are never
+    // conditional.
+    static_assert(16 % kWaves == 0, "the 16 quarters of a pair split evenly over the waves");
+    constexpr int kPer = 16 / kWaves;
+    u32x4 st[kPer];
+    auto stageLoad = [&](int pp) {
         pp = min(pp, last_pair);
         int ba = __builtin_amdgcn_readlane(bid, pp - p0);
         int bb = (pp + 1 < p1) ? __builtin_amdgcn_readlane(bid, pp + 1 - p0) : ba;
@@ -158,26 +184,63 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillKernel(Args
         bad_block |= bad;
         ba = bad ? 0 : ba;
         bb = bad ? 0 : bb;
-        loadPair(r, kp, vp, (size_t(ba) * a.nkvh + h) * 256, (size_t(bb) * a.nkvh + h) * 256);
+        const size_t oa = (size_t(ba) * a.nkvh + h) * 256, ob = (size_t(bb) * a.nkvh + h) * 256;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int q = wave + kWaves * j, part = q >> 2, quarter = q & 3;
+            const u32x4 *base = (part & 2) ? vp : kp;
+            st[j] = __builtin_nontemporal_load(base + ((part & 1) ? ob : oa) + quarter * 64);
+        }
+    };
+    auto stageStore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) kvs[buf][(wave + kWaves * j) * 64 + lane] = st[j];
     };
 
     Acc acc[kTiles];
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) acc[k].reset();
-    auto consume = [&](PagePair &r, int pp) {
+    stageLoad(p0);
+    stageStore(0);
+    __syncthreads();
+    stageLoad(p0 + 2);
+    for (int i = 0, pp = p0; pp < p1; ++i, pp += 2) {
+        // pair i + 1 into the other buffer (read by everyone before the last
+        // barrier), pair i + 2 into registers, then consume pair i from LDS.
+        stageStore((i + 1) & 1);
+        stageLoad(pp + 4);
+        if (active) {
+            // K of the pair, scores and P for every tile; then V, P.V: only
+            // one of K and V is live in registers at a time.
+            const u32x4 *src = kvs[i & 1];
+            const bool hasB = pp + 1 < p1;
+            PairP P[kTiles];
+            {
+                u32x4 ka[4], kb[4];
 #pragma unroll
-        for (int k = 0; k < kTiles; ++k) consumePair<OUT_F32>(acc[k], r, qop[k], pp * 16, pos[k], t.ctx, pp + 1 < p1, grp, a.scale_log2);
-    };
-    PagePair ra, rb;
-    issue(ra, p0);
-    issue(rb, p0 + 2);
-    for (int pp = p0; pp < p1; pp += 4) {
-        consume(ra, pp);
-        issue(ra, pp + 4);
-        if (pp + 2 < p1) consume(rb, pp + 2);
-        issue(rb, pp + 6);
+                for (int s = 0; s < 4; ++s) {
+                    ka[s] = src[(0 * 4 + s) * 64 + lane];
+                    kb[s] = src[(1 * 4 + s) * 64 + lane];
+                }
+#pragma unroll
+                for (int k = 0; k < kTiles; ++k)
+                    P[k] = scorePair<OUT_F32>(acc[k], ka, kb, qop[k], pp * 16, pos[k], hasB, grp, a.scale_log2);
+            }
+            u32x4 va[4], vb[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                va[s] = src[(2 * 4 + s) * 64 + lane];
+                vb[s] = src[(3 * 4 + s) * 64 + lane];
+            }
+            maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
+#pragma unroll
+            for (int k = 0; k < kTiles; ++k) accumulatePV<OUT_F32>(acc[k], va, vb, P[k]);
+        }
+        __syncthreads();
     }
     if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
+    if (!active) return;
+    const int unit = (group_base + group) * a.nkvh + h;
     float *rec = a.records + (size_t(unit) * a.max_splits + split) * kRecordFloats;
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) {
@@ -211,10 +274,12 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillCombineKern
     const int k = blockIdx.x - unit * kTiles; // tile of the group this wave merges
     if (unit >= a.units) return;
     const int h = unit % a.nkvh;
+    int b, group, group_base;
+    if (!locate(a, unit / a.nkvh, false, b, group, group_base)) return;
     TileGeom t;
-    if (!tileGeom(a, unit / a.nkvh, t, false) || t.nsplit <= 1) return;
+    if (!blockGeom(a, b, group / kWaves, t, false) || t.nsplit <= 1) return;
     const int G = a.G;
-    const int pair = (t.group * kTiles + k) * 16 + n;
+    const int pair = (group * kTiles + k) * 16 + n;
     const int qi = pair / G;
     const int g = pair - qi * G;
     const bool col_ok = qi < t.Lq;
@@ -267,15 +332,17 @@ int envInt(const char *name, int fallback) {
 
 PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages) {
     PagedAttentionPlan p{};
-    const int groups = ((T * group + 15) / 16 + kTiles - 1) / kTiles + B;
+    const int groups = ((T * group + 15) / 16 + kTiles - 1) / kTiles + B; // upper bound over the batch
     p.units = groups * nkvh;
-    p.units_padded = (p.units + kXcds - 1) / kXcds * kXcds;
+    p.units_padded = p.units;
+    p.block_units = (groups / kWaves + B) * nkvh;
+    p.block_units_padded = (p.block_units + kXcds - 1) / kXcds * kXcds;
     // Pages per split: even (pairs of pages), at most 64 (one block id per lane).
     int pps = envInt("LLAISYS_PAGES_PER_SPLIT", 64);
     pps = std::max(2, std::min(64, pps & ~1));
     p.pages_per_split = pps;
     p.max_splits = std::max(1, (max_pages + pps - 1) / pps);
-    p.partial_bytes = size_t(p.units_padded) * p.max_splits * kRecordFloats * sizeof(float);
+    p.partial_bytes = size_t(p.units) * p.max_splits * kRecordFloats * sizeof(float);
     return p;
 }
 
@@ -304,16 +371,17 @@ void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_
     a.pps = plan.pages_per_split;
     a.max_splits = plan.max_splits;
     a.units = plan.units;
-    a.units_padded = plan.units_padded;
+    a.block_units = plan.block_units;
+    a.block_units_padded = plan.block_units_padded;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const dim3 grid(plan.units_padded * plan.max_splits), block(64);
+    const dim3 grid(plan.block_units_padded * plan.max_splits), block(64 * kWaves), cblock(64);
     auto s = static_cast<hipStream_t>(stream);
     if (out_f32) {
         hipLaunchKernelGGL((prefillKernel<true>), grid, block, 0, s, a);
-        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<true>), dim3(plan.units * kTiles), block, 0, s, a);
+        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<true>), dim3(plan.units * kTiles), cblock, 0, s, a);
     } else {
         hipLaunchKernelGGL((prefillKernel<false>), grid, block, 0, s, a);
-        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<false>), dim3(plan.units * kTiles), block, 0, s, a);
+        if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<false>), dim3(plan.units * kTiles), cblock, 0, s, a);
     }
     HIP_CHECK(hipGetLastError());
 }
