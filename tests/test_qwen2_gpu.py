@@ -262,3 +262,21 @@ def test_multi_step_decode_equals_single_steps(monkeypatch, graphs):
     assert torch.equal(multi_logits, to_torch(model.logits()).cpu())
     for i in ids:
         assert seqs["a"][0].length(i) == model.length(i)
+
+
+def test_load_local_safetensors_and_generate(tmp_path):
+    # Qwen2(path) reads config.json + *.safetensors of a local HF directory (the
+    # reference's loader, python/llaisys/models/qwen2.py:12-20) and generates
+    # greedily; each generated token must be the reference's argmax wherever
+    # its top-2 margin exceeds the logit tolerance.
+    _, hf = build("tiny")
+    hf.to(torch.bfloat16).save_pretrained(tmp_path, safe_serialization=True)
+    hf.float()
+    model = Qwen2(tmp_path)
+    assert model.meta.nlayer == 2 and model.meta.voc == 1000 and model.meta.hs == 256
+    p = prompt(23, 1000, 77)
+    out = model.generate(p, max_new_tokens=6)
+    assert out[:23] == p and len(out) == 29
+    for i in range(23, 29):
+        ref = hf_logits(hf, out[:i])[-1]
+        check_token(out[i], ref, REL_TOL * ref.abs().max().item())
