@@ -193,6 +193,14 @@ def cpu_baseline_decode(inst, budget_s):
         total += time.perf_counter() - t0
         reps += 1
     sample_bytes = int(inst.ctx[:nseq].sum()) * 1024 + 2 * nseq * 12 * 128 * 2
+    # The same scalar code on one thread, over the first 4 sequences.
+    n1, reps1, total1 = min(4, len(inst.ctx)), 0, 0.0
+    while total1 < budget_s / 4:
+        t0 = time.perf_counter()
+        oracle.paged_attention(q[:n1], k_log, v_log, inst.table_np[:n1], inst.ctx[:n1], SCALE, nthreads=1)
+        total1 += time.perf_counter() - t0
+        reps1 += 1
+    bytes1 = int(inst.ctx[:n1].sum()) * 1024 + 2 * n1 * 12 * 128 * 2
     # Sanity: the GPU result for the sample agrees with the CPU result.
     got = host_copy(inst.out, torch.bfloat16, (inst.T, 12, 128))[:nseq].float().numpy()
     max_err = float(np.max(np.abs(got - ref)))
@@ -204,6 +212,11 @@ def cpu_baseline_decode(inst, budget_s):
         "sample": f"oracle/oracle.c paged attention (fp32) on the first {nseq} of {len(inst.ctx)} sequences "
                   f"({int(inst.ctx[:nseq].sum())} tokens), {reps} reps in {total:.1f} s; "
                   f"GPU bf16 vs CPU max|err| {max_err:.2e}",
+        "single_thread": {
+            "value": round(bytes1 * reps1 / total1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "sample": f"the same code with one thread on the first {n1} sequences "
+                      f"({int(inst.ctx[:n1].sum())} tokens), {reps1} reps in {total1:.1f} s",
+        },
     }
 
 
