@@ -51,6 +51,7 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--summarize", nargs=6, metavar=("STATS", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE", "TAG"),
                    help="summarise rocprofv3 output directories into profiles/TAG.md and profiles/TAG_traffic.json")
+    p.add_argument("--profiles-dir", default=str(ROOT / "profiles"), help="where the --summarize* outputs go")
     p.add_argument("--summarize-step", nargs=2, metavar=("TRACE_DIR", "TAG"),
                    help="per-step kernel table of a --workload qwen2 kernel trace into profiles/TAG.md")
     p.add_argument("--summarize-mfma", nargs=4, metavar=("STATS_DIR", "UTIL_DIR", "MOPS_DIR", "TAG"),
@@ -551,9 +552,10 @@ def summarize(args):
     print("\n".join(lines))
     out = {"tag": tag, "hbm_bytes_per_launch": int(total_bytes), "op_time_us_rocprof": round(total_us, 3),
            "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}
-    (ROOT / "profiles").mkdir(exist_ok=True)
-    (ROOT / "profiles" / f"{tag}_traffic.json").write_text(json.dumps(out, indent=1) + "\n")
-    (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
+    outdir = Path(args.profiles_dir)
+    outdir.mkdir(parents=True, exist_ok=True)
+    (outdir / f"{tag}_traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    (outdir / f"{tag}.md").write_text("\n".join(lines) + "\n")
 
 
 def summarize_step(args):
@@ -607,8 +609,9 @@ def summarize_step(args):
     for (name, grid), (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
         lines.append(f"| `{name}` | {grid} | {n / k:.0f} | {t / k:.1f} | {t / n:.2f} |")
     print("\n".join(lines))
-    (ROOT / "profiles").mkdir(exist_ok=True)
-    (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
+    outdir = Path(args.profiles_dir)
+    outdir.mkdir(parents=True, exist_ok=True)
+    (outdir / f"{tag}.md").write_text("\n".join(lines) + "\n")
 
 
 def summarize_mfma(args):
@@ -664,8 +667,9 @@ def summarize_mfma(args):
                      f"{'' if flop is None else f'{flop / 1e9:.2f}'} | {'' if tf is None else f'{tf:.1f}'} | "
                      f"{'' if tf is None else f'{100 * tf / 2500:.1f}'} |")
     print("\n".join(lines))
-    (ROOT / "profiles").mkdir(exist_ok=True)
-    (ROOT / "profiles" / f"{tag}.md").write_text("\n".join(lines) + "\n")
+    outdir = Path(args.profiles_dir)
+    outdir.mkdir(parents=True, exist_ok=True)
+    (outdir / f"{tag}.md").write_text("\n".join(lines) + "\n")
 
 
 def traffic_from_profiles(kernel_tag):
