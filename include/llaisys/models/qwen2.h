@@ -18,6 +18,9 @@
  *
  * KV cache: a pool of 16-token blocks per layer shared by all sequences, with
  * a prefix cache of full blocks keyed by their token ids.
+ *
+ * A model is driven from one thread at a time (its calls are not reentrant);
+ * work runs on that thread's context stream (llaisysGetContextStream).
  */
 __C {
     struct LlaisysQwen2Meta {

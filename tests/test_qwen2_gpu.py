@@ -280,3 +280,25 @@ def test_load_local_safetensors_and_generate(tmp_path):
     for i in range(23, 29):
         ref = hf_logits(hf, out[:i])[-1]
         check_token(out[i], ref, REL_TOL * ref.abs().max().item())
+
+
+def test_decode_graph_recaptured_after_workspace_growth(monkeypatch):
+    # A decode graph holds workspace pointers; a long prefill step in between
+    # grows (moves) the step and split workspaces, and the next decode steps
+    # must re-capture instead of replaying stale pointers.
+    monkeypatch.setenv("LLAISYS_QWEN2_GRAPHS", "1")
+    model, hf = build("tiny", num_blocks=256)
+    a, _ = model.create_sequence()
+    pa = prompt(20, model.meta.voc, 90)
+    nxt = model.step([a], [pa])[0]
+    hist = pa + [nxt]
+    for _ in range(3):  # capture + replays at batch 1
+        nxt = model.step([a], [[hist[-1]]])[0]
+        hist.append(nxt)
+    b, _ = model.create_sequence()
+    model.step([b], [prompt(700, model.meta.voc, 91)])  # 700-token prefill: larger workspaces
+    for _ in range(3):
+        nxt = model.step([a], [[hist[-1]]])[0]
+        ref = hf_logits(hf, hist)[-1]
+        check_token(nxt, ref, check_logits(to_torch(model.logits())[0], ref))
+        hist.append(nxt)
