@@ -38,6 +38,7 @@ using namespace mfma;
 constexpr int kXcds = 8;
 constexpr int kTiles = 2;                                    // query tiles per wave
 constexpr int kWaves = 4;                                    // waves (groups) per workgroup
+constexpr int kStagePairs = 2;                               // page pairs per LDS stage (one barrier each)
 constexpr int kRecordFloats = kTiles * 16 * (kHeadDim + 2); // O for the group's columns, then (m, l)
 
 struct Args {
@@ -119,7 +120,7 @@ __device__ bool blockGeom(const Args &a, int b, int block, TileGeom &t, bool rep
 
 template <bool OUT_F32>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) prefillKernel(Args a) {
-    __shared__ u32x4 kvs[2][16 * 64]; // one page pair: K a, K b, V a, V b quarters
+    __shared__ u32x4 kvs[2][kStagePairs * 16 * 64]; // page pairs: K a, K b, V a, V b quarters
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int n = lane & 15;
@@ -175,66 +176,77 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // conditional.
     static_assert(16 % kWaves == 0, "the 16 quarters of a pair split evenly over the waves");
     constexpr int kPer = 16 / kWaves;
-    u32x4 st[kPer];
-    auto stageLoad = [&](int pp) {
-        pp = min(pp, last_pair);
-        int ba = __builtin_amdgcn_readlane(bid, pp - p0);
-        int bb = (pp + 1 < p1) ? __builtin_amdgcn_readlane(bid, pp + 1 - p0) : ba;
-        const bool bad = unsigned(ba) >= unsigned(a.num_blocks) || unsigned(bb) >= unsigned(a.num_blocks);
-        bad_block |= bad;
-        ba = bad ? 0 : ba;
-        bb = bad ? 0 : bb;
-        const size_t oa = (size_t(ba) * a.nkvh + h) * 256, ob = (size_t(bb) * a.nkvh + h) * 256;
+    u32x4 st[kStagePairs][kPer];
+    auto stageLoad = [&](int pp) { // the kStagePairs pairs from page pp
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int q = wave + kWaves * j, part = q >> 2, quarter = q & 3;
-            const u32x4 *base = (part & 2) ? vp : kp;
-            st[j] = __builtin_nontemporal_load(base + ((part & 1) ? ob : oa) + quarter * 64);
+        for (int sp = 0; sp < kStagePairs; ++sp) {
+            const int q0 = min(pp + 2 * sp, last_pair);
+            int ba = __builtin_amdgcn_readlane(bid, q0 - p0);
+            int bb = (q0 + 1 < p1) ? __builtin_amdgcn_readlane(bid, q0 + 1 - p0) : ba;
+            const bool bad = unsigned(ba) >= unsigned(a.num_blocks) || unsigned(bb) >= unsigned(a.num_blocks);
+            bad_block |= bad;
+            ba = bad ? 0 : ba;
+            bb = bad ? 0 : bb;
+            const size_t oa = (size_t(ba) * a.nkvh + h) * 256, ob = (size_t(bb) * a.nkvh + h) * 256;
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const int q = wave + kWaves * j, part = q >> 2, quarter = q & 3;
+                const u32x4 *base = (part & 2) ? vp : kp;
+                st[sp][j] = __builtin_nontemporal_load(base + ((part & 1) ? ob : oa) + quarter * 64);
+            }
         }
     };
     auto stageStore = [&](int buf) {
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) kvs[buf][(wave + kWaves * j) * 64 + lane] = st[j];
+        for (int sp = 0; sp < kStagePairs; ++sp)
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) kvs[buf][(sp * 16 + wave + kWaves * j) * 64 + lane] = st[sp][j];
     };
 
     Acc acc[kTiles];
 #pragma unroll
     for (int k = 0; k < kTiles; ++k) acc[k].reset();
+    constexpr int kStagePages = 2 * kStagePairs;
     stageLoad(p0);
     stageStore(0);
     __syncthreads();
-    stageLoad(p0 + 2);
-    for (int i = 0, pp = p0; pp < p1; ++i, pp += 2) {
-        // pair i + 1 into the other buffer (read by everyone before the last
-        // barrier), pair i + 2 into registers, then consume pair i from LDS.
+    stageLoad(p0 + kStagePages);
+    for (int i = 0, ps = p0; ps < p1; ++i, ps += kStagePages) {
+        // stage i + 1 into the other buffer (read by everyone before the last
+        // barrier), stage i + 2 into registers, then consume stage i from LDS.
         stageStore((i + 1) & 1);
-        stageLoad(pp + 4);
+        stageLoad(ps + 2 * kStagePages);
         if (active) {
-            // K of the pair, scores and P for every tile; then V, P.V: only
-            // one of K and V is live in registers at a time.
-            const u32x4 *src = kvs[i & 1];
-            const bool hasB = pp + 1 < p1;
-            PairP P[kTiles];
-            {
-                u32x4 ka[4], kb[4];
+#pragma unroll
+            for (int sp = 0; sp < kStagePairs; ++sp) {
+                const int pp = ps + 2 * sp;
+                if (pp >= p1) break;
+                // K of the pair, scores and P for every tile; then V, P.V: only
+                // one of K and V is live in registers at a time.
+                const u32x4 *src = kvs[i & 1] + sp * 16 * 64;
+                const bool hasB = pp + 1 < p1;
+                PairP P[kTiles];
+                {
+                    u32x4 ka[4], kb[4];
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        ka[s] = src[(0 * 4 + s) * 64 + lane];
+                        kb[s] = src[(1 * 4 + s) * 64 + lane];
+                    }
+#pragma unroll
+                    for (int k = 0; k < kTiles; ++k)
+                        P[k] = scorePair<OUT_F32>(acc[k], ka, kb, qop[k], pp * 16, pos[k], hasB, grp, a.scale_log2);
+                }
+                u32x4 va[4], vb[4];
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    ka[s] = src[(0 * 4 + s) * 64 + lane];
-                    kb[s] = src[(1 * 4 + s) * 64 + lane];
+                    va[s] = src[(2 * 4 + s) * 64 + lane];
+                    vb[s] = src[(3 * 4 + s) * 64 + lane];
                 }
+                maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
 #pragma unroll
-                for (int k = 0; k < kTiles; ++k)
-                    P[k] = scorePair<OUT_F32>(acc[k], ka, kb, qop[k], pp * 16, pos[k], hasB, grp, a.scale_log2);
+                for (int k = 0; k < kTiles; ++k) accumulatePV<OUT_F32>(acc[k], va, vb, P[k]);
             }
-            u32x4 va[4], vb[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                va[s] = src[(2 * 4 + s) * 64 + lane];
-                vb[s] = src[(3 * 4 + s) * 64 + lane];
-            }
-            maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
-#pragma unroll
-            for (int k = 0; k < kTiles; ++k) accumulatePV<OUT_F32>(acc[k], va, vb, P[k]);
         }
         __syncthreads();
     }
