@@ -83,10 +83,13 @@ struct PairP {
 // Scores of one page pair (K pages a, b) against the lane's column, online
 // softmax update of acc (max, sum, rescaled O) and the pair's P. first_key =
 // key position of page A's token 0; pos = last key this lane's column may
-// see (-1: none); hasB = page B exists.
+// see (-1: none); hasB = page B exists. full = every key of the pair is
+// visible to every column of the wave (wave-uniform; the caller knows it for
+// all but the diagonal and last pairs): no per-key mask.
 template <bool SPLIT_P>
 __device__ __forceinline__ PairP scorePair(Acc &acc, const u32x4 (&ka)[4], const u32x4 (&kb)[4], const u32x4 (&qop)[4],
-                                          int first_key, int pos, bool hasB, int grp, float scale_log2) {
+                                          int first_key, int pos, bool hasB, int grp, float scale_log2,
+                                          bool full = false) {
     f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -95,10 +98,18 @@ __device__ __forceinline__ PairP scorePair(Acc &acc, const u32x4 (&ka)[4], const
     }
     const int kbase = first_key + grp * 4;
     float sv[8];
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        sv[i] = (kbase + i <= pos) ? sa[i] * scale_log2 : -INFINITY;
-        sv[4 + i] = (hasB && kbase + 16 + i <= pos) ? sb[i] * scale_log2 : -INFINITY;
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = sa[i] * scale_log2;
+            sv[4 + i] = sb[i] * scale_log2;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = (kbase + i <= pos) ? sa[i] * scale_log2 : -INFINITY;
+            sv[4 + i] = (hasB && kbase + 16 + i <= pos) ? sb[i] * scale_log2 : -INFINITY;
+        }
     }
     float mloc = sv[0];
 #pragma unroll

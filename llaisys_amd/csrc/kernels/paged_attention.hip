@@ -152,6 +152,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         pos[k] = col_ok[k] ? t.ctx - t.Lq + qi[k] : -1;
     }
 
+    // Smallest causal limit among the wave's real columns (wave-uniform).
+    int min_pos = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < kTiles; ++k) min_pos = min(min_pos, col_ok[k] ? pos[k] : 0x7fffffff);
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) min_pos = min(min_pos, __shfl_xor(min_pos, off));
+    min_pos = __builtin_amdgcn_readfirstlane(min_pos);
+
     int bid = 0;
     if (lane < p1 - p0) bid = a.table[size_t(t.b) * a.max_pages + p0 + lane];
 
@@ -225,6 +233,9 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                 // one of K and V is live in registers at a time.
                 const u32x4 *src = kvs[i & 1] + sp * 16 * 64;
                 const bool hasB = pp + 1 < p1;
+                // Every key of the pair visible to every column of the wave
+                // (no causal cut, no stale slots): the score and V masks drop.
+                const bool full = hasB && pp * 16 + 31 <= min_pos && pp * 16 + 32 <= t.ctx;
                 PairP P[kTiles];
                 {
                     u32x4 ka[4], kb[4];
@@ -235,7 +246,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                     }
 #pragma unroll
                     for (int k = 0; k < kTiles; ++k)
-                        P[k] = scorePair<OUT_F32>(acc[k], ka, kb, qop[k], pp * 16, pos[k], hasB, grp, a.scale_log2);
+                        P[k] = scorePair<OUT_F32>(acc[k], ka, kb, qop[k], pp * 16, pos[k], hasB, grp, a.scale_log2,
+                                                  full);
                 }
                 u32x4 va[4], vb[4];
 #pragma unroll
@@ -243,7 +255,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                     va[s] = src[(2 * 4 + s) * 64 + lane];
                     vb[s] = src[(3 * 4 + s) * 64 + lane];
                 }
-                maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
+                if (!full) maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
 #pragma unroll
                 for (int k = 0; k < kTiles; ++k) accumulatePV<OUT_F32>(acc[k], va, vb, P[k]);
             }
