@@ -80,16 +80,14 @@ struct PairP {
     bf16x8 hi, lo;
 };
 
-// Scores of one page pair (K pages a, b) against the lane's column, online
-// softmax update of acc (max, sum, rescaled O) and the pair's P. first_key =
-// key position of page A's token 0; pos = last key this lane's column may
-// see (-1: none); hasB = page B exists. full = every key of the pair is
-// visible to every column of the wave (wave-uniform; the caller knows it for
-// all but the diagonal and last pairs): no per-key mask.
-template <bool SPLIT_P>
-__device__ __forceinline__ PairP scorePair(Acc &acc, const u32x4 (&ka)[4], const u32x4 (&kb)[4], const u32x4 (&qop)[4],
-                                          int first_key, int pos, bool hasB, int grp, float scale_log2,
-                                          bool full = false) {
+// Raw scores of one page pair (K pages a, b) against the lane's column, with
+// keys the column may not see set to -inf. first_key = key position of page
+// A's token 0; pos = last key this lane's column may see (-1: none); hasB =
+// page B exists. full = every key of the pair is visible to every column of
+// the wave (wave-uniform): no per-key mask.
+__device__ __forceinline__ void pairScores(float (&sv)[8], const u32x4 (&ka)[4], const u32x4 (&kb)[4],
+                                           const u32x4 (&qop)[4], int first_key, int pos, bool hasB, int grp,
+                                           bool full = false) {
     f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -97,48 +95,55 @@ __device__ __forceinline__ PairP scorePair(Acc &acc, const u32x4 (&ka)[4], const
         sb = mfma(asBf16(kb[s]), asBf16(qop[s]), sb);
     }
     const int kbase = first_key + grp * 4;
-    float sv[8];
-    if (full) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sv[i] = sa[i] * scale_log2;
-            sv[4 + i] = sb[i] * scale_log2;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sv[i] = (kbase + i <= pos) ? sa[i] * scale_log2 : -INFINITY;
-            sv[4 + i] = (hasB && kbase + 16 + i <= pos) ? sb[i] * scale_log2 : -INFINITY;
-        }
+    for (int i = 0; i < 4; ++i) {
+        sv[i] = (full || kbase + i <= pos) ? sa[i] : -INFINITY;
+        sv[4 + i] = (full || (hasB && kbase + 16 + i <= pos)) ? sb[i] : -INFINITY;
     }
-    float mloc = sv[0];
+}
+
+// Online softmax over the raw scores of NP page pairs: update acc (running
+// max in log2 units, sum, rescaled O) and return each pair's P. Scores enter
+// as exp2(s * scale_log2 - m): the max is taken on raw scores (the scale is
+// positive) and the scaling folds into one fma per key.
+template <bool SPLIT_P, int NP>
+__device__ __forceinline__ void softmaxUpdate(Acc &acc, const float (&sv)[NP][8], PairP (&P)[NP], float scale_log2) {
+    float mloc = sv[0][0];
 #pragma unroll
-    for (int i = 1; i < 8; ++i) mloc = fmaxf(mloc, sv[i]);
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mloc = fmaxf(mloc, sv[j][i]);
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(acc.m, mloc);
+    const float m_new = fmaxf(acc.m, mloc * scale_log2);
     const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
     const float alpha = exp2Fast(acc.m - m_use);
-    float p[8];
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        p[i] = exp2Fast(sv[i] - m_use);
-        psum += p[i];
-    }
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float p = exp2Fast(__builtin_fmaf(sv[j][i], scale_log2, -m_use));
+            psum += p;
+            const __bf16 hi = (__bf16)p;
+            P[j].hi[i] = hi;
+            if constexpr (SPLIT_P) P[j].lo[i] = (__bf16)(p - (float)hi);
+        }
     acc.l = acc.l * alpha + psum;
     acc.m = m_new;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc.o[i] *= alpha;
+}
 
-    PairP P;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const __bf16 hi = (__bf16)p[i];
-        P.hi[i] = hi;
-        if constexpr (SPLIT_P) P.lo[i] = (__bf16)(p[i] - (float)hi);
-    }
-    return P;
+// Scores, online softmax update and P of one page pair (see pairScores).
+template <bool SPLIT_P>
+__device__ __forceinline__ PairP scorePair(Acc &acc, const u32x4 (&ka)[4], const u32x4 (&kb)[4], const u32x4 (&qop)[4],
+                                          int first_key, int pos, bool hasB, int grp, float scale_log2) {
+    float sv[1][8];
+    pairScores(sv[0], ka, kb, qop, first_key, pos, hasB, grp);
+    PairP P[1];
+    softmaxUpdate<SPLIT_P, 1>(acc, sv, P, scale_log2);
+    return P[0];
 }
 
 // Keys at or past ctx may hold stale bytes (even NaN patterns): zero their V

@@ -131,14 +131,22 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const int h = wunit % a.nkvh;
     int b, block, group_base;
     if (!locate(a, wunit / a.nkvh, true, b, block, group_base)) return;
+    b = __builtin_amdgcn_readfirstlane(b);
+    block = __builtin_amdgcn_readfirstlane(block);
+    group_base = __builtin_amdgcn_readfirstlane(group_base);
     TileGeom t;
     if (!blockGeom(a, b, block, t, split == 0 && wave == 0)) return;
+    // The geometry is wave-uniform: scalar registers, scalar branches.
+    t.q0 = __builtin_amdgcn_readfirstlane(t.q0);
+    t.Lq = __builtin_amdgcn_readfirstlane(t.Lq);
+    t.ctx = __builtin_amdgcn_readfirstlane(t.ctx);
+    t.npages = __builtin_amdgcn_readfirstlane(t.npages);
     const int G = a.G;
     const int p0 = split * a.pps;
     if (p0 >= t.npages) return;
     const int p1 = min(t.npages, p0 + a.pps);
     const int group = block * kWaves + wave;        // this wave's group in the sequence
-    const bool active = group < groupsOf(a, b);
+    const bool active = group < __builtin_amdgcn_readfirstlane(groupsOf(a, b));
 
     // Columns of the wave's tiles.
     int qi[kTiles], g[kTiles], pos[kTiles];
@@ -160,8 +168,15 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     for (int off = 1; off < 64; off <<= 1) min_pos = min(min_pos, __shfl_xor(min_pos, off));
     min_pos = __builtin_amdgcn_readfirstlane(min_pos);
 
-    int bid = 0;
-    if (lane < p1 - p0) bid = a.table[size_t(t.b) * a.max_pages + p0 + lane];
+    // Block ids of the split's pages: page p0 + i in lane i % 64 of bid[i / 64].
+    int bid[2] = {0, 0};
+#pragma unroll
+    for (int w = 0; w < 2; ++w)
+        if (lane + 64 * w < p1 - p0) bid[w] = a.table[size_t(t.b) * a.max_pages + p0 + 64 * w + lane];
+    auto blockOf = [&](int page) {
+        const int i = page - p0;
+        return i < 64 ? __builtin_amdgcn_readlane(bid[0], i) : __builtin_amdgcn_readlane(bid[1], i - 64);
+    };
 
     u32x4 qop[kTiles][4];
 #pragma unroll
@@ -189,8 +204,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int sp = 0; sp < kStagePairs; ++sp) {
             const int q0 = min(pp + 2 * sp, last_pair);
-            int ba = __builtin_amdgcn_readlane(bid, q0 - p0);
-            int bb = (q0 + 1 < p1) ? __builtin_amdgcn_readlane(bid, q0 + 1 - p0) : ba;
+            int ba = blockOf(q0);
+            int bb = (q0 + 1 < p1) ? blockOf(q0 + 1) : ba;
             const bool bad = unsigned(ba) >= unsigned(a.num_blocks) || unsigned(bb) >= unsigned(a.num_blocks);
             bad_block |= bad;
             ba = bad ? 0 : ba;
@@ -225,19 +240,25 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         stageStore((i + 1) & 1);
         stageLoad(ps + 2 * kStagePages);
         if (active) {
+            // Per softmax group of kSoft pairs: scores of each pair for every
+            // tile (K of one pair live at a time), one softmax update per tile
+            // over the group's keys, then P.V pair by pair (V of one pair live
+            // at a time). fp32 outputs carry P as hi + lo, which leaves
+            // registers for one pair per group only.
+            constexpr int kSoft = OUT_F32 ? 1 : kStagePairs;
+            const u32x4 *stage = kvs[i & 1];
 #pragma unroll
-            for (int sp = 0; sp < kStagePairs; ++sp) {
-                const int pp = ps + 2 * sp;
-                if (pp >= p1) break;
-                // K of the pair, scores and P for every tile; then V, P.V: only
-                // one of K and V is live in registers at a time.
-                const u32x4 *src = kvs[i & 1] + sp * 16 * 64;
-                const bool hasB = pp + 1 < p1;
-                // Every key of the pair visible to every column of the wave
-                // (no causal cut, no stale slots): the score and V masks drop.
-                const bool full = hasB && pp * 16 + 31 <= min_pos && pp * 16 + 32 <= t.ctx;
-                PairP P[kTiles];
-                {
+            for (int sg = 0; sg < kStagePairs; sg += kSoft) {
+                if (ps + 2 * sg >= p1) break;
+                float sv[kTiles][kSoft][8];
+#pragma unroll
+                for (int j = 0; j < kSoft; ++j) {
+                    const int pp = ps + 2 * (sg + j);
+                    const u32x4 *src = stage + (sg + j) * 16 * 64;
+                    const bool hasA = pp < p1, hasB = pp + 1 < p1;
+                    // Every key of the pair visible to every column of the
+                    // wave (no causal cut, no stale slots): no per-key mask.
+                    const bool full = hasB && pp * 16 + 31 <= min_pos && pp * 16 + 32 <= t.ctx;
                     u32x4 ka[4], kb[4];
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
@@ -246,18 +267,27 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                     }
 #pragma unroll
                     for (int k = 0; k < kTiles; ++k)
-                        P[k] = scorePair<OUT_F32>(acc[k], ka, kb, qop[k], pp * 16, pos[k], hasB, grp, a.scale_log2,
-                                                  full);
+                        pairScores(sv[k][j], ka, kb, qop[k], pp * 16, hasA ? pos[k] : -1, hasB, grp, full);
                 }
-                u32x4 va[4], vb[4];
+                PairP P[kTiles][kSoft];
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    va[s] = src[(2 * 4 + s) * 64 + lane];
-                    vb[s] = src[(3 * 4 + s) * 64 + lane];
+                for (int k = 0; k < kTiles; ++k) softmaxUpdate<OUT_F32, kSoft>(acc[k], sv[k], P[k], a.scale_log2);
+#pragma unroll
+                for (int j = 0; j < kSoft; ++j) {
+                    const int pp = ps + 2 * (sg + j);
+                    if (pp >= p1) break;
+                    const u32x4 *src = stage + (sg + j) * 16 * 64;
+                    const bool hasB = pp + 1 < p1;
+                    u32x4 va[4], vb[4];
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        va[s] = src[(2 * 4 + s) * 64 + lane];
+                        vb[s] = src[(3 * 4 + s) * 64 + lane];
+                    }
+                    maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
+#pragma unroll
+                    for (int k = 0; k < kTiles; ++k) accumulatePV<OUT_F32>(acc[k], va, vb, P[k][j]);
                 }
-                if (!full) maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
-#pragma unroll
-                for (int k = 0; k < kTiles; ++k) accumulatePV<OUT_F32>(acc[k], va, vb, P[k]);
             }
         }
         __syncthreads();
@@ -361,9 +391,9 @@ PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages)
     p.units_padded = p.units;
     p.block_units = (groups / kWaves + B) * nkvh;
     p.block_units_padded = (p.block_units + kXcds - 1) / kXcds * kXcds;
-    // Pages per split: even (pairs of pages), at most 64 (one block id per lane).
+    // Pages per split: even (pairs of pages), at most 128 (two block ids per lane).
     int pps = envInt("LLAISYS_PAGES_PER_SPLIT", 64);
-    pps = std::max(2, std::min(64, pps & ~1));
+    pps = std::max(2, std::min(128, pps & ~1));
     p.pages_per_split = pps;
     p.max_splits = std::max(1, (max_pages + pps - 1) / pps);
     p.partial_bytes = size_t(p.units) * p.max_splits * kRecordFloats * sizeof(float);
