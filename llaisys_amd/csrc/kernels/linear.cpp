@@ -19,6 +19,7 @@
 #include "../common.hpp"
 #include "../device/hip_check.hpp"
 
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
@@ -27,6 +28,7 @@
 #include <memory>
 #include <tuple>
 #include <unordered_map>
+#include <vector>
 
 namespace llaisys::kernels {
 
@@ -45,7 +47,9 @@ namespace {
     } while (0)
 
 constexpr int kTuneMaxM = 256;          // autotune decode-sized GEMMs only
-constexpr int kTuneCandidates = 16;
+constexpr int kTuneCandidates = 16;      // heuristic candidates timed per shape
+constexpr int kTuneCandidatesWide = 64;  // ... for weight matrices of >= kWideElems elements
+constexpr long long kWideElems = 1 << 20;
 constexpr size_t kWorkspaceBytes = 32u << 20;
 constexpr size_t kFlushBytes = size_t(512) << 20;   // > L2 + MALL
 
@@ -154,14 +158,31 @@ LtGemm &prepare(LtContext &ctx, ElemType t, int M, int N, int K, const void *bia
     LT_CHECK(hipblasLtMatmulPreferenceCreate(&pref));
     const uint64_t wsz = kWorkspaceBytes;
     LT_CHECK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof(wsz)));
-    hipblasLtMatmulHeuristicResult_t res[kTuneCandidates];
+    // The large decode-step weight GEMMs search wider (measured 4.5 % faster
+    // for the Qwen2-1.5B step); small shapes keep the short list.
+    const int want = (long long)N * K >= kWideElems ? kTuneCandidatesWide : kTuneCandidates;
+    std::vector<hipblasLtMatmulHeuristicResult_t> res(want);
     int got = 0;
-    const hipblasStatus_t hs = hipblasLtMatmulAlgoGetHeuristic(ctx.handle, g.desc, g.a, g.b, g.c, g.c, pref,
-                                                               kTuneCandidates, res, &got);
+    const hipblasStatus_t hs = hipblasLtMatmulAlgoGetHeuristic(ctx.handle, g.desc, g.a, g.b, g.c, g.c, pref, want,
+                                                               res.data(), &got);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (hs != HIPBLAS_STATUS_SUCCESS || got <= 0) return g; // rocBLAS fallback
-    g.algo = res[0].algo;
+    // Only candidates the library confirms for this problem and workspace run.
+    std::vector<hipblasLtMatmulAlgo_t> algos;
+    for (int i = 0; i < got; ++i) {
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspaceBytes) continue;
+        const float one = 1.f;
+        size_t need = 0;
+        if (hipblaslt_ext::matmulIsAlgoSupported(ctx.handle, g.desc, &one, g.a, g.b, &one, g.c, g.c, res[i].algo,
+                                                 need) != HIPBLAS_STATUS_SUCCESS ||
+            need > kWorkspaceBytes)
+            continue;
+        algos.push_back(res[i].algo);
+    }
+    if (algos.empty()) return g; // rocBLAS fallback
+    g.algo = algos[0];
     g.ok = true;
+    got = int(algos.size());
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     HIP_CHECK(hipStreamIsCapturing(s, &capture));
     if (got == 1 || M > kTuneMaxM || !autotuneEnabled() || capture != hipStreamCaptureStatusNone) return g;
@@ -186,12 +207,12 @@ LtGemm &prepare(LtContext &ctx, ElemType t, int M, int N, int K, const void *bia
     for (int i = 0; i < got; ++i) {
         const float alpha = 1.f, beta = 0.f;
         if (hipblasLtMatmul(ctx.handle, g.desc, &alpha, w, g.a, x, g.b, &beta, ctx.scratch, g.c, ctx.scratch, g.c,
-                            &res[i].algo, ctx.workspace, kWorkspaceBytes, s) != HIPBLAS_STATUS_SUCCESS)
+                            &algos[i], ctx.workspace, kWorkspaceBytes, s) != HIPBLAS_STATUS_SUCCESS)
             continue;
         for (int r = 0; r < kReps; ++r) {
             HIP_CHECK(hipMemsetAsync(flush, r, kFlushBytes, s));
             HIP_CHECK(hipEventRecord(ev[2 * r], s));
-            runLt(ctx, g, res[i].algo, ctx.scratch, x, w, 0.f, s);
+            runLt(ctx, g, algos[i], ctx.scratch, x, w, 0.f, s);
             HIP_CHECK(hipEventRecord(ev[2 * r + 1], s));
         }
         HIP_CHECK(hipEventSynchronize(ev[2 * kReps - 1]));
@@ -203,7 +224,7 @@ LtGemm &prepare(LtContext &ctx, ElemType t, int M, int N, int K, const void *bia
         }
         if (total < best) {
             best = total;
-            g.algo = res[i].algo;
+            g.algo = algos[i];
         }
     }
     for (auto &e : ev) HIP_CHECK(hipEventDestroy(e));
