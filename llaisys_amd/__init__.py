@@ -9,6 +9,7 @@ from .libllaisys import llaisysStream_t as Stream
 from .kv_cache import KVBlockManager
 from . import models
 from .ops import Ops
+from .serving import RequestStatus, Scheduler
 from .runtime import RuntimeAPI, context_stream, device_error_flags, set_context_runtime, set_context_stream
 from .tensor import Tensor
 
@@ -21,6 +22,8 @@ __all__ = [
     "Tensor",
     "Ops",
     "KVBlockManager",
+    "Scheduler",
+    "RequestStatus",
     "models",
     "LlaisysError",
     "set_context_runtime",

@@ -7,6 +7,7 @@
 #include "llaisys/models/qwen2.h"
 #include "llaisys/ops.h"
 #include "llaisys/runtime.h"
+#include "llaisys/serving.h"
 #include "llaisys/tensor.h"
 
 #include "common.hpp"
@@ -15,6 +16,7 @@
 #include "kvcache/block_manager.hpp"
 #include "models/qwen2.hpp"
 #include "ops/ops.hpp"
+#include "serving/scheduler.hpp"
 #include "tensor/tensor.hpp"
 
 #include <algorithm>
@@ -33,6 +35,12 @@ struct LlaisysKVBlockManager {
 // The model plus the handle boxes of its weights. `orig` keeps the boxes the
 // model handed out, so handles a caller swapped into `w` can be detected and
 // copied into the model's own tensors.
+struct LlaisysScheduler {
+    std::unique_ptr<llaisys::serving::Backend> backend;
+    std::unique_ptr<llaisys::serving::Scheduler> sched; // destroyed first
+    ~LlaisysScheduler() { sched.reset(); }
+};
+
 struct LlaisysQwen2Model {
     std::unique_ptr<llaisys::models::Qwen2Model> impl;
     LlaisysQwen2Weights w{};
@@ -153,6 +161,26 @@ llaisys::models::Qwen2Model &model(LlaisysQwen2Model *m) {
     LLAISYS_CHECK(m && m->impl, "qwen2: null model");
     return *m->impl;
 }
+
+// The scheduler's view of a Qwen2 model: its sequences, KV pool and step
+// (weights replaced by the caller are copied in first, as in ModelStep).
+class Qwen2Backend : public llaisys::serving::Backend {
+public:
+    explicit Qwen2Backend(LlaisysQwen2Model *m) : m_(m) {}
+    int64_t seqCreate(const int64_t *tokens, size_t n, size_t *reused) override {
+        return model(m_).seqCreate(tokens, n, reused);
+    }
+    void seqFree(int64_t id) override { model(m_).seqFree(id); }
+    int64_t numFreeBlocks() override { return int64_t(model(m_).numFreeBlocks()); }
+    size_t maxSeqLen() override { return model(m_).config().maxseq; }
+    void step(const int64_t *ids, size_t nseq, const int64_t *tokens, const size_t *ntokens, int64_t *next) override {
+        syncWeights(*m_);
+        model(m_).step(ids, nseq, tokens, ntokens, next);
+    }
+
+private:
+    LlaisysQwen2Model *m_;
+};
 
 } // namespace
 
@@ -481,6 +509,100 @@ int llaisysQwen2ModelDecode(LlaisysQwen2Model *m, const int64_t *seq_ids, size_t
 
 llaisysTensor_t llaisysQwen2ModelLogits(LlaisysQwen2Model *m) {
     return guarded([&] { return new LlaisysTensor{model(m).lastLogits()}; }, static_cast<llaisysTensor_t>(nullptr));
+}
+
+
+// ---------------------------------------------------------------- scheduler
+
+namespace {
+llaisys::serving::Scheduler &sched(LlaisysScheduler *s) {
+    if (!s || !s->sched) LLAISYS_RAISE("scheduler: null handle");
+    return *s->sched;
+}
+llaisys::serving::SchedulerConfig schedConfig(size_t max_seqs, size_t max_step_tokens, size_t prefill_chunk) {
+    llaisys::serving::SchedulerConfig c;
+    c.max_seqs = max_seqs;
+    c.max_step_tokens = max_step_tokens;
+    c.prefill_chunk = prefill_chunk;
+    return c;
+}
+} // namespace
+
+LlaisysScheduler *llaisysQwen2SchedulerCreate(LlaisysQwen2Model *m, size_t max_seqs, size_t max_step_tokens,
+                                              size_t prefill_chunk) {
+    return guarded(
+        [&] {
+            model(m);
+            auto s = std::make_unique<LlaisysScheduler>();
+            s->backend = std::make_unique<Qwen2Backend>(m);
+            s->sched = std::make_unique<llaisys::serving::Scheduler>(
+                *s->backend, schedConfig(max_seqs, max_step_tokens, prefill_chunk));
+            return s.release();
+        },
+        static_cast<LlaisysScheduler *>(nullptr));
+}
+
+LlaisysScheduler *llaisysSimSchedulerCreate(size_t num_blocks, int64_t vocab, size_t max_seq_len, size_t max_seqs,
+                                            size_t max_step_tokens, size_t prefill_chunk) {
+    return guarded(
+        [&] {
+            LLAISYS_CHECK(num_blocks <= size_t(1) << 30, "sim scheduler: num_blocks too large");
+            auto s = std::make_unique<LlaisysScheduler>();
+            s->backend = std::make_unique<llaisys::serving::SimBackend>(int(num_blocks), vocab, max_seq_len);
+            s->sched = std::make_unique<llaisys::serving::Scheduler>(
+                *s->backend, schedConfig(max_seqs, max_step_tokens, prefill_chunk));
+            return s.release();
+        },
+        static_cast<LlaisysScheduler *>(nullptr));
+}
+
+void llaisysSchedulerDestroy(LlaisysScheduler *s) {
+    guardedVoid([&] { delete s; });
+}
+
+int64_t llaisysSchedulerAdd(LlaisysScheduler *s, const int64_t *prompt, size_t nprompt, size_t max_new_tokens,
+                            int64_t eos) {
+    return guarded([&] { return sched(s).add(prompt, nprompt, max_new_tokens, eos); }, int64_t(-1));
+}
+
+int64_t llaisysSchedulerStep(LlaisysScheduler *s) {
+    return guarded([&] { return int64_t(sched(s).step()); }, int64_t(-1));
+}
+
+int llaisysSchedulerStatus(LlaisysScheduler *s, int64_t request) {
+    return guarded(
+        [&] {
+            auto &sc = sched(s);
+            if (!sc.known(request)) return -1;
+            return sc.finished(request) ? int(sc.reason(request)) : int(LLAISYS_REQUEST_ACTIVE);
+        },
+        -1);
+}
+
+int64_t llaisysSchedulerTokens(LlaisysScheduler *s, int64_t request, int64_t *out, size_t capacity) {
+    return guarded(
+        [&] {
+            const auto &t = sched(s).generated(request);
+            if (out) std::copy_n(t.begin(), std::min(capacity, t.size()), out);
+            return int64_t(t.size());
+        },
+        int64_t(-1));
+}
+
+int llaisysSchedulerRelease(LlaisysScheduler *s, int64_t request) {
+    return guarded([&] { sched(s).release(request); return 0; }, -1);
+}
+
+int llaisysSchedulerStats(LlaisysScheduler *s, int64_t *out) {
+    return guarded(
+        [&] {
+            LLAISYS_CHECK(out, "scheduler stats: null output");
+            const auto &st = sched(s).stats();
+            const int64_t v[5] = {st.steps, st.preemptions, st.prefill_tokens, st.decode_tokens, st.finished};
+            std::copy_n(v, 5, out);
+            return 0;
+        },
+        -1);
 }
 
 } // extern "C"

@@ -23,6 +23,7 @@ from .kv_cache import load_kv_cache, llaisysKVBlockManager_t
 from .qwen2 import LlaisysQwen2Meta, LlaisysQwen2Weights, llaisysQwen2Model_t, load_qwen2
 from .ops import load_ops
 from .runtime import LlaisysRuntimeAPI, load_runtime
+from .serving import llaisysScheduler_t, load_serving
 from .tensor import llaisysTensor_t, load_tensor
 
 # LLAISYS_LIBRARY may name another build of the same library (e.g. a tuning variant).
@@ -71,6 +72,7 @@ load_tensor(LIB_LLAISYS)
 load_ops(LIB_LLAISYS)
 load_kv_cache(LIB_LLAISYS)
 load_qwen2(LIB_LLAISYS)
+load_serving(LIB_LLAISYS)
 
 
 class LlaisysError(RuntimeError):
@@ -98,6 +100,7 @@ __all__ = [
     "LlaisysQwen2Meta",
     "LlaisysQwen2Weights",
     "llaisysQwen2Model_t",
+    "llaisysScheduler_t",
     "llaisysDataType_t",
     "DataType",
     "llaisysDeviceType_t",
