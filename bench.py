@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None, help="timed steps (default: 200; qwen2: 64)")
     p.add_argument("--warmup", type=int, default=None, help="untimed steps (default: 20; qwen2: 4)")
-    p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy", "qwen2"])
+    p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy", "qwen2", "serve"])
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-model", action="store_true",
@@ -415,6 +415,56 @@ def run_qwen2(args):
     }
 
 
+def run_serve(args):
+    """Continuous batching on the Qwen2-1.5B shape (random-init weights): R
+    requests with seeded prompt lengths U[128, 1024] and 128 greedy tokens
+    each go through the scheduler (128 sequences at once, 2048 tokens per step,
+    prefill chunks of 512); every scheduler step is one mixed varlen model
+    step. A warm-up pass of short requests first tunes the GEMM shapes the
+    steps meet. Timed: from the first step to the last request finishing, with
+    the device synchronised at both ends. --steps sets R (default 256)."""
+    import numpy as np
+    import torch
+
+    from llaisys_amd import Scheduler
+    from llaisys_amd.models import Qwen2, Qwen2Meta
+
+    R = args.steps if args.steps != 64 else 256
+    max_seqs, budget, chunk, new = 128, 2048, 512, 128
+    meta = Qwen2Meta(**QWEN2_1_5B, maxseq=1024 + new + 16)
+    blocks = max_seqs * ((meta.maxseq + 15) // 16) + 64
+    model = Qwen2.random(meta, seed=args.seed, std=0.02, num_blocks=blocks)
+    rng = np.random.default_rng(args.seed)
+
+    def serve(n, lo, hi, new_tokens):
+        sched = Scheduler(model, max_seqs=max_seqs, max_step_tokens=budget, prefill_chunk=chunk)
+        lens = rng.integers(lo, hi + 1, n)
+        rids = [sched.add(rng.integers(0, meta.voc, int(m)).tolist(), max_new_tokens=new_tokens) for m in lens]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        steps = sched.run()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        gen = sum(len(sched.tokens(r)) for r in rids)
+        return dt, steps, gen, int(lens.sum()), sched.stats()
+
+    serve(max(args.warmup, 1) * 64, 1, 300, 24)  # warm-up: tunes the step shapes
+    dt, steps, gen, prompt_tokens, st = serve(R, 128, 1024, new)
+    return {
+        "metric": "continuous-batching greedy generation tokens/s (Qwen2-1.5B shape), 1 GPU",
+        "value": round(gen / dt, 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init bf16 weights ~ N(0,0.02), seeded random prompts)",
+        "config": {"workload": "continuous batching through llaisysQwen2Scheduler*", "requests": R,
+                   "prompt_len": [128, 1024], "new_tokens": new, "max_seqs": max_seqs,
+                   "max_step_tokens": budget, "prefill_chunk": chunk, **QWEN2_1_5B,
+                   "prompt_tokens": prompt_tokens, "generated_tokens": gen,
+                   "prompt_plus_generated_tokens_per_s": round((prompt_tokens + gen) / dt, 1),
+                   "seconds": round(dt, 3), "scheduler": st},
+    }
+
+
 def run_append_gather(args):
     import numpy as np
     import torch
@@ -685,7 +735,7 @@ def traffic_from_profiles(kernel_tag):
 
 def main():
     args = parse()
-    small = args.workload == "qwen2"
+    small = args.workload in ("qwen2", "serve")
     args.steps = args.steps if args.steps is not None else (64 if small else 200)
     args.warmup = args.warmup if args.warmup is not None else (4 if small else 20)
     if args.summarize:
@@ -705,7 +755,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     line = {"decode": run_decode, "mixed": run_mixed, "append_gather": run_append_gather, "copy": run_copy,
-            "qwen2": run_qwen2}[args.workload](args)
+            "qwen2": run_qwen2, "serve": run_serve}[args.workload](args)
     print(json.dumps(line), flush=True)
 
 

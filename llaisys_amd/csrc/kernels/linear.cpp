@@ -108,7 +108,17 @@ struct LtContext {
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
     std::map<std::tuple<int, int, int, int, bool>, LtGemm> gemms;
+    // Autotuned kernel per (type, M bucket, N, K, bias): a serving loop sees
+    // a new M almost every step, and each exact shape reuses its bucket's pick.
+    std::map<std::tuple<int, int, int, int, bool>, hipblasLtMatmulAlgo_t> tuned;
 };
+
+// M buckets of the autotune: the next power of two.
+int tuneBucket(int M) {
+    int b = 1;
+    while (b < M) b <<= 1;
+    return b;
+}
 
 LtContext &ltContext() {
     thread_local std::unordered_map<int, std::unique_ptr<LtContext>> contexts;
@@ -185,7 +195,21 @@ LtGemm &prepare(LtContext &ctx, ElemType t, int M, int N, int K, const void *bia
     got = int(algos.size());
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     HIP_CHECK(hipStreamIsCapturing(s, &capture));
-    if (got == 1 || M > kTuneMaxM || !autotuneEnabled() || capture != hipStreamCaptureStatusNone) return g;
+    if (got == 1 || M > kTuneMaxM || !autotuneEnabled()) return g;
+    const auto bucket = std::make_tuple(int(t), tuneBucket(M), N, K, bias != nullptr);
+    auto pick = ctx.tuned.find(bucket);
+    if (pick != ctx.tuned.end()) {
+        // The bucket's pick, if the library confirms it for this exact shape.
+        const float one = 1.f;
+        size_t need = 0;
+        hipblasLtMatmulAlgo_t a = pick->second;
+        if (hipblaslt_ext::matmulIsAlgoSupported(ctx.handle, g.desc, &one, g.a, g.b, &one, g.c, g.c, a, need) ==
+                HIPBLAS_STATUS_SUCCESS &&
+            need <= kWorkspaceBytes)
+            g.algo = a;
+        return g;
+    }
+    if (capture != hipStreamCaptureStatusNone) return g;
 
     // Time the candidates into a scratch output (the caller's Y, possibly a
     // residual being accumulated, is not touched), each run from cold caches.
@@ -230,6 +254,7 @@ LtGemm &prepare(LtContext &ctx, ElemType t, int M, int N, int K, const void *bia
     for (auto &e : ev) HIP_CHECK(hipEventDestroy(e));
     HIP_CHECK(hipStreamSynchronize(s));
     HIP_CHECK(hipFree(flush));
+    ctx.tuned[bucket] = g.algo;
     return g;
 }
 
