@@ -420,8 +420,9 @@ def run_serve(args):
     requests with seeded prompt lengths U[128, 1024] and 128 greedy tokens
     each go through the scheduler (128 sequences at once, 2048 tokens per step,
     prefill chunks of 512); every scheduler step is one mixed varlen model
-    step. A warm-up pass of short requests first tunes the GEMM shapes the
-    steps meet. Timed: from the first step to the last request finishing, with
+    step. Model.warm_up() first tunes the GEMM kernel of every decode-sized
+    token-count bucket, and a pass of short requests captures the decode
+    graphs of the batch sizes. Timed: from the first step to the last request finishing, with
     the device synchronised at both ends. --steps sets R (default 256)."""
     import numpy as np
     import torch
@@ -448,7 +449,8 @@ def run_serve(args):
         gen = sum(len(sched.tokens(r)) for r in rids)
         return dt, steps, gen, int(lens.sum()), sched.stats()
 
-    serve(max(args.warmup, 1) * 64, 1, 300, 24)  # warm-up: tunes the step shapes
+    model.warm_up(256)  # tunes every decode-sized step shape bucket
+    serve(max(args.warmup, 1) * 64, 1, 300, 24)  # warm-up: graphs of the batch sizes
     dt, steps, gen, prompt_tokens, st = serve(R, 128, 1024, new)
     return {
         "metric": "continuous-batching greedy generation tokens/s (Qwen2-1.5B shape), 1 GPU",

@@ -230,6 +230,22 @@ class Qwen2:
     def num_free_blocks(self) -> int:
         return int(LIB_LLAISYS.llaisysQwen2NumFreeBlocks(self._model))
 
+    def warm_up(self, max_tokens: int = 256):
+        """Run one throwaway step of b single-token sequences for b = 1, 2, 4,
+        ... up to max_tokens (and the free blocks), so the library tunes its
+        GEMM kernel for every token-count bucket of decode-sized steps (and of
+        the LM head) before serving, instead of inside the first step that
+        meets each bucket."""
+        b = 1
+        while b <= min(max_tokens, self.num_free_blocks()):
+            ids = [self.create_sequence()[0] for _ in range(b)]
+            try:
+                self.step(ids, [[0]] * b)
+            finally:
+                for i in ids:
+                    self.free(i)
+            b *= 2
+
     def step(self, seq_ids: Sequence[int], tokens: Sequence[Sequence[int]]) -> List[int]:
         """Append tokens[i] to sequence seq_ids[i]; returns each greedy next token."""
         B = len(seq_ids)
