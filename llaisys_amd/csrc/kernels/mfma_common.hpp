@@ -179,6 +179,39 @@ __device__ __forceinline__ void accumulatePV(Acc &acc, const u32x4 (&va)[4], con
     }
 }
 
+// The same two steps with V already in operand order: v0[s] = {A.x, A.y, B.x,
+// B.y} and v1[s] = {A.z, A.w, B.z, B.w} of quarter s (the prefill kernel's LDS
+// stages hold V this way, so no register moves assemble the operands).
+__device__ __forceinline__ void maskStaleVPacked(u32x4 (&v0)[4], u32x4 (&v1)[4], int first_key, int ctx, bool hasB,
+                                                 int grp) {
+    if (first_key + 32 > ctx || !hasB) {
+        const int kbase = first_key + grp * 4;
+        const uint32_t ma01 = keepPair(kbase < ctx, kbase + 1 < ctx);
+        const uint32_t ma23 = keepPair(kbase + 2 < ctx, kbase + 3 < ctx);
+        const uint32_t mb01 = hasB ? keepPair(kbase + 16 < ctx, kbase + 17 < ctx) : 0u;
+        const uint32_t mb23 = hasB ? keepPair(kbase + 18 < ctx, kbase + 19 < ctx) : 0u;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            v0[s] &= u32x4{ma01, ma23, mb01, mb23};
+            v1[s] &= u32x4{ma01, ma23, mb01, mb23};
+        }
+    }
+}
+
+template <bool SPLIT_P>
+__device__ __forceinline__ void accumulatePVPacked(Acc &acc, const u32x4 (&v0)[4], const u32x4 (&v1)[4],
+                                                   const PairP &P) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        acc.o[2 * s] = mfma(asBf16(v0[s]), P.hi, acc.o[2 * s]);
+        acc.o[2 * s + 1] = mfma(asBf16(v1[s]), P.hi, acc.o[2 * s + 1]);
+        if constexpr (SPLIT_P) {
+            acc.o[2 * s] = mfma(asBf16(v0[s]), P.lo, acc.o[2 * s]);
+            acc.o[2 * s + 1] = mfma(asBf16(v1[s]), P.lo, acc.o[2 * s + 1]);
+        }
+    }
+}
+
 // Consume one page pair: scores, online softmax and P.V (see scorePair for
 // the arguments; ctx = keys in cache, whose later slots get zeroed V).
 // SPLIT_P: P enters P.V as hi + lo bf16 parts (fp32-accurate) or as one bf16.

@@ -219,11 +219,25 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             }
         }
     };
+    // K quarters go to LDS as loaded. V quarters go in P.V operand order:
+    // slot (8 + 2 s + h) of a pair holds, per lane, half h (dwords 2h, 2h+1)
+    // of V page A's quarter s in its low 8 bytes and of page B's in its high 8.
     auto stageStore = [&](int buf) {
 #pragma unroll
         for (int sp = 0; sp < kStagePairs; ++sp)
 #pragma unroll
-            for (int j = 0; j < kPer; ++j) kvs[buf][(sp * 16 + wave + kWaves * j) * 64 + lane] = st[sp][j];
+            for (int j = 0; j < kPer; ++j) {
+                const int q = wave + kWaves * j, part = q >> 2, quarter = q & 3;
+                u32x4 *pair = kvs[buf] + sp * 16 * 64;
+                if (part < 2) {
+                    pair[q * 64 + lane] = st[sp][j];
+                } else {
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    u32x2 *half = reinterpret_cast<u32x2 *>(pair + (8 + 2 * quarter) * 64 + lane) + (part & 1);
+                    half[0] = u32x2{st[sp][j][0], st[sp][j][1]};
+                    half[64 * 2] = u32x2{st[sp][j][2], st[sp][j][3]}; // next slot, same lane
+                }
+            }
     };
 
     Acc acc[kTiles];
@@ -278,15 +292,15 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                     if (pp >= p1) break;
                     const u32x4 *src = stage + (sg + j) * 16 * 64;
                     const bool hasB = pp + 1 < p1;
-                    u32x4 va[4], vb[4];
+                    u32x4 v0[4], v1[4];
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
-                        va[s] = src[(2 * 4 + s) * 64 + lane];
-                        vb[s] = src[(3 * 4 + s) * 64 + lane];
+                        v0[s] = src[(8 + 2 * s) * 64 + lane];
+                        v1[s] = src[(9 + 2 * s) * 64 + lane];
                     }
-                    maskStaleV(va, vb, pp * 16, t.ctx, hasB, grp);
+                    maskStaleVPacked(v0, v1, pp * 16, t.ctx, hasB, grp);
 #pragma unroll
-                    for (int k = 0; k < kTiles; ++k) accumulatePV<OUT_F32>(acc[k], va, vb, P[k][j]);
+                    for (int k = 0; k < kTiles; ++k) accumulatePVPacked<OUT_F32>(acc[k], v0, v1, P[k][j]);
                 }
             }
         }
