@@ -115,9 +115,20 @@ __device__ __forceinline__ void softmaxUpdate(Acc &acc, const float (&sv)[NP][8]
         for (int i = 0; i < 8; ++i) mloc = fmaxf(mloc, sv[j][i]);
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(acc.m, mloc * scale_log2);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2Fast(acc.m - m_use);
+    // Lazy rescale: a column keeps its running max until a score exceeds it
+    // by more than 2^kLazyLog2 (P then stays below that bound). Only when some
+    // column of the wave crosses it do all columns move to their true max and
+    // rescale O and l; the normalised result is the same either way.
+    constexpr float kLazyLog2 = 8.f;
+    const float m_true = fmaxf(acc.m, mloc * scale_log2);
+    if (__builtin_amdgcn_ballot_w64(m_true > acc.m + kLazyLog2) != 0) {
+        const float alpha = exp2Fast(acc.m - ((m_true == -INFINITY) ? 0.f : m_true));
+        acc.l *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc.o[i] *= alpha;
+        acc.m = m_true;
+    }
+    const float m_use = (acc.m == -INFINITY) ? 0.f : acc.m;
     float psum = 0.f;
 #pragma unroll
     for (int j = 0; j < NP; ++j)
@@ -129,10 +140,7 @@ __device__ __forceinline__ void softmaxUpdate(Acc &acc, const float (&sv)[NP][8]
             P[j].hi[i] = hi;
             if constexpr (SPLIT_P) P[j].lo[i] = (__bf16)(p - (float)hi);
         }
-    acc.l = acc.l * alpha + psum;
-    acc.m = m_new;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc.o[i] *= alpha;
+    acc.l += psum;
 }
 
 // Scores, online softmax update and P of one page pair (see pairScores).
