@@ -117,47 +117,44 @@ __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
     }
 }
 
-// One block per output row r (source row rows[r], or r), 8 columns per
-// thread-step; rows of up to kRowVecs * 256 * 8 elements are read once and
-// kept in registers between the sum of squares and the scaling.
-constexpr int kRowVecs = 4;
-
-__global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(uint16_t *out, const bf16 *x, const int64_t *rows,
-                                                              const bf16 *w, int d, float eps) {
-    __shared__ float red[kThreads / 64];
-    const int r = blockIdx.x;
+// One wave per output row r (source row rows[r], or r), VPL 16-byte vectors
+// (8 columns) per lane: the row and the norm weights are loaded together and
+// kept in registers, the sum of squares is a wave reduction (no LDS, no
+// barrier), then each element is scaled and rounded once.
+template <int VPL>
+__global__ void __launch_bounds__(64) rmsNormRowsKernel(uint16_t *out, const bf16 *x, const int64_t *rows,
+                                                        const bf16 *w, int d, float eps) {
+    const int r = blockIdx.x, lane = threadIdx.x;
     const uint4 *src = reinterpret_cast<const uint4 *>(x + size_t(rows ? rows[r] : r) * d);
     const uint4 *wr = reinterpret_cast<const uint4 *>(w);
     const int nv = d / 8;
-    uint4 v[kRowVecs];
+    uint4 v[VPL], g[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int c = lane + i * 64;
+        v[i] = c < nv ? src[c] : uint4{0, 0, 0, 0};
+        g[i] = c < nv ? wr[c] : uint4{0, 0, 0, 0};
+    }
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < kRowVecs; ++i) {
-        const int c = threadIdx.x + i * kThreads;
-        v[i] = c < nv ? src[c] : uint4{0, 0, 0, 0};
+    for (int i = 0; i < VPL; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const uint32_t u = (&v[i].x)[e];
             const float lo = __uint_as_float(u << 16), hi = __uint_as_float(u & 0xffff0000u);
             ss += lo * lo + hi * hi;
         }
-    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (int i = 0; i < kThreads / 64; ++i) tot += red[i];
-    const float inv = rsqrtf(tot / float(d) + eps);
+    const float inv = rsqrtf(ss / float(d) + eps);
 #pragma unroll
-    for (int i = 0; i < kRowVecs; ++i) {
-        const int c = threadIdx.x + i * kThreads;
+    for (int i = 0; i < VPL; ++i) {
+        const int c = lane + i * 64;
         if (c >= nv) break;
-        const uint4 g = wr[c];
         uint4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t u = (&v[i].x)[e], gw = (&g.x)[e];
+            const uint32_t u = (&v[i].x)[e], gw = (&g[i].x)[e];
             const uint32_t lo = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(u << 16) * inv *
                                                                                __uint_as_float(gw << 16)));
             const uint32_t hi = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(u & 0xffff0000u) * inv *
@@ -167,6 +164,7 @@ __global__ void __launch_bounds__(kThreads) rmsNormRowsKernel(uint16_t *out, con
         reinterpret_cast<uint4 *>(out)[size_t(r) * nv + c] = o;
     }
 }
+constexpr int kRowMaxVecs = 16; // d <= 16 * 64 * 8 = 8192
 
 // Multi-step decode: step s reads s from a device counter. Before the step:
 // lengths = base + s (before) and base + s + 1 (after), tokens = first at
@@ -231,11 +229,24 @@ void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *
 
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
                  void *stream) {
-    LLAISYS_CHECK(d % 8 == 0 && d <= kRowVecs * kThreads * 8,
-                  "rmsNormRows: d must be a multiple of 8 and at most " << kRowVecs * kThreads * 8 << ", got " << d);
+    LLAISYS_CHECK(d % 8 == 0 && d <= kRowMaxVecs * 64 * 8,
+                  "rmsNormRows: d must be a multiple of 8 and at most " << kRowMaxVecs * 64 * 8 << ", got " << d);
     if (!R) return;
-    hipLaunchKernelGGL(rmsNormRowsKernel, dim3(unsigned(R)), dim3(kThreads), 0, static_cast<hipStream_t>(stream), out,
-                       reinterpret_cast<const bf16 *>(x), rows, reinterpret_cast<const bf16 *>(w), d, eps);
+    const int vpl = (d / 8 + 63) / 64;
+    const auto s = static_cast<hipStream_t>(stream);
+    const auto *xb = reinterpret_cast<const bf16 *>(x);
+    const auto *wb = reinterpret_cast<const bf16 *>(w);
+    const dim3 grid{unsigned(R)}, block{64};
+    if (vpl <= 1)
+        hipLaunchKernelGGL(rmsNormRowsKernel<1>, grid, block, 0, s, out, xb, rows, wb, d, eps);
+    else if (vpl <= 2)
+        hipLaunchKernelGGL(rmsNormRowsKernel<2>, grid, block, 0, s, out, xb, rows, wb, d, eps);
+    else if (vpl <= 4)
+        hipLaunchKernelGGL(rmsNormRowsKernel<4>, grid, block, 0, s, out, xb, rows, wb, d, eps);
+    else if (vpl <= 8)
+        hipLaunchKernelGGL(rmsNormRowsKernel<8>, grid, block, 0, s, out, xb, rows, wb, d, eps);
+    else
+        hipLaunchKernelGGL(rmsNormRowsKernel<16>, grid, block, 0, s, out, xb, rows, wb, d, eps);
     HIP_CHECK(hipGetLastError());
 }
 

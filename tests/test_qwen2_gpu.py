@@ -327,3 +327,13 @@ def test_continuous_batching_scheduler_matches_reference():
             check_token(t, ref[len(p) - 1 + k], tol)
     del sched
     assert model.num_free_blocks() == 16
+
+
+def test_warm_up_leaves_the_pool_free_and_the_model_correct():
+    model, hf = build("tiny", num_blocks=64)
+    model.warm_up(32)  # steps of 1, 2, ..., 32 throwaway sequences
+    assert model.num_free_blocks() == 64
+    toks = prompt(20, model.meta.voc, 5)
+    nxt = model.infer(toks)
+    ref = hf_logits(hf, toks)[-1]
+    check_token(nxt, ref, check_logits(to_torch(model.logits())[0], ref))
