@@ -34,6 +34,7 @@ Runtime::~Runtime() {
         api_->set_device(id_);
         if (type_ != LLAISYS_DEVICE_CPU) api_->device_synchronize();
         if (scratch_) api_->free_device(scratch_);
+        if (slots_) api_->free_device(slots_);
         if (error_word_) api_->free_device(error_word_);
         api_->destroy_stream(stream_);
     } catch (...) {
@@ -60,8 +61,24 @@ void *Runtime::scratch(size_t bytes) {
         size_t grown = std::max(bytes, scratch_bytes_ * 2);
         scratch_ = api_->malloc_device(grown);
         scratch_bytes_ = grown;
+        ++ws_gen_;
     }
     return scratch_;
+}
+
+void *Runtime::decodeSlots(size_t bytes) {
+    LLAISYS_CHECK(type_ == LLAISYS_DEVICE_AMD, "device workspace exists on AMD runtimes only");
+    if (bytes > slots_bytes_) {
+        api_->device_synchronize();
+        if (slots_) api_->free_device(slots_);
+        const size_t grown = std::max(bytes, slots_bytes_ * 2);
+        slots_ = api_->malloc_device(grown);
+        if (hipMemset(slots_, 0, grown) != hipSuccess) LLAISYS_RAISE("hipMemset failed");
+        api_->device_synchronize();
+        slots_bytes_ = grown;
+        ++ws_gen_;
+    }
+    return slots_;
 }
 
 int *Runtime::errorWord() {

@@ -18,6 +18,7 @@
 #include "llaisys/runtime.h"
 
 #include <cstddef>
+#include <cstdint>
 #include <map>
 #include <memory>
 #include <vector>
@@ -69,6 +70,13 @@ public:
 
     // Device workspace (AMD only). Grow-only; growing waits for the device.
     void *scratch(size_t bytes);
+    // Persistent device buffer of the decode attention's per-unit record
+    // slots. Grow-only and zeroed when (re)allocated; kernels leave the slot
+    // headers at zero after every call, so contents carry over between calls.
+    void *decodeSlots(size_t bytes);
+    // Bumped whenever scratch() or decodeSlots() move: captured graphs that
+    // baked the old addresses in must be re-captured.
+    uint64_t workspaceGeneration() const { return ws_gen_; }
     // One int32 of kernel-side error bits.
     int *errorWord();
     int takeErrorFlags();
@@ -84,6 +92,9 @@ private:
     void *scratch_ = nullptr;
     size_t scratch_bytes_ = 0;
     int *error_word_ = nullptr;
+    void *slots_ = nullptr;
+    size_t slots_bytes_ = 0;
+    uint64_t ws_gen_ = 0;
 };
 
 class Context {

@@ -11,10 +11,16 @@
 //
 // A unit whose pairs all fall in one wave is finished by that wave
 // (normalised output). Otherwise every wave holding part of it writes a
-// record (unnormalised O, running max m, sum l) into one of its two slots
-// (slot 0: its first unit, slot 1: its last), and the combine kernel,
+// record (unnormalised O, running max m, sum l), and the combine kernel,
 // launched next on the same stream, merges each split unit's records with
-// log-sum-exp weights. The kernel boundary makes the records visible to the
+// log-sum-exp weights. A unit spread over at most kUnitSlots waves keeps its
+// records in slots of its own (slot k = the wave's place among the unit's
+// waves) in a persistent buffer, each with a header holding the record count:
+// the combine then finds them without knowing the lengths, in one memory
+// round trip, and returns the headers to zero. A unit spread further (or any
+// unit when a grid has more waves than pairs) uses per-wave records (slot 0:
+// the wave's first unit, slot 1: its last) with slot 0's header set to -1, and
+// the combine locates them through the length scan. The kernel boundary makes the records visible to the
 // combine on every XCD. (Merging inside this kernel instead needs either
 // agent-scope fences, which write back / invalidate a whole L2 per wave, or
 // device-scope record traffic plus a serial merge at the tail; both measured
@@ -27,6 +33,7 @@
 #include "../device/hip_check.hpp"
 
 #include <algorithm>
+#include <cstddef>
 #include <cstdlib>
 #include <mutex>
 #include <vector>
@@ -39,6 +46,7 @@ using namespace mfma;
 
 constexpr int kPairsPerWave = 64; // one pair per lane in the wave's block-id window
 constexpr int kMergeBatch = 4;    // records whose loads are in flight together
+constexpr int kUnitSlots = 8;     // per-unit record slots (units spread over more waves use per-wave records)
 
 struct DecodeArgs {
     const uint16_t *q;
@@ -51,6 +59,8 @@ struct DecodeArgs {
                          // sequences with exactly one query are handled here
     float *records;
     int *err;
+    int *slot_hdr;   // null: every split unit uses the per-wave records
+    float *slot_rec; // kUnitSlots records of G * (kHeadDim + 2) floats per unit
     int B, T, nh, nkvh, G, max_pages, num_blocks, W;
     float scale_log2;
 };
@@ -177,6 +187,8 @@ __global__ void __launch_bounds__(64)
         bidB = row[pb];
     }
 
+    // Record slot of this wave in its split units (set after the first issues).
+    int slot_k[2] = {0, 0}, slot_n[2] = {0, 0};
     const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
     const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
     const int ncol = min(n, G - 1); // columns past G read a valid row and are masked later
@@ -221,8 +233,24 @@ __global__ void __launch_bounds__(64)
             }
             return;
         }
+        // The unit's records: slot k (this wave's place among the unit's
+        // waves) of the unit's own slots with a header holding the record
+        // count, or, past kUnitSlots waves, this wave's per-wave record with
+        // slot 0's header marking the unit as overflowed (-1).
+        // (Grids with more waves than pairs, where empty waves sit between a
+        // unit's records, take the per-wave path.)
+        const int unit = cur_b * a.nkvh + cur_h;
+        const int nrec = first < s ? slot_n[0] : slot_n[1];
+        float *rec;
+        if (nrec <= kUnitSlots) {
+            const int k = first < s ? slot_k[0] : slot_k[1];
+            rec = a.slot_rec + size_t(unit * kUnitSlots + k) * G * (kHeadDim + 2);
+            if (lane == 0) a.slot_hdr[unit * kUnitSlots + k] = nrec;
+        } else {
+            rec = recordAt(a, 2 * w + (first <= s ? 0 : 1));
+            if (a.slot_hdr && first >= s && lane == 0) a.slot_hdr[unit * kUnitSlots] = -1;
+        }
         if (n < G) {
-            float *rec = recordAt(a, 2 * w + (first <= s ? 0 : 1));
 #pragma unroll
             for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4 *>(rec + recordO(G, i, n, grp)) = acc.o[i];
             if (grp == 0) *reinterpret_cast<float2 *>(rec + recordML(G, n)) = make_float2(acc.m, lt);
@@ -231,6 +259,30 @@ __global__ void __launch_bounds__(64)
 
 #pragma unroll
     for (int st = 0; st < NSTAGE; ++st) issue(st, st);
+    // The only units of this slice that can be split: the one holding its
+    // first pair (if it began in an earlier wave) and the one holding its last
+    // (if it continues in a later one). Their record counts and this wave's
+    // place among their waves are worked out once, while the first pairs
+    // load: index 0 for the unit that began earlier, 1 for the one that began
+    // in this slice.
+    {
+        const int bf = __builtin_amdgcn_readlane(lb, 0), hf = __builtin_amdgcn_readlane(lh, 0);
+        const int bl = __builtin_amdgcn_readlane(lb, cnt - 1), hl = __builtin_amdgcn_readlane(lh, cnt - 1);
+        const int nf = ((((C[bf] + 15) >> 4) + 1) >> 1), nl = ((((C[bl] + 15) >> 4) + 1) >> 1);
+        const int ff = S[bf] + hf * nf, fl = S[bl] + hl * nl;
+        auto wv = [&](int g) { return waveOf(g, N, a.W); };
+        const int w0f = wv(ff), w0l = fl < s ? w0f : w;
+        slot_k[0] = w - w0f;
+        slot_n[0] = wv(ff + nf - 1) - w0f + 1;
+        slot_k[1] = w - w0l;
+        slot_n[1] = wv(fl + nl - 1) - w0l + 1;
+        const bool slots = a.slot_hdr && N >= a.W;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) slot_n[i] = __builtin_amdgcn_readfirstlane(slots ? slot_n[i] : kUnitSlots + 1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) slot_k[i] = __builtin_amdgcn_readfirstlane(slot_k[i]);
+    }
+
     for (int k0 = 0; k0 < cnt; k0 += NSTAGE) {
 #pragma unroll
         for (int st = 0; st < NSTAGE; ++st) {
@@ -260,12 +312,14 @@ __global__ void __launch_bounds__(64)
 }
 
 // Merge the records of every unit that spans more than one wave.
-// 256 threads = 4 waves per unit. Wave 0 scans the lengths into LDS. Lane k
-// works out which wave/slot record k of the unit lives in (the integer
-// divisions run lane-parallel); wave v then takes records v, v+4, ... in
-// batches with all loads of a batch in flight, merging online
-// (O = sum_r 2^(m_r - M) O_r, l likewise); the four partial states meet in
-// LDS and wave 0 writes the output.
+// 256 threads = 4 waves per unit. With record slots, wave v loads slots 2v
+// and 2v+1 with their headers (and every wave slot 0's header) in one go and
+// merges the valid ones. Without them (or for an overflowed unit) wave 0
+// scans the lengths into LDS, lane k works out which per-wave record k of the
+// unit lives in (the integer divisions run lane-parallel), and wave v takes
+// records v, v+4, ... in batches with all loads of a batch in flight. Merging
+// is online (O = sum_r 2^(m_r - M) O_r, l likewise); the four partial states
+// meet in LDS and wave 0 writes the output.
 constexpr int kCombineWaves = 4;
 
 template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) decodeCombineKernel(DecodeArgs a) {
@@ -280,59 +334,103 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
     const int n = lane & 15;
     const int grp = lane >> 4;
     const int G = a.G;
-    if (wave == 0) scanPairs(a, S, C, Q, false);
-    __syncthreads();
-    const int N = S[a.B];
     const int u = blockIdx.x;
     const int b = u / a.nkvh;
     const int h = u - b * a.nkvh;
-    const int np = (C[b] + 15) >> 4;
-    const int npr = (np + 1) >> 1;
-    if (npr == 0) return;
-    const int first = S[b] + h * npr;
-    const int w0 = waveOf(first, N, a.W);
-    const int w1 = waveOf(first + npr - 1, N, a.W);
-    if (w0 == w1) return;
     const int col = min(n, G - 1);
-
     float M = -INFINITY, L = 0.f;
     f32x4 o[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int base = w0; base <= w1; base += 64) {
-        // Lane k: record of wave base+k, or -1 if that wave's range is empty
-        // (possible when N < W).
-        const int wk = base + lane;
-        int rec_k = -1;
-        if (wk <= w1) {
-            const int st = waveStart(wk, N, a.W);
-            if (waveStart(wk + 1, N, a.W) > st) rec_k = 2 * wk + ((wk == w0 && st < first) ? 1 : 0);
+    int row;
+    int clear_mask = 0; // this wave's slots whose headers go back to zero (after the barrier below)
+    bool per_wave = a.slot_hdr == nullptr;
+    if (!per_wave) {
+        // The unit's slots: wave v takes slots 2v and 2v+1. Headers, records
+        // and the output row are all requested before any of them is used, so
+        // the merge waits for one memory round trip.
+        int *hdr = a.slot_hdr + u * kUnitSlots;
+        const int h0 = hdr[0];
+        int hk[2];
+        float2 ml[2];
+        f32x4 orr[2][8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int k = 2 * wave + t;
+            hk[t] = hdr[k];
+            const float *rec = a.slot_rec + size_t(u * kUnitSlots + k) * G * (kHeadDim + 2);
+            ml[t] = *reinterpret_cast<const float2 *>(rec + recordML(G, col));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) orr[t][i] = *reinterpret_cast<const f32x4 *>(rec + recordO(G, i, col, grp));
         }
-        const int cnt = min(64, w1 - base + 1);
-        for (int k0 = wave * kMergeBatch; k0 < cnt; k0 += kCombineWaves * kMergeBatch) {
-            float mr[kMergeBatch], lr[kMergeBatch];
-            f32x4 orr[kMergeBatch][8];
+        row = a.cu_q ? a.cu_q[b] : b;
+        if (h0 == 0) return; // unit whole in one wave (or not a decode row): nothing to merge
+        if (h0 > 0) {
 #pragma unroll
-            for (int t = 0; t < kMergeBatch; ++t) {
-                const int r = __builtin_amdgcn_readlane(rec_k, min(k0 + t, cnt - 1));
-                const float *rec = recordAt(a, r < 0 ? 0 : r);
-                const float2 ml = *reinterpret_cast<const float2 *>(rec + recordML(G, col));
-                mr[t] = ml.x;
-                lr[t] = ml.y;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) orr[t][i] = *reinterpret_cast<const f32x4 *>(rec + recordO(G, i, col, grp));
-                if (r < 0 || k0 + t >= cnt) mr[t] = -INFINITY; // weight 0
-            }
-#pragma unroll
-            for (int t = 0; t < kMergeBatch; ++t) {
-                if (mr[t] == -INFINITY) continue;
-                const float Mn = fmaxf(M, mr[t]);
+            for (int t = 0; t < 2; ++t) {
+                if (hk[t] <= 0 || ml[t].x == -INFINITY) continue;
+                const float Mn = fmaxf(M, ml[t].x);
                 const float sa = exp2Fast(M - Mn);
-                const float sb = exp2Fast(mr[t] - Mn);
-                L = L * sa + lr[t] * sb;
+                const float sb = exp2Fast(ml[t].x - Mn);
+                L = L * sa + ml[t].y * sb;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) o[i] = o[i] * sa + orr[t][i] * sb;
                 M = Mn;
+            }
+            clear_mask = (hk[0] != 0 ? 1 : 0) | (hk[1] != 0 ? 2 : 0);
+        } else {
+            per_wave = true; // overflowed: per-wave records
+            clear_mask = wave == 0 ? 1 : 0;
+        }
+    }
+    if (per_wave) {
+        if (wave == 0) scanPairs(a, S, C, Q, false);
+        __syncthreads();
+        const int N = S[a.B];
+        const int np = (C[b] + 15) >> 4;
+        const int npr = (np + 1) >> 1;
+        if (npr == 0) return;
+        const int first = S[b] + h * npr;
+        const int w0 = waveOf(first, N, a.W);
+        const int w1 = waveOf(first + npr - 1, N, a.W);
+        if (w0 == w1) return;
+        row = Q[b];
+        for (int base = w0; base <= w1; base += 64) {
+            // Lane k: record of wave base+k, or -1 if that wave's range is empty
+            // (possible when N < W).
+            const int wk = base + lane;
+            int rec_k = -1;
+            if (wk <= w1) {
+                const int st = waveStart(wk, N, a.W);
+                if (waveStart(wk + 1, N, a.W) > st) rec_k = 2 * wk + ((wk == w0 && st < first) ? 1 : 0);
+            }
+            const int cnt = min(64, w1 - base + 1);
+            for (int k0 = wave * kMergeBatch; k0 < cnt; k0 += kCombineWaves * kMergeBatch) {
+                float mr[kMergeBatch], lr[kMergeBatch];
+                f32x4 orr[kMergeBatch][8];
+#pragma unroll
+                for (int t = 0; t < kMergeBatch; ++t) {
+                    const int r = __builtin_amdgcn_readlane(rec_k, min(k0 + t, cnt - 1));
+                    const float *rec = recordAt(a, r < 0 ? 0 : r);
+                    const float2 ml = *reinterpret_cast<const float2 *>(rec + recordML(G, col));
+                    mr[t] = ml.x;
+                    lr[t] = ml.y;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        orr[t][i] = *reinterpret_cast<const f32x4 *>(rec + recordO(G, i, col, grp));
+                    if (r < 0 || k0 + t >= cnt) mr[t] = -INFINITY; // weight 0
+                }
+#pragma unroll
+                for (int t = 0; t < kMergeBatch; ++t) {
+                    if (mr[t] == -INFINITY) continue;
+                    const float Mn = fmaxf(M, mr[t]);
+                    const float sa = exp2Fast(M - Mn);
+                    const float sb = exp2Fast(mr[t] - Mn);
+                    L = L * sa + lr[t] * sb;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = o[i] * sa + orr[t][i] * sb;
+                    M = Mn;
+                }
             }
         }
     }
@@ -345,6 +443,13 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
         part_ml[wave - 1][1][lane] = L;
     }
     __syncthreads();
+    // Every wave has read the unit's headers by now: leave them at zero for
+    // the next call.
+    if (clear_mask && lane == 0) {
+        int *hdr = a.slot_hdr + u * kUnitSlots + 2 * wave;
+        if (clear_mask & 1) hdr[0] = 0;
+        if (clear_mask & 2) hdr[1] = 0;
+    }
     if (wave > 0 || n >= G) return;
 #pragma unroll
     for (int v = 0; v < kCombineWaves - 1; ++v) {
@@ -361,10 +466,12 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
         M = Mn;
     }
     const float inv = 1.f / L;
-    const size_t row = (size_t(Q[b]) * a.nh + h * G + n) * kHeadDim;
+    const size_t orow = (size_t(row) * a.nh + h * G + n) * kHeadDim;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, o[i] * inv);
+    for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, orow, i, grp, o[i] * inv);
 }
+
+size_t slotHeaderBytes(size_t slots) { return (slots * sizeof(int) + 255) / 256 * 256; }
 
 int envInt(const char *name, int fallback) {
     const char *v = std::getenv(name);
@@ -394,13 +501,19 @@ DecodePlan planDecode(int B, int nkvh, int group, int max_pages) {
     p.record_bytes = size_t(2) * p.waves * group * (kHeadDim + 2) * sizeof(float);
     p.lds_bytes = size_t(3 * B + 1) * sizeof(int);
     p.stages = envInt("LLAISYS_DECODE_STAGES", 2) >= 3 ? 3 : 2;
+    // Per-unit record slots (headers first, then records), unless disabled
+    // or implausibly large.
+    const size_t units = size_t(B) * nkvh * kUnitSlots;
+    const size_t slot_bytes = slotHeaderBytes(units) + units * group * (kHeadDim + 2) * sizeof(float);
+    p.slot_bytes = (envInt("LLAISYS_DECODE_SLOTS", 1) != 0 && slot_bytes <= (size_t(1) << 30)) ? slot_bytes : 0;
     return p;
 }
 
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                  int nkvh, int max_pages,
-                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *err, void *stream) {
+                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *err, void *slots,
+                 void *stream) {
     if (B == 0) return;
     DecodeArgs a;
     a.q = q;
@@ -412,6 +525,13 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
     a.cu_q = cu_q;
     a.records = records;
     a.err = err;
+    a.slot_hdr = nullptr;
+    a.slot_rec = nullptr;
+    if (plan.slot_bytes && slots) {
+        a.slot_hdr = static_cast<int *>(slots);
+        a.slot_rec = reinterpret_cast<float *>(static_cast<std::byte *>(slots) +
+                                               slotHeaderBytes(size_t(B) * nkvh * kUnitSlots));
+    }
     a.B = B;
     a.T = T;
     a.nh = nh;

@@ -117,7 +117,7 @@ Qwen2Model::DecodeGraph Qwen2Model::capture(const std::function<void()> &work, s
     g.exec = exec;
     g.width = width;
     g.gen = ws_gen_;
-    g.scratch = rt.scratch(0);
+    g.ws = rt.workspaceGeneration();
     return g;
 }
 
@@ -125,7 +125,7 @@ void Qwen2Model::decodeGraph(size_t B, size_t width) {
     auto &rt = core::context().runtime();
     auto s = static_cast<hipStream_t>(rt.stream());
     DecodeGraph &g = graphs_[B];
-    if (g.exec && g.width == width && g.gen == ws_gen_ && g.scratch == rt.scratch(0)) {
+    if (g.exec && g.width == width && g.gen == ws_gen_ && g.ws == rt.workspaceGeneration()) {
         HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(g.exec), s));
         return;
     }
@@ -359,7 +359,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     size_t done = 0;
     if (use_graphs_) {
         DecodeGraph &g = multi_graphs_[B];
-        const bool valid = g.exec && g.width == width && g.gen == ws_gen_ && g.scratch == rt.scratch(0);
+        const bool valid = g.exec && g.width == width && g.gen == ws_gen_ && g.ws == rt.workspaceGeneration();
         if (!valid) {
             if (g.exec) HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(g.exec)));
             g.exec = nullptr;

@@ -106,7 +106,7 @@ private:
         void *exec = nullptr; // hipGraphExec_t
         size_t width = 0;     // block-table width it was captured with
         uint64_t gen = 0;     // workspace generation it was captured with
-        void *scratch = nullptr;
+        uint64_t ws = 0; // runtime workspace generation it was captured with
     };
     DecodeGraph capture(const std::function<void()> &work, size_t width);
     bool use_graphs_ = true;

@@ -55,8 +55,9 @@ def test_decode_edge_lengths(nh, nkvh):
     check(run_decode(case, q, torch.float32), run_decode(case, q, torch.bfloat16), ref)
 
 
+@pytest.mark.parametrize("slots", ["1", "0"])
 @pytest.mark.parametrize("waves", ["1", "7", "64", "1024", "5000"])
-def test_decode_wave_count_invariance(waves, monkeypatch):
+def test_decode_wave_count_invariance(waves, slots, monkeypatch):
     # The grid size only changes where sequences are cut into records: from
     # every unit whole in one wave to more waves than page pairs (empty ranges).
     ctx = oracle.randint(5, 9, 1, 3000).astype(np.int32)
@@ -64,7 +65,33 @@ def test_decode_wave_count_invariance(waves, monkeypatch):
     q = queries(22, case.B, 12)
     ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE)
     monkeypatch.setenv("LLAISYS_DECODE_WAVES", waves)
+    monkeypatch.setenv("LLAISYS_DECODE_SLOTS", slots)
     check(run_decode(case, q, torch.float32), run_decode(case, q, torch.bfloat16), ref)
+
+
+def test_decode_record_slots_reset_between_calls(monkeypatch):
+    # Split units merge through per-unit record slots whose headers the
+    # combine returns to zero: calls of different batches in a row (one whose
+    # long sequences overflow the slots) each match the oracle, and a repeat
+    # of the first batch gives bit-identical output.
+    a = make_case(51, oracle.randint(14, 64, 512, 8192).astype(np.int32))
+    qa = queries(52, a.B, 12)
+    ref_a = oracle.paged_attention(qa, a.k_log, a.v_log, a.table, a.ctx, SCALE, nthreads=16)
+    b = make_case(53, np.array([30000, 40], np.int32))  # one unit spread over many waves: overflow
+    qb = queries(54, b.B, 12)
+    ref_b = oracle.paged_attention(qb, b.k_log, b.v_log, b.table, b.ctx, SCALE)
+    c = make_case(55, oracle.randint(15, 9, 1, 3000).astype(np.int32))
+    qc = queries(56, c.B, 12)
+    ref_c = oracle.paged_attention(qc, c.k_log, c.v_log, c.table, c.ctx, SCALE)
+    first = run_decode(a, qa, torch.float32)
+    check(first, run_decode(a, qa, torch.bfloat16), ref_a)
+    for _ in range(3):
+        check(run_decode(b, qb, torch.float32), run_decode(b, qb, torch.bfloat16), ref_b)
+        check(run_decode(c, qc, torch.float32), run_decode(c, qc, torch.bfloat16), ref_c)
+        assert np.array_equal(run_decode(a, qa, torch.float32), first)
+    monkeypatch.setenv("LLAISYS_DECODE_SLOTS", "0")
+    per_wave = run_decode(a, qa, torch.float32)
+    assert np.max(np.abs(per_wave - first)) <= 1e-6 * np.max(np.abs(first))
 
 
 @pytest.mark.parametrize("stages", ["2", "3"])
