@@ -34,7 +34,8 @@ Runtime::~Runtime() {
         api_->set_device(id_);
         if (type_ != LLAISYS_DEVICE_CPU) api_->device_synchronize();
         if (scratch_) api_->free_device(scratch_);
-        if (slots_) api_->free_device(slots_);
+        if (slot_hdr_) api_->free_device(slot_hdr_);
+        if (slot_rec_) api_->free_device(slot_rec_);
         if (error_word_) api_->free_device(error_word_);
         api_->destroy_stream(stream_);
     } catch (...) {
@@ -66,19 +67,32 @@ void *Runtime::scratch(size_t bytes) {
     return scratch_;
 }
 
-void *Runtime::decodeSlots(size_t bytes) {
+int *Runtime::decodeSlotHeaders(size_t header_ints) {
     LLAISYS_CHECK(type_ == LLAISYS_DEVICE_AMD, "device workspace exists on AMD runtimes only");
-    if (bytes > slots_bytes_) {
+    if (header_ints > slot_hdr_ints_) {
         api_->device_synchronize();
-        if (slots_) api_->free_device(slots_);
-        const size_t grown = std::max(bytes, slots_bytes_ * 2);
-        slots_ = api_->malloc_device(grown);
-        if (hipMemset(slots_, 0, grown) != hipSuccess) LLAISYS_RAISE("hipMemset failed");
+        if (slot_hdr_) api_->free_device(slot_hdr_);
+        const size_t grown = std::max(header_ints, slot_hdr_ints_ * 2);
+        slot_hdr_ = static_cast<int *>(api_->malloc_device(grown * sizeof(int)));
+        if (hipMemset(slot_hdr_, 0, grown * sizeof(int)) != hipSuccess) LLAISYS_RAISE("hipMemset failed");
         api_->device_synchronize();
-        slots_bytes_ = grown;
+        slot_hdr_ints_ = grown;
         ++ws_gen_;
     }
-    return slots_;
+    return slot_hdr_;
+}
+
+void *Runtime::decodeSlotRecords(size_t record_bytes) {
+    LLAISYS_CHECK(type_ == LLAISYS_DEVICE_AMD, "device workspace exists on AMD runtimes only");
+    if (record_bytes > slot_rec_bytes_) {
+        api_->device_synchronize();
+        if (slot_rec_) api_->free_device(slot_rec_);
+        const size_t grown = std::max(record_bytes, slot_rec_bytes_ * 2);
+        slot_rec_ = api_->malloc_device(grown);
+        slot_rec_bytes_ = grown;
+        ++ws_gen_;
+    }
+    return slot_rec_;
 }
 
 int *Runtime::errorWord() {

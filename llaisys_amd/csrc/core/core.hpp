@@ -70,11 +70,14 @@ public:
 
     // Device workspace (AMD only). Grow-only; growing waits for the device.
     void *scratch(size_t bytes);
-    // Persistent device buffer of the decode attention's per-unit record
-    // slots. Grow-only and zeroed when (re)allocated; kernels leave the slot
-    // headers at zero after every call, so contents carry over between calls.
-    void *decodeSlots(size_t bytes);
-    // Bumped whenever scratch() or decodeSlots() move: captured graphs that
+    // Persistent device buffers of the decode attention's per-unit record
+    // slots: the headers (at least header_ints int32, zeroed when allocated;
+    // kernels leave them at zero after every call) and the records (at least
+    // record_bytes). Separate allocations, so records never land on headers
+    // whatever the batch shape of a call. Grow-only.
+    int *decodeSlotHeaders(size_t header_ints);
+    void *decodeSlotRecords(size_t record_bytes);
+    // Bumped whenever scratch() or the slot buffers move: captured graphs that
     // baked the old addresses in must be re-captured.
     uint64_t workspaceGeneration() const { return ws_gen_; }
     // One int32 of kernel-side error bits.
@@ -92,8 +95,10 @@ private:
     void *scratch_ = nullptr;
     size_t scratch_bytes_ = 0;
     int *error_word_ = nullptr;
-    void *slots_ = nullptr;
-    size_t slots_bytes_ = 0;
+    int *slot_hdr_ = nullptr;
+    size_t slot_hdr_ints_ = 0;
+    void *slot_rec_ = nullptr;
+    size_t slot_rec_bytes_ = 0;
     uint64_t ws_gen_ = 0;
 };
 

@@ -36,14 +36,15 @@ struct DecodePlan {
     int stages;          // page pairs in flight per wave
     size_t record_bytes; // workspace for split records
     size_t lds_bytes;    // per-workgroup LDS (length prefix)
-    size_t slot_bytes;   // persistent per-unit record slots (0: per-wave records only)
+    size_t slot_headers;      // per-unit record slot headers (int32; 0: per-wave records only)
+    size_t slot_record_bytes; // per-unit record slots
 };
 constexpr int kDecodeMaxBatch = 4096; // sequences per launch (LDS-resident prefix)
 DecodePlan planDecode(int B, int nkvh, int group, int max_pages);
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                  int nkvh, int max_pages, int num_blocks, float scale, const DecodePlan &plan, float *records,
-                 int *err, void *slots, void *stream);
+                 int *err, int *slot_headers, void *slot_records, void *stream);
 
 // Chunked prefill: the sequences of a varlen batch with >= 2 queries, as
 // (16-column query tile, kv head) units split over pages, then a combine kernel.

@@ -3,7 +3,8 @@
 // Work = every (sequence b, kv head h) unit's page pairs, laid end to end:
 // unit u = b*nkvh + h owns npairs(b) = ceil(ceil(ctx_b/16)/2) consecutive
 // pair indices. A grid of W single-wave workgroups (about one per CU) splits
-// the N pairs evenly: wave w takes pairs [w*N/W, (w+1)*N/W), at most 64, and
+// the N pairs evenly: wave w takes pairs [w*P, (w+1)*P), P = ceil(N/W) <= 64
+// (the last waves take what is left), and
 // streams them through a ring of NSTAGE page pairs in flight, crossing unit
 // boundaries without draining the ring. Every wave does the same small prefix
 // scan of ctx into LDS to find its slice, so no host-side knowledge of the
@@ -17,8 +18,8 @@
 // records in slots of its own (slot k = the wave's place among the unit's
 // waves) in a persistent buffer, each with a header holding the record count:
 // the combine then finds them without knowing the lengths, in one memory
-// round trip, and returns the headers to zero. A unit spread further (or any
-// unit when a grid has more waves than pairs) uses per-wave records (slot 0:
+// round trip, and returns the headers to zero. A unit spread further uses
+// per-wave records (slot 0:
 // the wave's first unit, slot 1: its last) with slot 0's header set to -1, and
 // the combine locates them through the length scan. The kernel boundary makes the records visible to the
 // combine on every XCD. (Merging inside this kernel instead needs either
@@ -113,13 +114,12 @@ __device__ int scanPairs(const DecodeArgs &a, int *S, int *C, int *Q, bool repor
     return carry;
 }
 
-__device__ __forceinline__ int waveStart(long long w, long long N, long long W) { return int(w * N / W); }
-
-// Wave holding pair g: the largest w with waveStart(w) <= g.
-__device__ __forceinline__ int waveOf(long long g, long long N, long long W) {
-    const long long w = ((g + 1) * W + N - 1) / N - 1;
-    return int(w < W - 1 ? w : W - 1);
-}
+// Slices of P = ceil(N / W) pairs: wave w takes [w P, min((w + 1) P, N)), so
+// only the last waves can be short or empty.
+__device__ __forceinline__ int pairsPerWave(int N, int W) { return (N + W - 1) / W; }
+__device__ __forceinline__ int waveStart(int w, int N, int P) { return min(w * P, N); }
+// Wave holding pair g (0 <= g < N).
+__device__ __forceinline__ int waveOf(int g, int W, int P) { return min(g / P, W - 1); }
 
 // Record r (2 per wave) holds, for the G live columns, O as 128*G floats in
 // [blk][col][dims 4*grp .. 4*grp+3] order, so a lane's 16 B access for one
@@ -152,8 +152,9 @@ __global__ void __launch_bounds__(64)
 
     const int N = scanPairs(a, S, C, Q, w == 0);
     __syncthreads();
-    const int s = waveStart(w, N, a.W);
-    const int e = waveStart(w + 1, N, a.W);
+    const int P = pairsPerWave(N, a.W);
+    const int s = waveStart(w, N, P);
+    const int e = waveStart(w + 1, N, P);
     const int cnt = e - s;
     if (cnt <= 0) return;
     if (cnt > kPairsPerWave) { // the host sizes W so this cannot happen
@@ -237,8 +238,6 @@ __global__ void __launch_bounds__(64)
         // waves) of the unit's own slots with a header holding the record
         // count, or, past kUnitSlots waves, this wave's per-wave record with
         // slot 0's header marking the unit as overflowed (-1).
-        // (Grids with more waves than pairs, where empty waves sit between a
-        // unit's records, take the per-wave path.)
         const int unit = cur_b * a.nkvh + cur_h;
         const int nrec = first < s ? slot_n[0] : slot_n[1];
         float *rec;
@@ -270,13 +269,13 @@ __global__ void __launch_bounds__(64)
         const int bl = __builtin_amdgcn_readlane(lb, cnt - 1), hl = __builtin_amdgcn_readlane(lh, cnt - 1);
         const int nf = ((((C[bf] + 15) >> 4) + 1) >> 1), nl = ((((C[bl] + 15) >> 4) + 1) >> 1);
         const int ff = S[bf] + hf * nf, fl = S[bl] + hl * nl;
-        auto wv = [&](int g) { return waveOf(g, N, a.W); };
+        auto wv = [&](int g) { return waveOf(g, a.W, P); };
         const int w0f = wv(ff), w0l = fl < s ? w0f : w;
         slot_k[0] = w - w0f;
         slot_n[0] = wv(ff + nf - 1) - w0f + 1;
         slot_k[1] = w - w0l;
         slot_n[1] = wv(fl + nl - 1) - w0l + 1;
-        const bool slots = a.slot_hdr && N >= a.W;
+        const bool slots = a.slot_hdr != nullptr;
 #pragma unroll
         for (int i = 0; i < 2; ++i) slot_n[i] = __builtin_amdgcn_readfirstlane(slots ? slot_n[i] : kUnitSlots + 1);
 #pragma unroll
@@ -391,8 +390,9 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
         const int npr = (np + 1) >> 1;
         if (npr == 0) return;
         const int first = S[b] + h * npr;
-        const int w0 = waveOf(first, N, a.W);
-        const int w1 = waveOf(first + npr - 1, N, a.W);
+        const int P = pairsPerWave(N, a.W);
+        const int w0 = waveOf(first, a.W, P);
+        const int w1 = waveOf(first + npr - 1, a.W, P);
         if (w0 == w1) return;
         row = Q[b];
         for (int base = w0; base <= w1; base += 64) {
@@ -401,8 +401,8 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
             const int wk = base + lane;
             int rec_k = -1;
             if (wk <= w1) {
-                const int st = waveStart(wk, N, a.W);
-                if (waveStart(wk + 1, N, a.W) > st) rec_k = 2 * wk + ((wk == w0 && st < first) ? 1 : 0);
+                const int st = waveStart(wk, N, P);
+                if (waveStart(wk + 1, N, P) > st) rec_k = 2 * wk + ((wk == w0 && st < first) ? 1 : 0);
             }
             const int cnt = min(64, w1 - base + 1);
             for (int k0 = wave * kMergeBatch; k0 < cnt; k0 += kCombineWaves * kMergeBatch) {
@@ -471,8 +471,6 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
     for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, orow, i, grp, o[i] * inv);
 }
 
-size_t slotHeaderBytes(size_t slots) { return (slots * sizeof(int) + 255) / 256 * 256; }
-
 int envInt(const char *name, int fallback) {
     const char *v = std::getenv(name);
     return (v && *v) ? std::atoi(v) : fallback;
@@ -501,19 +499,20 @@ DecodePlan planDecode(int B, int nkvh, int group, int max_pages) {
     p.record_bytes = size_t(2) * p.waves * group * (kHeadDim + 2) * sizeof(float);
     p.lds_bytes = size_t(3 * B + 1) * sizeof(int);
     p.stages = envInt("LLAISYS_DECODE_STAGES", 2) >= 3 ? 3 : 2;
-    // Per-unit record slots (headers first, then records), unless disabled
-    // or implausibly large.
-    const size_t units = size_t(B) * nkvh * kUnitSlots;
-    const size_t slot_bytes = slotHeaderBytes(units) + units * group * (kHeadDim + 2) * sizeof(float);
-    p.slot_bytes = (envInt("LLAISYS_DECODE_SLOTS", 1) != 0 && slot_bytes <= (size_t(1) << 30)) ? slot_bytes : 0;
+    // Per-unit record slots, unless disabled or implausibly large.
+    const size_t slots = size_t(B) * nkvh * kUnitSlots;
+    const size_t rec_bytes = slots * group * (kHeadDim + 2) * sizeof(float);
+    const bool use = envInt("LLAISYS_DECODE_SLOTS", 1) != 0 && rec_bytes <= (size_t(1) << 30);
+    p.slot_headers = use ? slots : 0;
+    p.slot_record_bytes = use ? rec_bytes : 0;
     return p;
 }
 
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                  int nkvh, int max_pages,
-                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *err, void *slots,
-                 void *stream) {
+                 int num_blocks, float scale, const DecodePlan &plan, float *records, int *err,
+                 int *slot_headers, void *slot_records, void *stream) {
     if (B == 0) return;
     DecodeArgs a;
     a.q = q;
@@ -525,13 +524,9 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
     a.cu_q = cu_q;
     a.records = records;
     a.err = err;
-    a.slot_hdr = nullptr;
-    a.slot_rec = nullptr;
-    if (plan.slot_bytes && slots) {
-        a.slot_hdr = static_cast<int *>(slots);
-        a.slot_rec = reinterpret_cast<float *>(static_cast<std::byte *>(slots) +
-                                               slotHeaderBytes(size_t(B) * nkvh * kUnitSlots));
-    }
+    const bool slots = plan.slot_headers && slot_headers && slot_records;
+    a.slot_hdr = slots ? slot_headers : nullptr;
+    a.slot_rec = slots ? static_cast<float *>(slot_records) : nullptr;
     a.B = B;
     a.T = T;
     a.nh = nh;

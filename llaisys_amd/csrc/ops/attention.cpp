@@ -235,7 +235,8 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
             K::pagedDecode(static_cast<std::byte *>(out->data()) + b0 * nh * K::kHeadDim * esz, f32,
                            qp + b0 * nh * K::kHeadDim, kp, vp, tab + b0 * size_t(max_pages), ctx + b0, nullptr, Bc,
                            Bc, int(nh), int(nkvh), max_pages, nb, scale, plan, records, rt.errorWord(),
-                           plan.slot_bytes ? rt.decodeSlots(plan.slot_bytes) : nullptr, rt.stream());
+                           plan.slot_headers ? rt.decodeSlotHeaders(plan.slot_headers) : nullptr,
+                           plan.slot_headers ? rt.decodeSlotRecords(plan.slot_record_bytes) : nullptr, rt.stream());
         }
         return;
     }
@@ -247,9 +248,10 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
     auto dplan = K::planDecode(int(B), int(nkvh), G, max_pages);
     auto pplan = K::planPrefill(int(B), int(T), int(nkvh), G, max_pages);
     float *records = static_cast<float *>(rt.scratch(std::max(dplan.record_bytes, pplan.partial_bytes)));
-    void *slots = dplan.slot_bytes ? rt.decodeSlots(dplan.slot_bytes) : nullptr;
+    int *slot_hdr = dplan.slot_headers ? rt.decodeSlotHeaders(dplan.slot_headers) : nullptr;
+    void *slot_rec = dplan.slot_headers ? rt.decodeSlotRecords(dplan.slot_record_bytes) : nullptr;
     K::pagedDecode(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
-                   scale, dplan, records, rt.errorWord(), slots, rt.stream());
+                   scale, dplan, records, rt.errorWord(), slot_hdr, slot_rec, rt.stream());
     K::pagedPrefill(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
                     scale, pplan, records, rt.errorWord(), rt.stream());
 }

@@ -83,11 +83,19 @@ def test_decode_record_slots_reset_between_calls(monkeypatch):
     c = make_case(55, oracle.randint(15, 9, 1, 3000).astype(np.int32))
     qc = queries(56, c.B, 12)
     ref_c = oracle.paged_attention(qc, c.k_log, c.v_log, c.table, c.ctx, SCALE)
+    # a small batch whose units use the slots (one pair per wave), so its
+    # records land where a larger batch's slot headers would sit in a shared
+    # layout
+    d = make_case(57, np.array([100, 150, 200, 250], np.int32))
+    qd = queries(58, d.B, 12)
+    ref_d = oracle.paged_attention(qd, d.k_log, d.v_log, d.table, d.ctx, SCALE)
     first = run_decode(a, qa, torch.float32)
     check(first, run_decode(a, qa, torch.bfloat16), ref_a)
     for _ in range(3):
         check(run_decode(b, qb, torch.float32), run_decode(b, qb, torch.bfloat16), ref_b)
         check(run_decode(c, qc, torch.float32), run_decode(c, qc, torch.bfloat16), ref_c)
+        assert np.array_equal(run_decode(a, qa, torch.float32), first)
+        check(run_decode(d, qd, torch.float32), run_decode(d, qd, torch.bfloat16), ref_d)
         assert np.array_equal(run_decode(a, qa, torch.float32), first)
     monkeypatch.setenv("LLAISYS_DECODE_SLOTS", "0")
     per_wave = run_decode(a, qa, torch.float32)
