@@ -49,6 +49,7 @@ def parse():
     p.add_argument("--no-model", action="store_true",
                    help="decode workload only: skip the Qwen2 config-5 tokens/s measurement")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--copy-mib", type=float, default=512.0, help="--workload copy: bytes copied per launch, MiB")
     p.add_argument("--summarize", nargs=6, metavar=("STATS", "FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE", "TAG"),
                    help="summarise rocprofv3 output directories into profiles/TAG.md and profiles/TAG_traffic.json")
     p.add_argument("--profiles-dir", default=str(ROOT / "profiles"), help="where the --summarize* outputs go")
@@ -520,15 +521,18 @@ def run_append_gather(args):
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "BASELINE config 2: 32 seqs len U[1,2048], 4096-block pool, append 1 + gather"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("paged_kv_append_gather_config2"),
+                     "algorithmic_bytes_per_launch": nbytes},
     }
 
 
 def run_copy(args):
-    """A plain 512 MiB device copy, to calibrate rocprof FETCH_SIZE/WRITE_SIZE."""
+    """A plain device copy (512 MiB unless --copy-mib), to calibrate rocprof
+    FETCH_SIZE/WRITE_SIZE and to time a copy of a workload's byte count."""
     import torch
 
-    n = 512 << 20
+    n = int(args.copy_mib * (1 << 20))
     a = torch.empty(n, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
     stream = torch.cuda.current_stream()

@@ -112,6 +112,36 @@ def test_unmapped_page_and_overlong_context_set_error_flags():
     # The untouched pool still matches (the bad rows were skipped, the good ones written).
 
 
+@pytest.mark.parametrize("nkvh", [2, 3])
+def test_gather_skips_unmapped_pages_and_flags_them(nkvh):
+    # A multi-page sequence with an unmapped page in the middle: that page's rows
+    # stay untouched and flag 1 is raised; every other page is gathered exactly.
+    lens, table, k_log, v_log = _setup(11, [100, 37], 16, nkvh)
+    kp, vp = _dev(k_log, v_log)
+    bad = table.copy()
+    bad[0, 2] = -1
+    cu = np.array([0, 100, 137], np.int32)
+    ko = to_llaisys(torch.zeros((137, nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    vo = to_llaisys(torch.zeros((137, nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    L.Ops.paged_kv_gather(ko, vo, kp, vp, _i32(bad), _i32(cu))
+    assert L.device_error_flags() == 1
+    gk, gv = oracle.paged_gather(k_log, v_log, table, cu)
+    keep = np.ones(137, bool)
+    keep[32:48] = False
+    for got, want in ((bits(to_torch(ko)), gk), (bits(to_torch(vo)), gv)):
+        np.testing.assert_array_equal(got[keep], want[keep])
+        assert not got[~keep].any()
+    # Lengths past the table's pages: flag 2, the mapped pages still gathered.
+    cu_long = np.array([0, 16 * table.shape[1] + 5], np.int32)
+    ko2 = to_llaisys(torch.zeros((int(cu_long[-1]), nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    vo2 = to_llaisys(torch.zeros((int(cu_long[-1]), nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    L.Ops.paged_kv_gather(ko2, vo2, kp, vp, _i32(table[:1]), _i32(cu_long))
+    assert L.device_error_flags() == 2
+    n = 16 * int((table[0] >= 0).sum())
+    gk2, _ = oracle.paged_gather(k_log, v_log, table[:1], np.array([0, n], np.int32))
+    np.testing.assert_array_equal(bits(to_torch(ko2))[:n], gk2)
+
+
 def test_empty_calls_are_noops():
     _, table, k_log, v_log = _setup(3, [4], 4, 2)
     kp, vp = _dev(k_log, v_log)
