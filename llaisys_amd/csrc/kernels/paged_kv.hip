@@ -35,6 +35,8 @@ __device__ int owningSequence(const int32_t *cu, int B, int r) {
 }
 
 // One 64-lane block per new token row; each lane moves 16 B chunks (8 dims).
+// The row's own loads do not depend on the position or the block table, so
+// each lane's first chunk is loaded before those lookups.
 __global__ void __launch_bounds__(64) appendKernel(uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool,
                                                    const uint16_t *__restrict__ k_new,
                                                    const uint16_t *__restrict__ v_new,
@@ -42,6 +44,13 @@ __global__ void __launch_bounds__(64) appendKernel(uint16_t *__restrict__ k_pool
                                                    const int32_t *__restrict__ cu, int B, int nkvh, int max_pages,
                                                    int num_blocks, int *err) {
     const int r = blockIdx.x;
+    const int chunks = nkvh * 16; // 16 chunks of 8 dims per kv head
+    const size_t row = size_t(r) * nkvh * kHeadDim;
+    uint4 k0 = {}, v0 = {};
+    if (int(threadIdx.x) < chunks) {
+        k0 = *reinterpret_cast<const uint4 *>(k_new + row + threadIdx.x * 8);
+        v0 = *reinterpret_cast<const uint4 *>(v_new + row + threadIdx.x * 8);
+    }
     int b, pos;
     if (cu) {
         b = owningSequence(cu, B, r);
@@ -61,17 +70,15 @@ __global__ void __launch_bounds__(64) appendKernel(uint16_t *__restrict__ k_pool
         if (threadIdx.x == 0) atomicOr(err, kErrBadBlock);
         return;
     }
-    const int chunks = nkvh * 16; // 16 chunks of 8 dims per kv head
     for (int c = threadIdx.x; c < chunks; c += 64) {
         const int h = c >> 4;
         const int d0 = (c & 15) * 8;
-        const size_t src = (size_t(r) * nkvh + h) * kHeadDim + d0;
+        const uint4 kv = c < 64 ? k0 : *reinterpret_cast<const uint4 *>(k_new + row + c * 8);
+        const uint4 vv = c < 64 ? v0 : *reinterpret_cast<const uint4 *>(v_new + row + c * 8);
         const size_t page_base = (size_t(blk) * nkvh + h) * kPageElems;
         // K: 8 consecutive dims are contiguous in the page -> one 16 B store.
-        *reinterpret_cast<uint4 *>(k_pool + page_base + kIndex(t, d0)) =
-            *reinterpret_cast<const uint4 *>(k_new + src);
+        *reinterpret_cast<uint4 *>(k_pool + page_base + kIndex(t, d0)) = kv;
         // V: 8 consecutive dims land 8 elements apart.
-        const uint4 vv = *reinterpret_cast<const uint4 *>(v_new + src);
         const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -94,6 +101,8 @@ __global__ void __launch_bounds__(256) gatherKernel(uint16_t *__restrict__ k_out
     const int page = blockIdx.x;
     const int b = blockIdx.y;
     const int h = blockIdx.z;
+    // The table entry does not depend on the lengths: both loads go out together.
+    const int blk = table[size_t(b) * max_pages + page];
     const int row0 = cu[b];
     const int len = cu[b + 1] - row0;
     if (page * 16 >= len) return;
@@ -102,7 +111,6 @@ __global__ void __launch_bounds__(256) gatherKernel(uint16_t *__restrict__ k_out
         return;
     }
     if (page == max_pages - 1 && len > max_pages * 16 && threadIdx.x == 0) atomicOr(err, kErrTooLong);
-    const int blk = table[size_t(b) * max_pages + page];
     if (blk < 0 || blk >= num_blocks) {
         if (threadIdx.x == 0) atomicOr(err, kErrBadBlock);
         return;
