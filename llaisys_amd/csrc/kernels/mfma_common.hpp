@@ -94,11 +94,20 @@ __device__ __forceinline__ void pairScores(float (&sv)[8], const u32x4 (&ka)[4],
         sa = mfma(asBf16(ka[s]), asBf16(qop[s]), sa);
         sb = mfma(asBf16(kb[s]), asBf16(qop[s]), sb);
     }
-    const int kbase = first_key + grp * 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        sv[i] = (full || kbase + i <= pos) ? sa[i] : -INFINITY;
-        sv[4 + i] = (full || (hasB && kbase + 16 + i <= pos)) ? sb[i] : -INFINITY;
+        sv[i] = sa[i];
+        sv[4 + i] = sb[i];
+    }
+    // A branch of its own: folded into the selects, the wave-uniform `full`
+    // would still leave every compare and select on the path.
+    if (!full) {
+        const int kbase = first_key + grp * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv[i] = kbase + i <= pos ? sv[i] : -INFINITY;
+            sv[4 + i] = (hasB && kbase + 16 + i <= pos) ? sv[4 + i] : -INFINITY;
+        }
     }
 }
 

@@ -121,7 +121,7 @@ __device__ bool blockGeom(const Args &a, int b, int block, TileGeom &t, bool rep
 template <bool OUT_F32>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) prefillKernel(Args a) {
     __shared__ u32x4 kvs[2][kStagePairs * 16 * 64]; // page pairs: K a, K b, V a, V b quarters
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: scalar branches on it
     const int lane = threadIdx.x & 63;
     const int n = lane & 15;
     const int grp = lane >> 4;
