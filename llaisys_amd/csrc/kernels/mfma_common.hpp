@@ -38,6 +38,20 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 
 __device__ __forceinline__ float exp2Fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Max over the lanes n, n+16, n+32, n+48 (the four key groups of a column),
+// by the gfx950 lane swaps: v_permlane32_swap with one value in both operands
+// leaves each lane its own value and its partner 32 lanes away, one in each
+// result; v_permlane16_swap does the same 16 lanes away. Plain VALU, no LDS
+// round trip as a ds_bpermute shuffle would take.
+__device__ __forceinline__ float maxOverGroups(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const float y = fmaxf(__builtin_bit_cast(float, h[0]), __builtin_bit_cast(float, h[1]));
+    const uint32_t v = __builtin_bit_cast(uint32_t, y);
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
 // Keeps the 16-bit halves of a word whose key is valid.
 __device__ __forceinline__ uint32_t keepPair(bool lo, bool hi) {
     return (lo ? 0x0000ffffu : 0u) | (hi ? 0xffff0000u : 0u);
@@ -122,8 +136,7 @@ __device__ __forceinline__ void softmaxUpdate(Acc &acc, const float (&sv)[NP][8]
     for (int j = 0; j < NP; ++j)
 #pragma unroll
         for (int i = 0; i < 8; ++i) mloc = fmaxf(mloc, sv[j][i]);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    mloc = maxOverGroups(mloc);
     // Lazy rescale: a column keeps its running max until a score exceeds it
     // by more than 2^kLazyLog2 (P then stays below that bound). Only when some
     // column of the wave crosses it do all columns move to their true max and
