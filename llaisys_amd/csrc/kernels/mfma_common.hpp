@@ -52,6 +52,21 @@ __device__ __forceinline__ float maxOverGroups(float x) {
     return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP: row shifts by
+// 1, 2, 4, 8 sum within each row of 16 lanes (lanes without a source add 0),
+// then row_bcast:15 adds row 0's total to row 1 and row 2's to row 3, and
+// row_bcast:31 adds the total of rows 0-1 to rows 2-3. All VALU; a shuffle
+// scan would take six LDS round trips.
+__device__ __forceinline__ int waveInclusiveSum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false); // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false); // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false); // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false); // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false); // row_bcast:15 -> rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false); // row_bcast:31 -> rows 2, 3
+    return x;
+}
+
 // Keeps the 16-bit halves of a word whose key is valid.
 __device__ __forceinline__ uint32_t keepPair(bool lo, bool hi) {
     return (lo ? 0x0000ffffu : 0u) | (hi ? 0xffff0000u : 0u);

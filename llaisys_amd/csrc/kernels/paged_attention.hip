@@ -71,26 +71,18 @@ __device__ bool locate(const Args &a, int index, bool blocks, int &b, int &local
         const int bb = base + lane;
         const int ng = bb < a.B ? groupsOf(a, bb) : 0;
         const int ni = blocks ? (ng + kWaves - 1) / kWaves : ng;
-        int incl = ni, gincl = ng;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(incl, off), gy = __shfl_up(gincl, off);
-            if (lane >= off) {
-                incl += y;
-                gincl += gy;
-            }
-        }
-        const int total = __shfl(incl, 63);
+        const int incl = waveInclusiveSum(ni), gincl = waveInclusiveSum(ng);
+        const int total = __builtin_amdgcn_readlane(incl, 63);
         if (remaining < total) {
             const unsigned long long hit = __ballot(incl > remaining);
-            const int first = __ffsll(hit) - 1;
+            const int first = __builtin_amdgcn_readfirstlane(__ffsll(hit) - 1);
             b = base + first;
-            local = remaining - (__shfl(incl, first) - __shfl(ni, first));
-            group_base = groups_before + __shfl(gincl, first) - __shfl(ng, first);
+            local = remaining - (__builtin_amdgcn_readlane(incl, first) - __builtin_amdgcn_readlane(ni, first));
+            group_base = groups_before + __builtin_amdgcn_readlane(gincl, first) - __builtin_amdgcn_readlane(ng, first);
             return true;
         }
         remaining -= total;
-        groups_before += __shfl(gincl, 63);
+        groups_before += __builtin_amdgcn_readlane(gincl, 63);
     }
     return false;
 }

@@ -97,18 +97,13 @@ __device__ int scanPairs(const DecodeArgs &a, int *S, int *C, int *Q, bool repor
             if (!mine) c = 0;
         }
         const int mine_pairs = ((((c + 15) >> 4) + 1) >> 1) * a.nkvh;
-        int incl = mine_pairs;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int y = __shfl_up(incl, off);
-            if (lane >= off) incl += y;
-        }
+        const int incl = waveInclusiveSum(mine_pairs);
         if (bb < a.B) {
             S[bb] = carry + incl - mine_pairs;
             C[bb] = c;
             Q[bb] = row;
         }
-        carry += __shfl(incl, 63);
+        carry += __builtin_amdgcn_readlane(incl, 63);
     }
     if (lane == 0) S[a.B] = carry;
     return carry;
