@@ -110,6 +110,30 @@ __device__ bool blockGeom(const Args &a, int b, int block, TileGeom &t, bool rep
     return true;
 }
 
+// Partial O of a split record, element `idx` of the record's O block. For
+// bf16 outputs it is kept as bf16 (RNE): its 2^-9 relative rounding matches
+// the output's own, and it halves the record bytes that the attention kernel
+// writes and the combine reads. fp32 outputs keep fp32 records. The (m, l)
+// pairs stay fp32 after the O block either way.
+template <bool OUT_F32> __device__ __forceinline__ void storeRecordO(float *rec, int idx, f32x4 v) {
+    if constexpr (OUT_F32) {
+        *reinterpret_cast<f32x4 *>(rec + idx) = v;
+    } else {
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        const bf16x4 h = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+        *reinterpret_cast<bf16x4 *>(reinterpret_cast<uint16_t *>(rec) + idx) = h;
+    }
+}
+template <bool OUT_F32> __device__ __forceinline__ f32x4 loadRecordO(const float *rec, int idx) {
+    if constexpr (OUT_F32) {
+        return *reinterpret_cast<const f32x4 *>(rec + idx);
+    } else {
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        const bf16x4 h = *reinterpret_cast<const bf16x4 *>(reinterpret_cast<const uint16_t *>(rec) + idx);
+        return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    }
+}
+
 template <bool OUT_F32>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) prefillKernel(Args a) {
     __shared__ u32x4 kvs[2][kStagePairs * 16 * 64]; // page pairs: K a, K b, V a, V b quarters
@@ -316,8 +340,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         }
         const int c = k * 16 + n; // column within the group
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<f32x4 *>(rec + (i * kTiles * 16 + c) * 16 + grp * 4) = acc[k].o[i];
+        for (int i = 0; i < 8; ++i) storeRecordO<OUT_F32>(rec, (i * kTiles * 16 + c) * 16 + grp * 4, acc[k].o[i]);
         if (grp == 0)
             *reinterpret_cast<float2 *>(rec + kTiles * 16 * kHeadDim + 2 * c) = make_float2(acc[k].m, lt);
     }
@@ -359,8 +382,7 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64) prefillCombineKern
             mr[s] = k0 + s < t.nsplit ? ml.x : -INFINITY;
             lr[s] = ml.y;
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                orr[s][i] = *reinterpret_cast<const f32x4 *>(rec + (i * kTiles * 16 + c) * 16 + grp * 4);
+            for (int i = 0; i < 8; ++i) orr[s][i] = loadRecordO<OUT_F32>(rec, (i * kTiles * 16 + c) * 16 + grp * 4);
         }
 #pragma unroll
         for (int s = 0; s < kMergeBatch; ++s) {
