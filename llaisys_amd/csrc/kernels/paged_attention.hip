@@ -37,7 +37,7 @@ using namespace mfma;
 
 constexpr int kXcds = 8;
 constexpr int kTiles = 2;                                    // query tiles per wave
-constexpr int kWaves = 4;                                    // waves (groups) per workgroup
+constexpr int kWaves = 8;                                    // waves (groups) per workgroup
 constexpr int kStagePairs = 2;                               // page pairs per LDS stage (one barrier each)
 constexpr int kRecordFloats = kTiles * 16 * (kHeadDim + 2); // O for the group's columns, then (m, l)
 
