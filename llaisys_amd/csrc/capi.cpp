@@ -233,7 +233,14 @@ llaisysTensor_t tensorCreate(size_t *shape, size_t ndim, llaisysDataType_t dtype
 void tensorDestroy(llaisysTensor_t tensor) { delete tensor; }
 
 void *tensorGetData(llaisysTensor_t t) {
-    return guarded([&]() -> void * { return unbox(t, "tensorGetData")->data(); }, nullptr);
+    // The caller may write through the pointer: count it as a write.
+    return guarded(
+        [&]() -> void * {
+            const auto &x = unbox(t, "tensorGetData");
+            x->touch();
+            return x->data();
+        },
+        nullptr);
 }
 
 size_t tensorGetNdim(llaisysTensor_t t) {

@@ -15,6 +15,8 @@
 // split-KV partial results and an error word.
 #pragma once
 
+#include <atomic>
+
 #include "llaisys/runtime.h"
 
 #include <cstddef>
@@ -39,8 +41,14 @@ public:
     // Host storage reports CPU/0, as storage.cpp:21-35.
     llaisysDeviceType_t deviceType() const { return is_host_ ? LLAISYS_DEVICE_CPU : type_; }
     int deviceId() const { return is_host_ ? 0 : id_; }
+    // Write generation: bumped by every write the library cannot see (a load
+    // from the host, a raw data pointer handed out through the C-API), so
+    // copies derived from the bytes (folded model weights) know to refresh.
+    uint64_t version() const { return version_.load(std::memory_order_relaxed); }
+    void touch() { version_.fetch_add(1, std::memory_order_relaxed); }
 
 private:
+    std::atomic<uint64_t> version_{0};
     std::byte *mem_;
     size_t size_;
     const LlaisysRuntimeAPI *api_;

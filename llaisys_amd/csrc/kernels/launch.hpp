@@ -97,11 +97,19 @@ void linear(void *y, const void *x, const void *w, const void *bias, ElemType t,
 // into the paged pool at each token's position (decode: cu == null, T == B;
 // else row r belongs to the sequence b with cu[b] <= r < cu[b+1]);
 // ctx = lengths before the append. Error bits 1 (bad block), 2 (past table).
+// x (may be null): residual rows [T, hs] whose RMSNorm weight was folded into
+// the QKV weights; qkv is then scaled by each row's 1/rms before the bias.
 void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv, const uint16_t *bias,
                    const int32_t *table, const int32_t *ctx, const int32_t *cu, int T, int B, int nh, int nkvh, int d,
-                   int max_pages, int num_blocks, float theta, int *err, void *stream);
+                   int max_pages, int num_blocks, float theta, int *err, const uint16_t *x, int hs, float eps,
+                   void *stream);
 // act [T, di] = up * silu(gate) with gate_up rows [gate (di) | up (di)]; di % 8 == 0.
-void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *stream);
+// x (may be null): as for qkvRopeAppend, gate and up scaled by the row's 1/rms.
+void swigluRows(uint16_t *act, const uint16_t *gate_up, const uint16_t *x, size_t T, int di, int hs, float eps,
+                void *stream);
+// out[r, c] = w[r, c] * g[c] (bf16, one rounding): an RMSNorm weight folded
+// into the columns of the projection that consumes the normalised rows.
+void foldNormColumns(uint16_t *out, const uint16_t *w, const uint16_t *g, size_t rows, int cols, void *stream);
 // Multi-step decode bookkeeping on the device (s = *counter): before a step,
 // ctx_before = base + s, ctx_after = base + s + 1, tok = s ? next : first;
 // after it, history[s][:] = next and *counter = s + 1.

@@ -8,7 +8,13 @@
 //  * swigluRows: act = up * silu(gate) over fused [gate | up] rows
 //    (test/ops/swiglu.py:11-12);
 //  * rmsNormRows: rms_norm of all or selected rows (the last position of each
-//    sequence before the LM head; test/ops/rms_norm.py:11-17).
+//    sequence before the LM head; test/ops/rms_norm.py:11-17);
+//  * foldNormColumns: W' = W diag(w), the RMSNorm weight folded into the
+//    columns of the projection that consumes the normalised rows. With it,
+//    rms_norm(x) W^T = r(x) * (x W'^T), r(x) = 1/sqrt(mean(x^2) + eps), and
+//    the per-row factor r is applied by the kernel that reads the GEMM's
+//    output (qkvRopeAppend, swigluRows take the residual rows x for it), so
+//    the layer runs no separate rms_norm launch.
 #include "launch.hpp"
 
 #include "../common.hpp"
@@ -27,20 +33,64 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ float f(bf16 v) { return __bfloat162float(v); }
 
-// 8 columns per thread (di % 8 == 0): 16 B loads of gate and up, one 16 B store.
-__global__ void swigluRowsKernel(bf16 *act, const bf16 *gu, size_t T, int di) {
-    const int nv = di / 8;
-    const size_t n = T * size_t(nv);
+// 1/sqrt(mean(x^2) + eps) of one row of d (% 8 == 0) bf16 values, computed
+// by the whole 64-lane wave (every lane gets the result), as rmsNormRows does.
+__device__ __forceinline__ float rowInvRms(const bf16 *xrow, int d, float eps) {
+    const int lane = threadIdx.x & 63;
+    const uint4 *src = reinterpret_cast<const uint4 *>(xrow);
+    float ss = 0.f;
+    for (int c = lane; c < d / 8; c += 64) {
+        const uint4 v = src[c];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t u = (&v.x)[e];
+            const float lo = __uint_as_float(u << 16), hi = __uint_as_float(u & 0xffff0000u);
+            ss += lo * lo + hi * hi;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    return rsqrtf(ss / float(d) + eps);
+}
+
+// out[r, c] = bf16(w[r, c] * g[c]) over rows x cols (cols % 8 == 0); the
+// product of two bf16 values is exact in fp32, so this is one rounding.
+__global__ void foldNormColumnsKernel(uint4 *out, const uint4 *w, const uint4 *g, size_t n, int nv) {
     for (size_t i = blockIdx.x * size_t(kThreads) + threadIdx.x; i < n; i += size_t(gridDim.x) * kThreads) {
-        const size_t r = i / nv, c = i - r * nv;
+        const uint4 a = w[i], b = g[i % nv];
+        uint4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t aw = (&a.x)[e], bw = (&b.x)[e];
+            const uint32_t lo = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(aw << 16) *
+                                                                               __uint_as_float(bw << 16)));
+            const uint32_t hi = __builtin_bit_cast(uint16_t, __float2bfloat16(__uint_as_float(aw & 0xffff0000u) *
+                                                                               __uint_as_float(bw & 0xffff0000u)));
+            (&o.x)[e] = lo | (hi << 16);
+        }
+        out[i] = o;
+    }
+}
+
+// Row r = blockIdx.y, 8 columns per thread (di % 8 == 0): 16 B loads of gate
+// and up, one 16 B store. x (may be null): the residual rows whose RMSNorm
+// weight was folded into the gate/up projection; gate and up are then scaled
+// by the row's 1/rms (each wave works it out itself: no barrier).
+__global__ void __launch_bounds__(kThreads) swigluRowsKernel(bf16 *act, const bf16 *gu, const bf16 *x, int di, int hs,
+                                                             float eps) {
+    const int nv = di / 8;
+    const size_t r = blockIdx.y;
+    const float rs = x ? rowInvRms(x + r * hs, hs, eps) : 1.f;
+    const int c = blockIdx.x * kThreads + threadIdx.x;
+    if (c < nv) {
         const uint4 g = reinterpret_cast<const uint4 *>(gu + r * 2 * di)[c];
         const uint4 u = reinterpret_cast<const uint4 *>(gu + r * 2 * di + di)[c];
         uint4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const uint32_t gw = (&g.x)[e], uw = (&u.x)[e];
-            const float g0 = __uint_as_float(gw << 16), g1 = __uint_as_float(gw & 0xffff0000u);
-            const float u0 = __uint_as_float(uw << 16), u1 = __uint_as_float(uw & 0xffff0000u);
+            const float g0 = rs * __uint_as_float(gw << 16), g1 = rs * __uint_as_float(gw & 0xffff0000u);
+            const float u0 = rs * __uint_as_float(uw << 16), u1 = rs * __uint_as_float(uw & 0xffff0000u);
             const uint32_t lo = __builtin_bit_cast(uint16_t, __float2bfloat16(u0 * g0 / (1.f + expf(-g0))));
             const uint32_t hi = __builtin_bit_cast(uint16_t, __float2bfloat16(u1 * g1 / (1.f + expf(-g1))));
             (&o.x)[e] = lo | (hi << 16);
@@ -62,8 +112,10 @@ __device__ __forceinline__ int vPageIndex(int t, int d) {
 __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
     bf16 *q, uint16_t *k_pool, uint16_t *v_pool, const bf16 *qkv, const bf16 *bias, const int32_t *table,
     const int32_t *ctx, const int32_t *cu, int B, int nh, int nkvh, int d, int max_pages, int num_blocks, float theta,
-    int *err) {
+    int *err, const bf16 *x, int hs, float eps) {
     const int r = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
+    // Row factor of the RMSNorm folded into the QKV weights (x null: none).
+    const float rs = x ? rowInvRms(x + size_t(r) * hs, hs, eps) : 1.f;
     int b = r;
     if (cu) {
         int lo = 0, hi = B - 1;
@@ -81,7 +133,7 @@ __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
         float sn, cs;
         sincosf(phi, &sn, &cs);
         const int c = h * d + j;
-        const float a = f(row[c]) + f(bias[c]), bb = f(row[c + half]) + f(bias[c + half]);
+        const float a = rs * f(row[c]) + f(bias[c]), bb = rs * f(row[c + half]) + f(bias[c + half]);
         const bf16 ra = __float2bfloat16(a * cs - bb * sn), rb = __float2bfloat16(bb * cs + a * sn);
         if (h < nh) {
             bf16 *dst = q + (size_t(r) * nh + h) * d;
@@ -100,7 +152,7 @@ __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
     }
     if (h < nh + nkvh) {
         const int c = h * d + j;
-        const float a = f(row[c]) + f(bias[c]), bb = f(row[c + half]) + f(bias[c + half]);
+        const float a = rs * f(row[c]) + f(bias[c]), bb = rs * f(row[c + half]) + f(bias[c + half]);
         const float phi = float(pos) / powf(theta, float(2 * j) / float(d));
         float sn, cs;
         sincosf(phi, &sn, &cs);
@@ -112,7 +164,7 @@ __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
         uint16_t *pg = v_pool + (size_t(blk) * nkvh + hv) * kPageElems;
         for (int dd = 2 * j; dd < 2 * j + 2; ++dd) {
             const int c = (nh + nkvh) * d + hv * d + dd;
-            pg[vPageIndex(slot, dd)] = __builtin_bit_cast(uint16_t, __float2bfloat16(f(row[c]) + f(bias[c])));
+            pg[vPageIndex(slot, dd)] = __builtin_bit_cast(uint16_t, __float2bfloat16(rs * f(row[c]) + f(bias[c])));
         }
     }
 }
@@ -206,24 +258,42 @@ void decodeRecord(int64_t *history, const int64_t *next, int32_t *counter, int B
 
 void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv, const uint16_t *bias,
                    const int32_t *table, const int32_t *ctx, const int32_t *cu, int T, int B, int nh, int nkvh, int d,
-                   int max_pages, int num_blocks, float theta, int *err, void *stream) {
+                   int max_pages, int num_blocks, float theta, int *err, const uint16_t *x, int hs, float eps,
+                   void *stream) {
     if (!T) return;
     LLAISYS_CHECK(d == 128, "qkvRopeAppend: head dim must be 128, got " << d);
+    LLAISYS_CHECK(!x || (hs > 0 && hs % 8 == 0), "qkvRopeAppend: hidden size must be a positive multiple of 8");
     hipLaunchKernelGGL(qkvRopeAppendKernel, dim3(unsigned(T), unsigned(nh + 2 * nkvh)), dim3(d / 2), 0,
                        static_cast<hipStream_t>(stream),
                        reinterpret_cast<bf16 *>(q), k_pool, v_pool, reinterpret_cast<const bf16 *>(qkv),
                        reinterpret_cast<const bf16 *>(bias), table, ctx, cu, B, nh, nkvh, d, max_pages, num_blocks,
-                       theta, err);
+                       theta, err, reinterpret_cast<const bf16 *>(x), hs, eps);
     HIP_CHECK(hipGetLastError());
 }
 
-void swigluRows(uint16_t *act, const uint16_t *gate_up, size_t T, int di, void *stream) {
+void swigluRows(uint16_t *act, const uint16_t *gate_up, const uint16_t *x, size_t T, int di, int hs, float eps,
+                void *stream) {
     LLAISYS_CHECK(di % 8 == 0, "swigluRows: di must be a multiple of 8, got " << di);
-    const size_t n = T * size_t(di / 8);
+    LLAISYS_CHECK(!x || (hs > 0 && hs % 8 == 0), "swigluRows: hidden size must be a positive multiple of 8");
+    constexpr size_t kMaxRows = 65535; // grid y limit: longer batches take several launches
+    for (size_t r0 = 0; r0 < T; r0 += kMaxRows) {
+        const size_t rows = std::min(kMaxRows, T - r0);
+        const dim3 grid(unsigned((di / 8 + kThreads - 1) / kThreads), unsigned(rows));
+        hipLaunchKernelGGL(swigluRowsKernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                           reinterpret_cast<bf16 *>(act + r0 * di), reinterpret_cast<const bf16 *>(gate_up + r0 * 2 * di),
+                           x ? reinterpret_cast<const bf16 *>(x + r0 * hs) : nullptr, di, hs, eps);
+        HIP_CHECK(hipGetLastError());
+    }
+}
+
+void foldNormColumns(uint16_t *out, const uint16_t *w, const uint16_t *g, size_t rows, int cols, void *stream) {
+    LLAISYS_CHECK(cols % 8 == 0, "foldNormColumns: cols must be a multiple of 8, got " << cols);
+    const size_t n = rows * size_t(cols / 8);
     if (!n) return;
     const unsigned grid = unsigned(std::min<size_t>((n + kThreads - 1) / kThreads, 65536));
-    hipLaunchKernelGGL(swigluRowsKernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                       reinterpret_cast<bf16 *>(act), reinterpret_cast<const bf16 *>(gate_up), T, di);
+    hipLaunchKernelGGL(foldNormColumnsKernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<uint4 *>(out), reinterpret_cast<const uint4 *>(w),
+                       reinterpret_cast<const uint4 *>(g), n, cols / 8);
     HIP_CHECK(hipGetLastError());
 }
 

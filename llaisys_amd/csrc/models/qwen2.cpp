@@ -55,6 +55,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     LLAISYS_CHECK(num_blocks > 0 && num_blocks < (size_t(1) << 31), "qwen2: bad KV block count " << num_blocks);
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     if (const char *e = std::getenv("LLAISYS_QWEN2_GRAPHS")) use_graphs_ = e[0] != '0';
+    if (const char *e = std::getenv("LLAISYS_QWEN2_FOLD_NORM")) fold_norm_ = e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -77,6 +78,10 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
         L.v_b = L.qkv_b->slice(0, q + kv, q + 2 * kv);
         L.gate_w = L.gate_up_w->slice(0, 0, cfg.di);
         L.up_w = L.gate_up_w->slice(0, cfg.di, 2 * cfg.di);
+        if (fold_norm_) {
+            L.qkv_wf = dev({q + 2 * kv, cfg.hs}, dt, dev_);
+            L.gate_up_wf = dev({2 * cfg.di, cfg.hs}, dt, dev_);
+        }
     }
     for (size_t l = 0; l < cfg.nlayer; ++l) {
         k_pool_.push_back(dev({num_blocks, cfg.nkvh, size_t(K::kPageTokens), cfg.dh}, LLAISYS_DTYPE_BF16, dev_));
@@ -211,6 +216,7 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     LLAISYS_CHECK(nseq > 0, "qwen2 step: no sequences");
     LLAISYS_CHECK(ids && tokens && ntokens && next, "qwen2 step: null argument");
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
+    ensureFolded();
     auto &rt = core::context().runtime();
     const size_t B = nseq;
     size_t T = 0;
@@ -293,6 +299,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     LLAISYS_CHECK(nseq > 0 && nsteps > 0, "qwen2 decode: no sequences or no steps");
     LLAISYS_CHECK(ids && first && out, "qwen2 decode: null argument");
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
+    ensureFolded();
     auto &rt = core::context().runtime();
     const size_t B = nseq;
     for (size_t i = 0; i < B; ++i) {
@@ -387,6 +394,26 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     }
 }
 
+void Qwen2Model::ensureFolded() {
+    if (!fold_norm_) return;
+    void *s = core::context().runtime().stream();
+    for (auto &L : layers_) {
+        const uint64_t v[4] = {L.qkv_w->version(), L.attn_norm->version(), L.gate_up_w->version(),
+                               L.mlp_norm->version()};
+        if (v[0] != L.folded_from[0] || v[1] != L.folded_from[1]) {
+            K::foldNormColumns(u16(L.qkv_wf), u16(L.qkv_w), u16(L.attn_norm), L.qkv_w->shape()[0], int(cfg_.hs), s);
+            L.folded_from[0] = v[0];
+            L.folded_from[1] = v[1];
+        }
+        if (v[2] != L.folded_from[2] || v[3] != L.folded_from[3]) {
+            K::foldNormColumns(u16(L.gate_up_wf), u16(L.gate_up_w), u16(L.mlp_norm), L.gate_up_w->shape()[0],
+                               int(cfg_.hs), s);
+            L.folded_from[2] = v[2];
+            L.folded_from[3] = v[3];
+        }
+    }
+}
+
 void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     auto &rt = core::context().runtime();
     void *s = rt.stream();
@@ -400,16 +427,20 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     const tensor_t q3 = rows(q_, T), a3 = rows(attn_, T);
     for (size_t l = 0; l < cfg_.nlayer; ++l) {
         const auto &L = layers_[l];
-        K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
-        gemm(qkv_, h_, L.qkv_w, nullptr, M, q + 2 * kv, hs, false, s);
+        // Folded norms: the projections read the residual x itself and the
+        // next kernel applies each row's 1/rms (see foldNormColumns).
+        const uint16_t *xr = fold_norm_ ? u16(x_) : nullptr;
+        if (!fold_norm_) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
+        gemm(qkv_, fold_norm_ ? x_ : h_, fold_norm_ ? L.qkv_wf : L.qkv_w, nullptr, M, q + 2 * kv, hs, false, s);
         K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
                          i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh), int(cfg_.nkvh),
-                         int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), s);
+                         int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), xr, hs,
+                         cfg_.epsilon, s);
         ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_, scale);
         gemm(x_, attn_, L.o_w, nullptr, M, hs, q, true, s);
-        K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
-        gemm(gu_, h_, L.gate_up_w, nullptr, M, 2 * di, hs, false, s);
-        K::swigluRows(u16(act_), u16(gu_), T, di, s);
+        if (!fold_norm_) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
+        gemm(gu_, fold_norm_ ? x_ : h_, fold_norm_ ? L.gate_up_wf : L.gate_up_w, nullptr, M, 2 * di, hs, false, s);
+        K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s);
         gemm(x_, act_, L.down_w, nullptr, M, hs, di, true, s);
     }
     K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);

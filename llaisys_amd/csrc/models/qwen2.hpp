@@ -36,6 +36,11 @@ struct Qwen2LayerWeights {
     tensor_t attn_norm, qkv_w, qkv_b, o_w, mlp_norm, gate_up_w, down_w;
     // reference-named slices of the fused tensors
     tensor_t q_w, k_w, v_w, q_b, k_b, v_b, gate_w, up_w;
+    // qkv_w and gate_up_w with the preceding RMSNorm weight folded into their
+    // columns (W diag(w)), and the write versions of (qkv_w, attn_norm,
+    // gate_up_w, mlp_norm) they were folded from
+    tensor_t qkv_wf, gate_up_wf;
+    uint64_t folded_from[4] = {~0ull, ~0ull, ~0ull, ~0ull};
 };
 
 class Qwen2Model {
@@ -78,6 +83,9 @@ public:
 private:
     void ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints64);
     void forward(size_t T, size_t B, bool decode_only);
+    // Refold each layer whose projection or norm weights were written since
+    // their folded copies were made (a check of version counters per step).
+    void ensureFolded();
     void decodeGraph(size_t B, size_t width);
     std::vector<int32_t> reserveAll(const int64_t *ids, size_t B, const size_t *n, std::vector<int32_t> &before);
 
@@ -110,6 +118,7 @@ private:
     };
     DecodeGraph capture(const std::function<void()> &work, size_t width);
     bool use_graphs_ = true;
+    bool fold_norm_ = true; // LLAISYS_QWEN2_FOLD_NORM=0: separate rms_norm launches instead
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
     std::map<size_t, DecodeGraph> graphs_;       // one step (step())
     std::map<size_t, DecodeGraph> multi_graphs_; // advance + step + record (decode())

@@ -199,6 +199,7 @@ void Tensor::load(const void *host_src) {
     LLAISYS_CHECK(isContiguous(), "load: tensor must be contiguous");
     size_t bytes = numel() * elementSize();
     if (!bytes) return;
+    touch();
     auto &ctx = core::context();
     if (deviceType() == LLAISYS_DEVICE_CPU) {
         std::memcpy(data(), host_src, bytes);

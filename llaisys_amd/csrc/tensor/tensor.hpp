@@ -37,6 +37,9 @@ public:
     tensor_t slice(size_t dim, size_t start, size_t end) const;
     tensor_t view(const std::vector<size_t> &shape) const;
     void load(const void *host_src);
+    // Write generation of the underlying storage (shared by views and slices).
+    uint64_t version() const { return storage_->version(); }
+    void touch() const { storage_->touch(); }
 
 private:
     Tensor(llaisysDataType_t dtype, std::vector<size_t> shape, std::vector<ptrdiff_t> strides,

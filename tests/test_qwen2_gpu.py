@@ -337,3 +337,53 @@ def test_warm_up_leaves_the_pool_free_and_the_model_correct():
     nxt = model.infer(toks)
     ref = hf_logits(hf, toks)[-1]
     check_token(nxt, ref, check_logits(to_torch(model.logits())[0], ref))
+
+
+def test_rewritten_weights_reach_the_folded_projections():
+    # The qkv and gate/up projections run on copies with the RMSNorm weight
+    # folded into their columns. Weights written after a step, by tensorLoad
+    # or through a raw data pointer, must refresh those copies at the next step.
+    model, hf = build("tiny")
+    toks = prompt(23, model.meta.voc, 5)
+    model.infer(toks)
+    check_logits(to_torch(model.logits())[0], hf_logits(hf, toks)[-1])
+    toks2 = [2] + toks
+    stale = hf_logits(hf, toks2)[-1]
+    params = dict(hf.named_parameters())
+    torch.manual_seed(11)
+    with torch.no_grad():
+        for name in ("model.layers.0.input_layernorm.weight", "model.layers.1.mlp.gate_proj.weight"):
+            p = params[name]
+            p.copy_((p + 0.2 * torch.randn_like(p)).to(torch.bfloat16).float())
+            host = p.detach().to(torch.bfloat16).cpu().contiguous()  # alive until tensorLoad returns
+            model.load_weight(name, host.data_ptr())
+        name = "model.layers.1.post_attention_layernorm.weight"
+        p = params[name]
+        p.copy_((p * 1.5).to(torch.bfloat16).float())
+        h = L.Tensor(tensor=model.weight_handle(name))
+        try:
+            src = p.detach().to(torch.bfloat16).contiguous()
+            L.RuntimeAPI(L.DeviceType.AMD).memcpy_sync(h.data_ptr(), src.data_ptr(), src.numel() * 2,
+                                                       L.MemcpyKind.D2D)
+        finally:
+            h._tensor = None  # borrowed handle: the model owns it
+    # A new history shares no cached prefix, so every position runs on the new weights.
+    nxt = model.infer(toks2)
+    ref = hf_logits(hf, toks2)[-1]
+    tol = check_logits(to_torch(model.logits())[0], ref)
+    check_token(nxt, ref, tol)
+    # stale folded copies would fail the check above: the rewrite moves the logits
+    assert (ref - stale).abs().max().item() > 2 * tol
+
+
+def test_unfolded_norm_path_matches_transformers(monkeypatch):
+    # LLAISYS_QWEN2_FOLD_NORM=0: separate rms_norm launches on the original weights.
+    monkeypatch.setenv("LLAISYS_QWEN2_FOLD_NORM", "0")
+    model, hf = build("gqa12")
+    toks = prompt(29, model.meta.voc, 2)
+    for _ in range(3):
+        nxt = model.infer(toks)
+        ref = hf_logits(hf, toks)[-1]
+        tol = check_logits(to_torch(model.logits())[0], ref)
+        check_token(nxt, ref, tol)
+        toks = toks + [int(ref.argmax())]
