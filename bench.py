@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--steps", type=int, default=None, help="timed steps (default: 200; qwen2: 64)")
     p.add_argument("--warmup", type=int, default=None, help="untimed steps (default: 20; qwen2: 4)")
     p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy", "qwen2", "serve"])
+    p.add_argument("--ag-fused-only", action="store_true",
+                   help="--workload append_gather: time only the fused entry point (profiling runs)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-model", action="store_true",
@@ -532,7 +534,10 @@ def run_append_gather(args):
     cut = to_llaisys(torch.from_numpy(cu))
     stream = torch.cuda.ExternalStream(L.context_stream())
 
-    def step(i):
+    def step(i):  # one launch: the append fused into the gather
+        L.Ops.paged_kv_append_gather(ko, vo, kp, vp, kn, vn, tab, ctx, cut)
+
+    def step_two_calls(i):
         L.Ops.paged_kv_append(kp, vp, kn, vn, tab, ctx)
         L.Ops.paged_kv_gather(ko, vo, kp, vp, tab, cut)
 
@@ -540,6 +545,10 @@ def run_append_gather(args):
     # flush so the inputs come from HBM, and report the cache-warm rate beside it.
     kern_ms, wall_ms = time_steps_flushed(step, stream, args.steps, args.warmup)
     warm_ms, _ = time_steps(step, stream, args.steps, args.warmup)
+    two_ms = two_warm_ms = None
+    if not getattr(args, "ag_fused_only", False):
+        two_ms, _ = time_steps_flushed(step_two_calls, stream, args.steps, args.warmup)
+        two_warm_ms, _ = time_steps(step_two_calls, stream, args.steps, args.warmup)
     nbytes = 2 * T * 1024 + 2 * B * 1024
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
     return {
@@ -548,9 +557,14 @@ def run_append_gather(args):
         "kernel_ms": round(kern_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "BASELINE config 2: 32 seqs len U[1,2048], 4096-block pool, append 1 + gather",
+                   "entry_point": "llaisysPagedKVAppendGather (append fused into the gather, one launch)",
                    "timing": "HIP events per step, L2/MALL flushed by an untimed 512 MiB read before each step"},
         "mall_resident": {"kernel_ms": round(warm_ms, 5), "GB/s": round(nbytes / (warm_ms * 1e-3) / 1e9, 2),
                           "timing": "back-to-back steps, inputs left in the MALL"},
+        "two_calls": None if two_ms is None else {
+            "entry_points": "llaisysPagedKVAppend then llaisysPagedKVGather",
+            "kernel_ms": round(two_ms, 5), "GB/s": round(nbytes / (two_ms * 1e-3) / 1e9, 2),
+            "mall_resident_kernel_ms": round(two_warm_ms, 5)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles("paged_kv_append_gather_config2"),

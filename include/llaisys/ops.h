@@ -79,6 +79,18 @@ __C {
                                        llaisysTensor_t v_pool, llaisysTensor_t block_table,
                                        llaisysTensor_t cu_seqlens);
 
+    /* New; no counterpart in the reference (its KV cache is a README prompt,
+     * README.md:316, :412). llaisysPagedKVAppend of one token per sequence
+     * (k_new, v_new: [B, nkvh, 128] BF16, written at position ctx_len[b])
+     * followed by llaisysPagedKVGather of the contexts including it, in one
+     * launch: cu_seqlens [B+1] must give every sequence ctx_len[b] + 1 output
+     * rows (a sequence that does not raises device error flag 2 and is
+     * skipped). Same bytes in the pool and in k_out, v_out as the two calls. */
+    __export void llaisysPagedKVAppendGather(llaisysTensor_t k_out, llaisysTensor_t v_out, llaisysTensor_t k_pool,
+                                             llaisysTensor_t v_pool, llaisysTensor_t k_new, llaisysTensor_t v_new,
+                                             llaisysTensor_t block_table, llaisysTensor_t ctx_len,
+                                             llaisysTensor_t cu_seqlens);
+
     /* New. Copy whole (block, all kv heads) pages inside the pools:
      * pairs [P, 2] I32 of (src, dst) block ids, as produced by
      * llaisysKVSeqReserve for copy-on-write of a shared last block. */

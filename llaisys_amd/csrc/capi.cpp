@@ -367,6 +367,17 @@ void llaisysPagedKVGather(llaisysTensor_t k_out, llaisysTensor_t v_out, llaisysT
     });
 }
 
+void llaisysPagedKVAppendGather(llaisysTensor_t k_out, llaisysTensor_t v_out, llaisysTensor_t k_pool,
+                                llaisysTensor_t v_pool, llaisysTensor_t k_new, llaisysTensor_t v_new,
+                                llaisysTensor_t block_table, llaisysTensor_t ctx_len, llaisysTensor_t cu_seqlens) {
+    guardedVoid([&] {
+        const char *w = "paged_kv_append_gather";
+        llaisys::ops::pagedKVAppendGather(unbox(k_out, w), unbox(v_out, w), unbox(k_pool, w), unbox(v_pool, w),
+                                          unbox(k_new, w), unbox(v_new, w), unbox(block_table, w),
+                                          unbox(ctx_len, w), unbox(cu_seqlens, w));
+    });
+}
+
 void llaisysPagedAttention(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor_t k_pool, llaisysTensor_t v_pool,
                            llaisysTensor_t block_table, llaisysTensor_t ctx_len, float scale) {
     guardedVoid([&] {

@@ -27,6 +27,14 @@ void pagedGather(uint16_t *k_out, uint16_t *v_out, const uint16_t *k_pool, const
                  const int32_t *block_table, const int32_t *cu_seqlens, int T, int B, int nkvh, int max_pages,
                  int num_blocks, int *err, void *stream);
 
+// Append of one token per sequence (k_new/v_new [B, nkvh, 128]) fused into the
+// gather of the contexts including it (cu_seqlens[b+1] - cu_seqlens[b] must be
+// ctx_len[b] + 1).
+void pagedAppendGather(uint16_t *k_out, uint16_t *v_out, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *k_new,
+                       const uint16_t *v_new, const int32_t *block_table, const int32_t *ctx_len,
+                       const int32_t *cu_seqlens, int T, int B, int nkvh, int max_pages, int num_blocks, int *err,
+                       void *stream);
+
 // Batched decode: stream-K over all page pairs, then a combine kernel for
 // sequences split across waves. cu_q == nullptr: sequence b's query is row b
 // (T == B); else its row is cu_q[b] and sequences with cu_q[b+1]-cu_q[b] != 1

@@ -136,6 +136,83 @@ __global__ void __launch_bounds__(256) gatherKernel(uint16_t *__restrict__ k_out
     *reinterpret_cast<uint4 *>(v_out + dst) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Append then gather in one launch, for one new token per sequence: the
+// gather grid of gatherKernel, where the block holding page ctx[b] / 16 of
+// sequence b also writes the new token's K/V (k_new/v_new row b) into slot
+// ctx[b] % 16 of that page, in the pool and in its LDS copy, before the rows
+// go out. Output rows of sequence b: [cu[b], cu[b+1]) with cu[b+1] - cu[b]
+// == ctx[b] + 1 (other sequences raise kErrTooLong and are skipped). Same
+// bytes as appendKernel followed by gatherKernel; the append's own chain of
+// lookups no longer runs ahead of the gather.
+__global__ void __launch_bounds__(256) appendGatherKernel(
+    uint16_t *__restrict__ k_out, uint16_t *__restrict__ v_out, uint16_t *__restrict__ k_pool,
+    uint16_t *__restrict__ v_pool, const uint16_t *__restrict__ k_new, const uint16_t *__restrict__ v_new,
+    const int32_t *__restrict__ table, const int32_t *__restrict__ ctx, const int32_t *__restrict__ cu, int T,
+    int nkvh, int max_pages, int num_blocks, int *err) {
+    __shared__ uint4 ks[256];
+    __shared__ uint16_t vs[kPageElems];
+    const int page = blockIdx.x;
+    const int b = blockIdx.y;
+    const int h = blockIdx.z;
+    const int tid = threadIdx.x;
+    // None of these loads depends on another: all go out together.
+    const int blk = table[size_t(b) * max_pages + page];
+    const int c = ctx[b];
+    const int row0 = cu[b];
+    const int len = cu[b + 1] - row0;
+    // The new row does not depend on the lookups either.
+    const size_t new_row = (size_t(b) * nkvh + h) * kHeadDim;
+    uint4 kv = {};
+    uint16_t vv = 0;
+    if (tid < 16)
+        kv = reinterpret_cast<const uint4 *>(k_new + new_row)[tid];
+    else if (tid < 16 + kHeadDim)
+        vv = v_new[new_row + tid - 16];
+    if (c < 0 || len != c + 1) { // output rows must hold the context plus the new token
+        if (page == 0 && h == 0 && tid == 0) atomicOr(err, kErrTooLong);
+        return;
+    }
+    if (page * 16 >= len) return;
+    if (row0 < 0 || cu[b + 1] > T) {
+        if (tid == 0) atomicOr(err, kErrTooLong);
+        return;
+    }
+    if (page == max_pages - 1 && len > max_pages * 16 && tid == 0) atomicOr(err, kErrTooLong);
+    if (blk < 0 || blk >= num_blocks) {
+        if (tid == 0) atomicOr(err, kErrBadBlock);
+        return;
+    }
+    const size_t page_base = (size_t(blk) * nkvh + h) * kPageElems;
+    ks[tid] = reinterpret_cast<const uint4 *>(k_pool + page_base)[tid];
+    reinterpret_cast<uint4 *>(vs)[tid] = reinterpret_cast<const uint4 *>(v_pool + page_base)[tid];
+    if (page == (c >> 4)) { // block-uniform: this block's page receives the new token
+        const int slot = c & 15;
+        __syncthreads(); // the page is in LDS before its slot is overwritten
+        if (tid < 16) {
+            ks[tid * 16 + slot] = kv; // K chunk tid of token `slot`
+            *reinterpret_cast<uint4 *>(k_pool + page_base + kIndex(slot, tid * 8)) = kv;
+        } else if (tid < 16 + kHeadDim) {
+            const int d = tid - 16;
+            vs[vIndex(slot, d)] = vv;
+            v_pool[page_base + vIndex(slot, d)] = vv;
+        }
+    }
+    __syncthreads();
+    const int t = tid >> 4;
+    const int cc = tid & 15;
+    if (page * 16 + t >= len) return;
+    const size_t dst = (size_t(row0 + page * 16 + t) * nkvh + h) * kHeadDim + cc * 8;
+    *reinterpret_cast<uint4 *>(k_out + dst) = ks[cc * 16 + t];
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const uint32_t lo = vs[vIndex(t, cc * 8 + e)];
+        const uint32_t hi = vs[vIndex(t, cc * 8 + e + 1)];
+        w[e >> 1] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4 *>(v_out + dst) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // One 256-thread block per (pair, pool): 16 B per thread per 4 KiB page,
 // looping over the kv heads of the block.
 __global__ void __launch_bounds__(256) copyBlocksKernel(uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool,
@@ -178,6 +255,17 @@ void pagedGather(uint16_t *k_out, uint16_t *v_out, const uint16_t *k_pool, const
     // One block per possible page; blocks past a sequence's length exit at once.
     hipLaunchKernelGGL(gatherKernel, dim3(max_pages, B, nkvh), dim3(256), 0, static_cast<hipStream_t>(stream), k_out,
                        v_out, k_pool, v_pool, block_table, cu_seqlens, T, nkvh, max_pages, num_blocks, err);
+    HIP_CHECK(hipGetLastError());
+}
+
+void pagedAppendGather(uint16_t *k_out, uint16_t *v_out, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *k_new,
+                       const uint16_t *v_new, const int32_t *block_table, const int32_t *ctx_len,
+                       const int32_t *cu_seqlens, int T, int B, int nkvh, int max_pages, int num_blocks, int *err,
+                       void *stream) {
+    if (B == 0 || max_pages == 0) return;
+    hipLaunchKernelGGL(appendGatherKernel, dim3(max_pages, B, nkvh), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       k_out, v_out, k_pool, v_pool, k_new, v_new, block_table, ctx_len, cu_seqlens, T, nkvh,
+                       max_pages, num_blocks, err);
     HIP_CHECK(hipGetLastError());
 }
 

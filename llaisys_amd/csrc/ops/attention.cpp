@@ -172,6 +172,43 @@ void pagedKVGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t 
                    int(block_table->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
 }
 
+void pagedKVAppendGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t &k_pool, const tensor_t &v_pool,
+                         const tensor_t &k_new, const tensor_t &v_new, const tensor_t &block_table,
+                         const tensor_t &ctx_len, const tensor_t &cu_seqlens) {
+    const char *op = "paged_kv_append_gather";
+    LLAISYS_CHECK(k_out && v_out && k_pool && v_pool && k_new && v_new && block_table && ctx_len && cu_seqlens,
+                  op << ": null tensor");
+    checkPool(k_pool, v_pool, op);
+    const size_t nkvh = k_pool->shape()[1];
+    for (const auto *t : {&k_out, &k_new}) {
+        const char *name = t == &k_out ? "k_out" : "k_new";
+        LLAISYS_CHECK((*t)->ndim() == 3 && (*t)->shape()[1] == nkvh && (*t)->shape()[2] == size_t(K::kHeadDim),
+                      op << ": " << name << " must be [rows, nkvh=" << nkvh << ", 128], got " << shapeStr(*t));
+    }
+    LLAISYS_CHECK(v_out->shape() == k_out->shape(), op << ": v_out shape differs from k_out");
+    LLAISYS_CHECK(v_new->shape() == k_new->shape(), op << ": v_new shape differs from k_new");
+    for (const auto *t : {&k_out, &v_out, &k_new, &v_new}) {
+        requireDtype(*t, LLAISYS_DTYPE_BF16, op, "k_out, v_out, k_new and v_new");
+        requireContiguous(*t, op, "k_out, v_out, k_new and v_new");
+    }
+    LLAISYS_CHECK(cu_seqlens->ndim() == 1 && cu_seqlens->shape()[0] >= 1, op << ": cu_seqlens must be [B+1]");
+    const size_t B = cu_seqlens->shape()[0] - 1;
+    checkI32Vec(cu_seqlens, B + 1, op, "cu_seqlens");
+    checkI32Vec(ctx_len, B, op, "ctx_len");
+    checkTable(block_table, B, op);
+    LLAISYS_CHECK(k_new->shape()[0] == B, op << ": k_new must hold one token per sequence (rows=" << k_new->shape()[0]
+                                             << ", B=" << B << ")");
+    requireAmd(op, {&k_out, &v_out, &k_pool, &v_pool, &k_new, &v_new, &block_table, &ctx_len, &cu_seqlens});
+    K::pagedAppendGather(reinterpret_cast<uint16_t *>(k_out->data()), reinterpret_cast<uint16_t *>(v_out->data()),
+                         reinterpret_cast<uint16_t *>(k_pool->data()), reinterpret_cast<uint16_t *>(v_pool->data()),
+                         reinterpret_cast<const uint16_t *>(k_new->data()),
+                         reinterpret_cast<const uint16_t *>(v_new->data()),
+                         reinterpret_cast<const int32_t *>(block_table->data()),
+                         reinterpret_cast<const int32_t *>(ctx_len->data()),
+                         reinterpret_cast<const int32_t *>(cu_seqlens->data()), int(k_out->shape()[0]), int(B),
+                         int(nkvh), int(block_table->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
+}
+
 void pagedKVCopyBlocks(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_t &pairs) {
     const char *op = "paged_kv_copy_blocks";
     LLAISYS_CHECK(k_pool && v_pool && pairs, op << ": null tensor");

@@ -13,6 +13,9 @@ void pagedKVAppend(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_
 
 void pagedKVGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t &k_pool, const tensor_t &v_pool,
                    const tensor_t &block_table, const tensor_t &cu_seqlens);
+void pagedKVAppendGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t &k_pool, const tensor_t &v_pool,
+                         const tensor_t &k_new, const tensor_t &v_new, const tensor_t &block_table,
+                         const tensor_t &ctx_len, const tensor_t &cu_seqlens);
 
 void pagedKVCopyBlocks(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_t &pairs);
 

@@ -24,6 +24,8 @@ def load_ops(lib):
         ("llaisysPagedKVCopyBlocks", [T, T, T]),
         # k_out, v_out, k_pool, v_pool, block_table, cu_seqlens
         ("llaisysPagedKVGather", [T, T, T, T, T, T]),
+        # k_out, v_out, k_pool, v_pool, k_new, v_new, block_table, ctx_len, cu_seqlens
+        ("llaisysPagedKVAppendGather", [T, T, T, T, T, T, T, T, T]),
         # out, q, k_pool, v_pool, block_table, ctx_len, scale
         ("llaisysPagedAttention", [T, T, T, T, T, T, c_float]),
         # out, q, k_pool, v_pool, block_table, cu_q, ctx_len, scale

@@ -77,6 +77,15 @@ class Ops:
         check_last_error()
 
     @staticmethod
+    def paged_kv_append_gather(k_out: Tensor, v_out: Tensor, k_pool: Tensor, v_pool: Tensor, k_new: Tensor,
+                               v_new: Tensor, block_table: Tensor, ctx_len: Tensor, cu_seqlens: Tensor):
+        """paged_kv_append of one token per sequence, then paged_kv_gather of the
+        contexts including it (cu_seqlens[b+1] - cu_seqlens[b] == ctx_len[b] + 1), in one launch."""
+        LIB_LLAISYS.llaisysPagedKVAppendGather(_h(k_out), _h(v_out), _h(k_pool), _h(v_pool), _h(k_new), _h(v_new),
+                                               _h(block_table), _h(ctx_len), _h(cu_seqlens))
+        check_last_error()
+
+    @staticmethod
     def paged_kv_copy_blocks(k_pool: Tensor, v_pool: Tensor, pairs: Tensor):
         """Copy whole blocks (src -> dst, pairs [P, 2] I32), e.g. for copy-on-write."""
         LIB_LLAISYS.llaisysPagedKVCopyBlocks(_h(k_pool), _h(v_pool), _h(pairs))

@@ -148,3 +148,84 @@ def test_empty_calls_are_noops():
     empty = to_llaisys(torch.zeros((0, 2, 128), dtype=torch.bfloat16, device="cuda"))
     L.Ops.paged_kv_append(kp, vp, empty, empty, _i32(table), _i32([4]), _i32([0, 0]))
     np.testing.assert_array_equal(_pool_logical(kp, False, k_log.shape), k_log)
+
+
+def _fused_case(lens, nkvh, seed, nb=None):
+    lens = np.asarray(lens, np.int32)
+    nb = nb or int(((lens + 16) // 16).sum()) + 3
+    lens, table, k_log, v_log = _setup(seed, lens, nb, nkvh)
+    B = len(lens)
+    kn = oracle.randint(seed + 3, B * nkvh * 128, 0, 65535).astype(np.uint16).reshape(B, nkvh, 128)
+    vn = oracle.randint(seed + 4, B * nkvh * 128, 0, 65535).astype(np.uint16).reshape(B, nkvh, 128)
+    return lens, table, k_log, v_log, kn, vn
+
+
+@pytest.mark.parametrize("nkvh", [1, 2, 3])
+def test_fused_append_gather_equals_append_then_gather(nkvh):
+    # Contexts that put the new token at a page start (0, 16, 32), a page end
+    # (15, 31), mid-page, and one long sequence: same pool and output bytes as
+    # the oracle's append followed by its gather.
+    lens, table, k_log, v_log, kn, vn = _fused_case([0, 15, 16, 31, 32, 7, 300, 1], nkvh, 31)
+    kp, vp = _dev(k_log, v_log)
+    cu = np.concatenate([[0], np.cumsum(lens + 1)]).astype(np.int32)
+    T = int(cu[-1])
+    ko = to_llaisys(torch.zeros((T, nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    vo = to_llaisys(torch.zeros((T, nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    L.Ops.paged_kv_append_gather(ko, vo, kp, vp, to_llaisys(from_bits(kn)), to_llaisys(from_bits(vn)), _i32(table),
+                                 _i32(lens), _i32(cu))
+    assert L.device_error_flags() == 0
+    assert oracle.paged_append(k_log, v_log, kn, vn, table, lens) == 0
+    np.testing.assert_array_equal(_pool_logical(kp, False, k_log.shape), k_log)
+    np.testing.assert_array_equal(_pool_logical(vp, True, v_log.shape), v_log)
+    gk, gv = oracle.paged_gather(k_log, v_log, table, cu)
+    np.testing.assert_array_equal(bits(to_torch(ko)), gk)
+    np.testing.assert_array_equal(bits(to_torch(vo)), gv)
+
+
+def test_fused_append_gather_config2_bit_exact():
+    # BASELINE config 2 through the fused entry point.
+    B, nb, nkvh = 32, 4096, 2
+    seed = 0
+    while True:
+        lens = oracle.randint(seed, B, 1, 2048).astype(np.int32)
+        if ((lens + 16) // 16).sum() <= nb:
+            break
+        seed += 1
+    lens, table, k_log, v_log = _setup(100, lens, nb, nkvh)
+    kp, vp = _dev(k_log, v_log)
+    kn = oracle.f32_to_bf16(oracle.randn(7, (B, nkvh, 128)))
+    vn = oracle.f32_to_bf16(oracle.randn(8, (B, nkvh, 128)))
+    cu = np.concatenate([[0], np.cumsum(lens + 1)]).astype(np.int32)
+    T = int(cu[-1])
+    ko = to_llaisys(torch.zeros((T, nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    vo = to_llaisys(torch.zeros((T, nkvh, 128), dtype=torch.bfloat16, device="cuda"))
+    L.Ops.paged_kv_append_gather(ko, vo, kp, vp, to_llaisys(from_bits(kn)), to_llaisys(from_bits(vn)), _i32(table),
+                                 _i32(lens), _i32(cu))
+    assert L.device_error_flags() == 0
+    assert oracle.paged_append(k_log, v_log, kn, vn, table, lens) == 0
+    np.testing.assert_array_equal(_pool_logical(kp, False, k_log.shape), k_log)
+    np.testing.assert_array_equal(_pool_logical(vp, True, v_log.shape), v_log)
+    gk, gv = oracle.paged_gather(k_log, v_log, table, cu)
+    np.testing.assert_array_equal(bits(to_torch(ko)), gk)
+    np.testing.assert_array_equal(bits(to_torch(vo)), gv)
+
+
+def test_fused_append_gather_flags_bad_rows_and_blocks():
+    lens, table, k_log, v_log, kn, vn = _fused_case([20, 3], 2, 9)
+    kp, vp = _dev(k_log, v_log)
+    knd, vnd = to_llaisys(from_bits(kn)), to_llaisys(from_bits(vn))
+    ko = to_llaisys(torch.zeros((40, 2, 128), dtype=torch.bfloat16, device="cuda"))
+    vo = to_llaisys(torch.zeros((40, 2, 128), dtype=torch.bfloat16, device="cuda"))
+    # 5 rows for sequence 1, whose ctx + 1 is 4: flag 2, sequence skipped, sequence 0 done
+    cu = np.array([0, 21, 26], np.int32)
+    L.Ops.paged_kv_append_gather(ko, vo, kp, vp, knd, vnd, _i32(table), _i32(lens), _i32(cu))
+    assert L.device_error_flags() == 2
+    assert oracle.paged_append(k_log, v_log, kn[:1], vn[:1], table[:1], lens[:1]) == 0
+    gk, _ = oracle.paged_gather(k_log, v_log, table[:1], cu[:2])
+    np.testing.assert_array_equal(bits(to_torch(ko))[:21], gk)
+    # a block id outside the pool: flag 1
+    bad = table.copy()
+    bad[0, 1] = 1000
+    L.Ops.paged_kv_append_gather(ko, vo, kp, vp, knd, vnd, _i32(bad), _i32(lens), _i32(np.array([0, 21, 25], np.int32)))
+    assert L.device_error_flags() & 1
+    assert L.device_error_flags() == 0
