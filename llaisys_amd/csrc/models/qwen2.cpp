@@ -25,6 +25,9 @@ namespace llaisys::models {
 
 namespace K = llaisys::kernels;
 
+// Steps with at most this many token rows use the folded-norm projections.
+constexpr size_t kFoldMaxRows = 512;
+
 namespace {
 
 tensor_t dev(std::vector<size_t> shape, llaisysDataType_t dt, int id) {
@@ -427,19 +430,23 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     const tensor_t q3 = rows(q_, T), a3 = rows(attn_, T);
     for (size_t l = 0; l < cfg_.nlayer; ++l) {
         const auto &L = layers_[l];
-        // Folded norms: the projections read the residual x itself and the
-        // next kernel applies each row's 1/rms (see foldNormColumns).
-        const uint16_t *xr = fold_norm_ ? u16(x_) : nullptr;
-        if (!fold_norm_) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
-        gemm(qkv_, fold_norm_ ? x_ : h_, fold_norm_ ? L.qkv_wf : L.qkv_w, nullptr, M, q + 2 * kv, hs, false, s);
+        // Folded norms (decode-sized steps): the projections read the residual
+        // x itself and the next kernel applies each row's 1/rms (see
+        // foldNormColumns). Every wave of those kernels reduces its row again,
+        // which costs more than one rms_norm launch once a step holds
+        // thousands of rows, so long prefill steps keep the separate launch.
+        const bool fold = fold_norm_ && T <= kFoldMaxRows;
+        const uint16_t *xr = fold ? u16(x_) : nullptr;
+        if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
+        gemm(qkv_, fold ? x_ : h_, fold ? L.qkv_wf : L.qkv_w, nullptr, M, q + 2 * kv, hs, false, s);
         K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
                          i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh), int(cfg_.nkvh),
                          int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), xr, hs,
                          cfg_.epsilon, s);
         ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_, scale);
         gemm(x_, attn_, L.o_w, nullptr, M, hs, q, true, s);
-        if (!fold_norm_) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
-        gemm(gu_, fold_norm_ ? x_ : h_, fold_norm_ ? L.gate_up_wf : L.gate_up_w, nullptr, M, 2 * di, hs, false, s);
+        if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
+        gemm(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, nullptr, M, 2 * di, hs, false, s);
         K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s);
         gemm(x_, act_, L.down_w, nullptr, M, hs, di, true, s);
     }
