@@ -17,7 +17,7 @@ uint64_t mix(uint64_t z) {
 }
 } // namespace
 
-BlockManager::BlockManager(int num_blocks) {
+BlockManager::BlockManager(int num_blocks, bool scatter) {
     LLAISYS_CHECK(num_blocks > 0, "kv block manager: num_blocks must be positive, got " << num_blocks);
     ref_.assign(num_blocks, 0);
     lru_pos_.resize(num_blocks);
@@ -26,7 +26,23 @@ BlockManager::BlockManager(int num_blocks) {
     cached_.assign(num_blocks, false);
     cached_data_.resize(num_blocks);
     free_.reserve(num_blocks);
-    for (int b = num_blocks - 1; b >= 0; --b) free_.push_back(b); // hand out 0, 1, 2, ...
+    // The stack hands out free_.back() first: block order[0], order[1], ...
+    // Scattered order: i * stride mod n, stride ~ 0.618 n and coprime to n (a
+    // permutation that puts consecutive allocations far apart).
+    int64_t stride = 1;
+    if (scatter && num_blocks > 2) {
+        stride = int64_t(double(num_blocks) * 0.6180339887) | 1;
+        auto gcd = [](int64_t a, int64_t b) {
+            while (b) {
+                const int64_t t = a % b;
+                a = b;
+                b = t;
+            }
+            return a;
+        };
+        while (gcd(stride, num_blocks) != 1) stride += 2;
+    }
+    for (int64_t i = num_blocks - 1; i >= 0; --i) free_.push_back(int((i * stride) % num_blocks));
 }
 
 uint64_t BlockManager::chainHash(uint64_t parent, const int64_t *tokens) {

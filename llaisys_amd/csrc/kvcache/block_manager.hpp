@@ -18,7 +18,12 @@ constexpr int kBlockTokens = 16;
 
 class BlockManager {
 public:
-    explicit BlockManager(int num_blocks);
+    // scatter: hand out fresh blocks in a fixed scattered order instead of
+    // 0, 1, 2, ...; consecutive pages of a sequence then land far apart in the
+    // pool, which streams faster (the attention kernels' waves start at the
+    // same offsets of their sequences, so pools laid out in order concentrate
+    // each moment's reads at one stride).
+    explicit BlockManager(int num_blocks, bool scatter = false);
 
     int numBlocks() const { return int(ref_.size()); }
     int numFree() const { return int(free_.size() + lru_.size()); }

@@ -25,6 +25,13 @@ namespace llaisys::models {
 
 namespace K = llaisys::kernels;
 
+// KV pages handed out in the block manager's scattered order unless
+// LLAISYS_KV_SCATTER=0.
+bool scatterBlocks() {
+    const char *e = std::getenv("LLAISYS_KV_SCATTER");
+    return !(e && e[0] == '0');
+}
+
 // Steps with at most this many token rows use the folded-norm projections.
 constexpr size_t kFoldMaxRows = 512;
 
@@ -48,7 +55,7 @@ void gemm(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_
 } // namespace
 
 Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
-    : cfg_(cfg), dev_(device_id), num_blocks_(num_blocks), blocks_(int(num_blocks)) {
+    : cfg_(cfg), dev_(device_id), num_blocks_(num_blocks), blocks_(int(num_blocks), scatterBlocks()) {
     LLAISYS_CHECK(cfg.dtype == LLAISYS_DTYPE_BF16, "qwen2: the paged KV path runs bf16 models (meta.dtype)");
     LLAISYS_CHECK(cfg.dh == size_t(K::kHeadDim), "qwen2: head dim must be " << K::kHeadDim << ", got " << cfg.dh);
     LLAISYS_CHECK(cfg.nlayer > 0 && cfg.hs > 0 && cfg.nh > 0 && cfg.nkvh > 0 && cfg.di > 0 && cfg.voc > 0,
