@@ -25,6 +25,8 @@ namespace llaisys::models {
 
 namespace K = llaisys::kernels;
 
+namespace {
+
 // KV pages handed out in the block manager's scattered order unless
 // LLAISYS_KV_SCATTER=0.
 bool scatterBlocks() {
@@ -34,8 +36,6 @@ bool scatterBlocks() {
 
 // Steps with at most this many token rows use the folded-norm projections.
 constexpr size_t kFoldMaxRows = 512;
-
-namespace {
 
 tensor_t dev(std::vector<size_t> shape, llaisysDataType_t dt, int id) {
     return Tensor::create(shape, dt, LLAISYS_DEVICE_AMD, id);
