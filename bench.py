@@ -288,7 +288,7 @@ def run_decode(args):
             "q_heads": 12, "kv_heads": 2, "head_dim": 128, "accumulate": "fp32",
             "split": "stream-K over page pairs, log-sum-exp combine kernel",
             "waves": int(os.environ.get("LLAISYS_DECODE_WAVES",
-                                        torch.cuda.get_device_properties(0).multi_processor_count * 3 // 2)),
+                                        torch.cuda.get_device_properties(0).multi_processor_count * 7 // 4)),
         },
         "roofline": {
             "bound": "hbm",

@@ -487,9 +487,11 @@ int computeUnits() {
 DecodePlan planDecode(int B, int nkvh, int group, int max_pages) {
     DecodePlan p{};
     const long long max_pairs = (long long)B * nkvh * ((max_pages + 1) / 2);
-    // 1.5 waves per CU: measured best for 128 x ~2100-token batches (3.96 vs
-    // 4.09 ms per model step at 1 wave per CU) and neutral for config 3.
-    const int fill = std::max(1, envInt("LLAISYS_DECODE_WAVES", computeUnits() * 3 / 2));
+    // 1.75 waves per CU: measured best for the model's 128 x ~2100-token
+    // batches (3.54 ms per step against 3.56-3.60 at 1.5 and 3.56 at 2 waves
+    // per CU; 1 wave per CU was 3 % slower than 1.5), slightly ahead for the
+    // mixed batch and neutral for the config-3 batch (53.15 us at 1.5 or 1.75).
+    const int fill = std::max(1, envInt("LLAISYS_DECODE_WAVES", computeUnits() * 7 / 4));
     p.waves = int(std::max<long long>(fill, (max_pairs + kPairsPerWave - 1) / kPairsPerWave));
     p.record_bytes = size_t(2) * p.waves * group * (kHeadDim + 2) * sizeof(float);
     p.lds_bytes = size_t(3 * B + 1) * sizeof(int);
