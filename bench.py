@@ -315,6 +315,21 @@ def run_decode(args):
                          "single_step_call_ms": m["config"]["single_step_call_ms"],
                          "batch": m["config"]["batch"], "context_at_start": m["config"]["context_at_start"],
                          "prefill_tokens_per_s": m["config"]["prefill_tokens_per_s"], "roofline": m["roofline"]}
+        # The other measured rows of the path, for the record (their own
+        # --workload runs give the full lines).
+        torch.cuda.empty_cache()
+        oargs = argparse.Namespace(**vars(args))
+        oargs.steps, oargs.warmup = 100, 10
+        ag = run_append_gather(oargs)
+        torch.cuda.empty_cache()
+        mx = run_mixed(oargs)
+        torch.cuda.empty_cache()
+        line["other_configs"] = {
+            "config2_append_gather": {"GB/s": ag["value"], "frac_of_hbm_peak": ag["roofline"]["frac"],
+                                      "kernel_ms": ag["kernel_ms"], "entry_point": ag["config"]["entry_point"],
+                                      "two_calls_kernel_ms": (ag["two_calls"] or {}).get("kernel_ms")},
+            "config4_mixed_prefill_decode": {"TFLOP/s": mx["value"], "kernel_ms": mx["kernel_ms"]},
+        }
     return line
 
 
