@@ -3,10 +3,12 @@
  *
  * llaisysSelfAttention and the eight other reference ops keep the reference's
  * declarations (include/llaisys/ops.h:7-15) so python/llaisys/libllaisys/ops.py
- * binds unchanged. All run on LLAISYS_DEVICE_AMD tensors (F32, F16, BF16;
- * indices I64), contiguous unless stated; CPU tensors are rejected (the
- * reference's CPU ops are TO_BE_IMPLEMENTED stubs, src/ops/<op>/op.cpp:4-6,
- * except add). Contracts are the reference README's (README.md:157-292):
+ * binds unchanged. Every op dispatches on its tensors' device, as the
+ * reference's src/ops/add/op.cpp:16-33 does: LLAISYS_DEVICE_AMD tensors run the
+ * HIP kernels, LLAISYS_DEVICE_CPU tensors the host implementations (fp32 math,
+ * host threads); one call may not mix devices. F32, F16, BF16; indices I64;
+ * contiguous unless stated. Contracts are the reference README's
+ * (README.md:157-292).
  *
  * The llaisysPagedKV* / llaisysPagedAttention* entry points are new. The
  * reference has no paged KV code; they follow its op conventions
@@ -14,7 +16,8 @@
  * written in place, errors reported as the reference reports them).
  *
  * Paged KV pool (one per layer, one for K and one for V):
- *   shape [num_blocks, nkvh, 16, 128], dtype BF16, device AMD, contiguous.
+ *   shape [num_blocks, nkvh, 16, 128], dtype BF16, contiguous, on the AMD
+ *   device or the host (the same page format on both).
  *   A (block, kv-head) page holds 16 tokens x 128 dims = 4 KiB. Inside a page
  *   the bytes are in the MI355X page format, not row-major [16][128]:
  *     K page: element (token t, dim d) at bf16 index

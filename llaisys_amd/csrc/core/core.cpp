@@ -96,6 +96,7 @@ void *Runtime::decodeSlotRecords(size_t record_bytes) {
 }
 
 int *Runtime::errorWord() {
+    if (type_ == LLAISYS_DEVICE_CPU) return &host_error_word_;
     LLAISYS_CHECK(type_ == LLAISYS_DEVICE_AMD, "device workspace exists on AMD runtimes only");
     if (!error_word_) {
         error_word_ = static_cast<int *>(api_->malloc_device(sizeof(int)));
@@ -106,6 +107,7 @@ int *Runtime::errorWord() {
 }
 
 int Runtime::takeErrorFlags() {
+    if (type_ == LLAISYS_DEVICE_CPU) return __atomic_exchange_n(&host_error_word_, 0, __ATOMIC_RELAXED);
     if (type_ != LLAISYS_DEVICE_AMD || !error_word_) return 0;
     int flags = 0;
     api_->stream_synchronize(stream());
@@ -115,6 +117,16 @@ int Runtime::takeErrorFlags() {
         api_->memcpy_sync(error_word_, &zero, sizeof(int), LLAISYS_MEMCPY_H2D);
     }
     return flags;
+}
+
+void Runtime::clearErrorFlagsAsync() {
+    if (type_ == LLAISYS_DEVICE_CPU) {
+        __atomic_store_n(&host_error_word_, 0, __ATOMIC_RELAXED);
+        return;
+    }
+    if (type_ != LLAISYS_DEVICE_AMD || !error_word_) return;
+    if (hipMemsetAsync(error_word_, 0, sizeof(int), static_cast<hipStream_t>(stream())) != hipSuccess)
+        LLAISYS_RAISE("hipMemsetAsync failed");
 }
 
 Context::Context() {

@@ -88,9 +88,14 @@ public:
     // Bumped whenever scratch() or the slot buffers move: captured graphs that
     // baked the old addresses in must be re-captured.
     uint64_t workspaceGeneration() const { return ws_gen_; }
-    // One int32 of kernel-side error bits.
+    // One int32 of kernel-side error bits (device memory on AMD; on CPU a host
+    // word the host ops raise bits in, read and cleared the same way).
     int *errorWord();
     int takeErrorFlags();
+    // Zero the error word in stream order, without waiting: a caller that
+    // checks its own launches' flags afterwards is not failed by bits an
+    // earlier, unrelated call left unread.
+    void clearErrorFlagsAsync();
 
     void activate();
 
@@ -103,6 +108,7 @@ private:
     void *scratch_ = nullptr;
     size_t scratch_bytes_ = 0;
     int *error_word_ = nullptr;
+    int host_error_word_ = 0;
     int *slot_hdr_ = nullptr;
     size_t slot_hdr_ints_ = 0;
     void *slot_rec_ = nullptr;

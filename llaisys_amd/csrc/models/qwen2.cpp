@@ -228,6 +228,7 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     ensureFolded();
     auto &rt = core::context().runtime();
+    rt.clearErrorFlagsAsync(); // this call's kernels alone decide its error check
     const size_t B = nseq;
     size_t T = 0;
     for (size_t i = 0; i < B; ++i) {
@@ -311,6 +312,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     ensureFolded();
     auto &rt = core::context().runtime();
+    rt.clearErrorFlagsAsync(); // this call's kernels alone decide its error check
     const size_t B = nseq;
     for (size_t i = 0; i < B; ++i) {
         LLAISYS_CHECK(size_t(blocks_.length(ids[i])) + nsteps <= cfg_.maxseq,

@@ -2,6 +2,7 @@
 
 #include "../common.hpp"
 #include "../kernels/launch.hpp"
+#include "cpu/cpu_kernels.hpp"
 
 #include <algorithm>
 
@@ -33,20 +34,22 @@ void requireShape(const tensor_t &t, std::initializer_list<size_t> shape, const 
     LLAISYS_CHECK(t->shape() == want, op << ": " << name << " has shape " << shapeStr(t) << ", expected a different shape");
 }
 
-// Every tensor of an op must live on the same AMD device; the CPU path of
-// these ops is not part of this library (the reference's own CPU op is a
-// TO_BE_IMPLEMENTED stub, src/ops/self_attention/op.cpp:4-6), so CPU tensors
-// are rejected rather than silently computed somewhere else.
-void requireAmd(const char *op, std::initializer_list<const tensor_t *> ts) {
+// Every tensor of an op must live on one device: the AMD GPU (HIP kernels) or
+// the host (the CPU implementations), as the reference dispatches on the
+// tensor's device (src/ops/add/op.cpp:16-33). Returns true for the host.
+bool onHost(const char *op, std::initializer_list<const tensor_t *> ts) {
     const tensor_t &first = **ts.begin();
+    const auto dev = first->deviceType();
+    LLAISYS_CHECK(dev == LLAISYS_DEVICE_AMD || dev == LLAISYS_DEVICE_CPU,
+                  op << ": no implementation for device " << deviceName(dev));
     for (auto *t : ts) {
         if (!*t) continue;
-        LLAISYS_CHECK((*t)->deviceType() == LLAISYS_DEVICE_AMD,
-                      op << ": tensors must be on the AMD device (got " << deviceName((*t)->deviceType())
-                         << "); llaisys_amd implements this op for MI355X only");
-        LLAISYS_CHECK((*t)->deviceId() == first->deviceId(), op << ": tensors are on different devices");
+        LLAISYS_CHECK((*t)->deviceType() == dev && (*t)->deviceId() == first->deviceId(),
+                      op << ": tensors are on different devices (" << deviceName(dev) << " and "
+                         << deviceName((*t)->deviceType()) << ")");
     }
-    core::context().setDevice(LLAISYS_DEVICE_AMD, first->deviceId());
+    core::context().setDevice(dev, first->deviceId());
+    return dev == LLAISYS_DEVICE_CPU;
 }
 
 K::ElemType elemType(llaisysDataType_t dt, const char *op) {
@@ -86,6 +89,7 @@ void checkI32Vec(const tensor_t &t, size_t n, const char *op, const char *name) 
 }
 
 void *streamOf() { return core::context().runtime().stream(); }
+namespace C = llaisys::cpu;
 int *errWord() { return core::context().runtime().errorWord(); }
 
 } // namespace
@@ -106,9 +110,12 @@ void selfAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k, co
     LLAISYS_CHECK(q->dtype() == k->dtype() && q->dtype() == v->dtype() && q->dtype() == out->dtype(),
                   op << ": q, k, v, attn_val must share one dtype");
     for (auto *t : {&out, &q, &k, &v}) requireContiguous(*t, op, "every tensor");
-    requireAmd(op, {&out, &q, &k, &v});
+    const bool host = onHost(op, {&out, &q, &k, &v});
     if (L == 0) return;
     LLAISYS_CHECK(S > 0, op << ": empty key set");
+    if (host)
+        return C::selfAttention(out->data(), q->data(), k->data(), v->data(), elemType(q->dtype(), op), int(L),
+                                int(S), int(nh), int(nkvh), int(d), int(dv), scale);
     K::selfAttention(out->data(), q->data(), k->data(), v->data(), elemType(q->dtype(), op), int(L), int(S),
                      int(nh), int(nkvh), int(d), int(dv), scale, streamOf());
 }
@@ -135,15 +142,21 @@ void pagedKVAppend(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_
     } else {
         LLAISYS_CHECK(T == B, op << ": without cu_new, k_new must hold one token per sequence (T=" << T << ", B=" << B << ")");
     }
-    requireAmd(op, {&k_pool, &v_pool, &k_new, &v_new, &block_table, &ctx_len, &cu_new});
+    const bool host = onHost(op, {&k_pool, &v_pool, &k_new, &v_new, &block_table, &ctx_len, &cu_new});
     if (T == 0) return;
     LLAISYS_CHECK(B > 0, op << ": tokens given for zero sequences");
-    K::pagedAppend(reinterpret_cast<uint16_t *>(k_pool->data()), reinterpret_cast<uint16_t *>(v_pool->data()),
-                   reinterpret_cast<const uint16_t *>(k_new->data()), reinterpret_cast<const uint16_t *>(v_new->data()),
-                   reinterpret_cast<const int32_t *>(block_table->data()),
-                   reinterpret_cast<const int32_t *>(ctx_len->data()),
-                   cu_new ? reinterpret_cast<const int32_t *>(cu_new->data()) : nullptr, int(T), int(B), int(nkvh),
-                   int(block_table->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
+    auto *kp = reinterpret_cast<uint16_t *>(k_pool->data());
+    auto *vp = reinterpret_cast<uint16_t *>(v_pool->data());
+    const auto *kn = reinterpret_cast<const uint16_t *>(k_new->data());
+    const auto *vn = reinterpret_cast<const uint16_t *>(v_new->data());
+    const auto *tab = reinterpret_cast<const int32_t *>(block_table->data());
+    const auto *ctx = reinterpret_cast<const int32_t *>(ctx_len->data());
+    const auto *cu = cu_new ? reinterpret_cast<const int32_t *>(cu_new->data()) : nullptr;
+    const int maxp = int(block_table->shape()[1]), nb = int(k_pool->shape()[0]);
+    if (host)
+        C::pagedAppend(kp, vp, kn, vn, tab, ctx, cu, int(T), int(B), int(nkvh), maxp, nb, errWord());
+    else
+        K::pagedAppend(kp, vp, kn, vn, tab, ctx, cu, int(T), int(B), int(nkvh), maxp, nb, errWord(), streamOf());
 }
 
 void pagedKVGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t &k_pool, const tensor_t &v_pool,
@@ -163,13 +176,18 @@ void pagedKVGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t 
     const size_t B = cu_seqlens->shape()[0] - 1;
     checkI32Vec(cu_seqlens, B + 1, op, "cu_seqlens");
     checkTable(block_table, B, op);
-    requireAmd(op, {&k_out, &v_out, &k_pool, &v_pool, &block_table, &cu_seqlens});
-    K::pagedGather(reinterpret_cast<uint16_t *>(k_out->data()), reinterpret_cast<uint16_t *>(v_out->data()),
-                   reinterpret_cast<const uint16_t *>(k_pool->data()),
-                   reinterpret_cast<const uint16_t *>(v_pool->data()),
-                   reinterpret_cast<const int32_t *>(block_table->data()),
-                   reinterpret_cast<const int32_t *>(cu_seqlens->data()), int(k_out->shape()[0]), int(B), int(nkvh),
-                   int(block_table->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
+    const bool host = onHost(op, {&k_out, &v_out, &k_pool, &v_pool, &block_table, &cu_seqlens});
+    auto *ko = reinterpret_cast<uint16_t *>(k_out->data());
+    auto *vo = reinterpret_cast<uint16_t *>(v_out->data());
+    const auto *kp = reinterpret_cast<const uint16_t *>(k_pool->data());
+    const auto *vp = reinterpret_cast<const uint16_t *>(v_pool->data());
+    const auto *tab = reinterpret_cast<const int32_t *>(block_table->data());
+    const auto *cu = reinterpret_cast<const int32_t *>(cu_seqlens->data());
+    const int T = int(k_out->shape()[0]), maxp = int(block_table->shape()[1]), nb = int(k_pool->shape()[0]);
+    if (host)
+        C::pagedGather(ko, vo, kp, vp, tab, cu, T, int(B), int(nkvh), maxp, nb, errWord());
+    else
+        K::pagedGather(ko, vo, kp, vp, tab, cu, T, int(B), int(nkvh), maxp, nb, errWord(), streamOf());
 }
 
 void pagedKVAppendGather(const tensor_t &k_out, const tensor_t &v_out, const tensor_t &k_pool, const tensor_t &v_pool,
@@ -198,15 +216,22 @@ void pagedKVAppendGather(const tensor_t &k_out, const tensor_t &v_out, const ten
     checkTable(block_table, B, op);
     LLAISYS_CHECK(k_new->shape()[0] == B, op << ": k_new must hold one token per sequence (rows=" << k_new->shape()[0]
                                              << ", B=" << B << ")");
-    requireAmd(op, {&k_out, &v_out, &k_pool, &v_pool, &k_new, &v_new, &block_table, &ctx_len, &cu_seqlens});
-    K::pagedAppendGather(reinterpret_cast<uint16_t *>(k_out->data()), reinterpret_cast<uint16_t *>(v_out->data()),
-                         reinterpret_cast<uint16_t *>(k_pool->data()), reinterpret_cast<uint16_t *>(v_pool->data()),
-                         reinterpret_cast<const uint16_t *>(k_new->data()),
-                         reinterpret_cast<const uint16_t *>(v_new->data()),
-                         reinterpret_cast<const int32_t *>(block_table->data()),
-                         reinterpret_cast<const int32_t *>(ctx_len->data()),
-                         reinterpret_cast<const int32_t *>(cu_seqlens->data()), int(k_out->shape()[0]), int(B),
-                         int(nkvh), int(block_table->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
+    const bool host = onHost(op, {&k_out, &v_out, &k_pool, &v_pool, &k_new, &v_new, &block_table, &ctx_len, &cu_seqlens});
+    auto *ko = reinterpret_cast<uint16_t *>(k_out->data());
+    auto *vo = reinterpret_cast<uint16_t *>(v_out->data());
+    auto *kp = reinterpret_cast<uint16_t *>(k_pool->data());
+    auto *vp = reinterpret_cast<uint16_t *>(v_pool->data());
+    const auto *kn = reinterpret_cast<const uint16_t *>(k_new->data());
+    const auto *vn = reinterpret_cast<const uint16_t *>(v_new->data());
+    const auto *tab = reinterpret_cast<const int32_t *>(block_table->data());
+    const auto *ctx = reinterpret_cast<const int32_t *>(ctx_len->data());
+    const auto *cu = reinterpret_cast<const int32_t *>(cu_seqlens->data());
+    const int T = int(k_out->shape()[0]), maxp = int(block_table->shape()[1]), nb = int(k_pool->shape()[0]);
+    if (host)
+        C::pagedAppendGather(ko, vo, kp, vp, kn, vn, tab, ctx, cu, T, int(B), int(nkvh), maxp, nb, errWord());
+    else
+        K::pagedAppendGather(ko, vo, kp, vp, kn, vn, tab, ctx, cu, T, int(B), int(nkvh), maxp, nb, errWord(),
+                             streamOf());
 }
 
 void pagedKVCopyBlocks(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_t &pairs) {
@@ -216,10 +241,15 @@ void pagedKVCopyBlocks(const tensor_t &k_pool, const tensor_t &v_pool, const ten
     LLAISYS_CHECK(pairs->ndim() == 2 && pairs->shape()[1] == 2, op << ": pairs must be [P, 2], got " << shapeStr(pairs));
     requireDtype(pairs, LLAISYS_DTYPE_I32, op, "pairs");
     requireContiguous(pairs, op, "pairs");
-    requireAmd(op, {&k_pool, &v_pool, &pairs});
-    K::pagedCopyBlocks(reinterpret_cast<uint16_t *>(k_pool->data()), reinterpret_cast<uint16_t *>(v_pool->data()),
-                       reinterpret_cast<const int32_t *>(pairs->data()), int(pairs->shape()[0]),
-                       int(k_pool->shape()[1]), int(k_pool->shape()[0]), errWord(), streamOf());
+    const bool host = onHost(op, {&k_pool, &v_pool, &pairs});
+    auto *kp = reinterpret_cast<uint16_t *>(k_pool->data());
+    auto *vp = reinterpret_cast<uint16_t *>(v_pool->data());
+    const auto *pr = reinterpret_cast<const int32_t *>(pairs->data());
+    const int P = int(pairs->shape()[0]), nkvh = int(k_pool->shape()[1]), nb = int(k_pool->shape()[0]);
+    if (host)
+        C::pagedCopyBlocks(kp, vp, pr, P, nkvh, nb, errWord());
+    else
+        K::pagedCopyBlocks(kp, vp, pr, P, nkvh, nb, errWord(), streamOf());
 }
 
 void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_pool, const tensor_t &v_pool,
@@ -248,10 +278,19 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
     } else {
         LLAISYS_CHECK(T == B, op << ": q must hold one query per sequence (T=" << T << ", B=" << B << ")");
     }
-    requireAmd(op, {&out, &q, &k_pool, &v_pool, &block_table, &ctx_len, &cu_q});
+    const bool host = onHost(op, {&out, &q, &k_pool, &v_pool, &block_table, &ctx_len, &cu_q});
     if (T == 0 || B == 0) return;
     const int max_pages = int(block_table->shape()[1]);
     LLAISYS_CHECK(max_pages > 0, op << ": block_table has no pages");
+    if (host)
+        return C::pagedAttention(out->data(), out->dtype() == LLAISYS_DTYPE_F32,
+                                 reinterpret_cast<const uint16_t *>(q->data()),
+                                 reinterpret_cast<const uint16_t *>(k_pool->data()),
+                                 reinterpret_cast<const uint16_t *>(v_pool->data()),
+                                 reinterpret_cast<const int32_t *>(block_table->data()),
+                                 reinterpret_cast<const int32_t *>(ctx_len->data()),
+                                 cu_q ? reinterpret_cast<const int32_t *>(cu_q->data()) : nullptr, int(B), int(T),
+                                 int(nh), int(nkvh), max_pages, int(k_pool->shape()[0]), scale, errWord());
     auto &rt = core::context().runtime();
     const int G = int(nh / nkvh);
     const bool f32 = out->dtype() == LLAISYS_DTYPE_F32;

@@ -1,16 +1,18 @@
-// The reference's model ops on the AMD device (README.md:145-292), as used
+// The reference's model ops on the AMD device and the host (README.md:145-292), as used
 // by the Qwen2 decode step. Shape/dtype contracts follow the reference
 // README and test/ops/*.py; all tensors contiguous unless stated.
 #include "ops.hpp"
 
 #include "../common.hpp"
 #include "../kernels/launch.hpp"
+#include "cpu/cpu_kernels.hpp"
 
 namespace llaisys::ops {
 
 namespace {
 
 namespace K = llaisys::kernels;
+namespace C = llaisys::cpu;
 
 std::string shapeOf(const tensor_t &t) {
     std::ostringstream os;
@@ -29,17 +31,25 @@ K::ElemType floatType(const tensor_t &t, const char *op) {
     }
 }
 
-void onAmd(const char *op, std::initializer_list<const tensor_t *> ts, bool contiguous = true) {
-    int id = -1;
+// All tensors on one device, AMD (HIP kernels) or the host (CPU
+// implementations), dispatched as src/ops/add/op.cpp:16-33 does. Returns true
+// for the host.
+bool onHost(const char *op, std::initializer_list<const tensor_t *> ts, bool contiguous = true) {
+    const tensor_t *first = nullptr;
     for (auto *t : ts) {
         if (!*t) continue;
-        LLAISYS_CHECK((*t)->deviceType() == LLAISYS_DEVICE_AMD,
-                      op << ": tensors must be on the AMD device; llaisys_amd implements this op for MI355X only");
-        LLAISYS_CHECK(id < 0 || (*t)->deviceId() == id, op << ": tensors are on different devices");
-        id = (*t)->deviceId();
+        if (!first) {
+            first = t;
+            const auto dev = (*t)->deviceType();
+            LLAISYS_CHECK(dev == LLAISYS_DEVICE_AMD || dev == LLAISYS_DEVICE_CPU,
+                          op << ": no implementation for device " << deviceName(dev));
+        }
+        LLAISYS_CHECK((*t)->deviceType() == (*first)->deviceType() && (*t)->deviceId() == (*first)->deviceId(),
+                      op << ": tensors are on different devices");
         if (contiguous) LLAISYS_CHECK((*t)->isContiguous(), op << ": tensors must be contiguous");
     }
-    core::context().setDevice(LLAISYS_DEVICE_AMD, id);
+    core::context().setDevice((*first)->deviceType(), (*first)->deviceId());
+    return (*first)->deviceType() == LLAISYS_DEVICE_CPU;
 }
 
 void sameDtype(const char *op, std::initializer_list<const tensor_t *> ts) {
@@ -57,7 +67,7 @@ void add(const tensor_t &c, const tensor_t &a, const tensor_t &b) {
     LLAISYS_CHECK(c && a && b, op << ": null tensor");
     LLAISYS_CHECK(c->shape() == a->shape() && c->shape() == b->shape(), op << ": shapes differ");
     sameDtype(op, {&c, &a, &b});
-    onAmd(op, {&c, &a, &b});
+    if (onHost(op, {&c, &a, &b})) return C::add(c->data(), a->data(), b->data(), floatType(c, op), c->numel());
     K::add(c->data(), a->data(), b->data(), floatType(c, op), c->numel(), stream());
 }
 
@@ -73,7 +83,9 @@ void argmax(const tensor_t &max_idx, const tensor_t &max_val, const tensor_t &va
         LLAISYS_CHECK(max_val->numel() == rows && max_val->dtype() == vals->dtype(),
                       op << ": max_val must match vals' dtype with one element per row");
     }
-    onAmd(op, {&max_idx, &max_val, &vals});
+    if (onHost(op, {&max_idx, &max_val, &vals}))
+        return C::argmax(reinterpret_cast<int64_t *>(max_idx->data()), max_val ? max_val->data() : nullptr,
+                         vals->data(), floatType(vals, op), rows, int64_t(n));
     void *ws = core::context().runtime().scratch(K::argmaxWorkspaceBytes(rows, int64_t(n)));
     K::argmax(reinterpret_cast<int64_t *>(max_idx->data()), max_val ? max_val->data() : nullptr, vals->data(),
               floatType(vals, op), rows, int64_t(n), ws, stream());
@@ -87,7 +99,10 @@ void embedding(const tensor_t &out, const tensor_t &index, const tensor_t &weigh
     LLAISYS_CHECK(out->ndim() == 2 && out->shape()[0] == index->shape()[0] && out->shape()[1] == weight->shape()[1],
                   op << ": out must be [" << index->shape()[0] << ", " << weight->shape()[1] << "], got " << shapeOf(out));
     sameDtype(op, {&out, &weight});
-    onAmd(op, {&out, &index, &weight});
+    if (onHost(op, {&out, &index, &weight}))
+        return C::embedding(out->data(), reinterpret_cast<const int64_t *>(index->data()), weight->data(),
+                            floatType(out, op), index->shape()[0], int64_t(weight->shape()[0]),
+                            int(weight->shape()[1]), core::context().runtime().errorWord());
     K::embedding(out->data(), reinterpret_cast<const int64_t *>(index->data()), weight->data(), floatType(out, op),
                  index->shape()[0], int64_t(weight->shape()[0]), int(weight->shape()[1]),
                  core::context().runtime().errorWord(), stream());
@@ -102,7 +117,9 @@ void linear(const tensor_t &out, const tensor_t &in, const tensor_t &weight, con
     LLAISYS_CHECK(out->shape()[0] == M && out->shape()[1] == N, op << ": out must be [" << M << ", " << N << "]");
     if (bias) LLAISYS_CHECK(bias->ndim() == 1 && bias->shape()[0] == N, op << ": bias must be [" << N << "]");
     sameDtype(op, {&out, &in, &weight, &bias});
-    onAmd(op, {&out, &in, &weight, &bias});
+    if (onHost(op, {&out, &in, &weight, &bias}))
+        return C::linear(out->data(), in->data(), weight->data(), bias ? bias->data() : nullptr, floatType(out, op),
+                         int(M), int(N), int(Kd));
     K::linear(out->data(), in->data(), weight->data(), bias ? bias->data() : nullptr, floatType(out, op), int(M),
               int(N), int(Kd), stream());
 }
@@ -112,13 +129,16 @@ void rearrange(const tensor_t &out, const tensor_t &in) {
     LLAISYS_CHECK(out && in, op << ": null tensor");
     LLAISYS_CHECK(out->shape() == in->shape(), op << ": shapes differ");
     sameDtype(op, {&out, &in});
-    onAmd(op, {&out, &in}, false);
+    const bool host = onHost(op, {&out, &in}, false);
     std::vector<int64_t> shape(out->ndim()), os(out->ndim()), is(out->ndim());
     for (size_t k = 0; k < out->ndim(); ++k) {
         shape[k] = int64_t(out->shape()[k]);
         os[k] = out->strides()[k];
         is[k] = in->strides()[k];
     }
+    if (host)
+        return C::rearrange(out->data(), in->data(), out->elementSize(), int(out->ndim()), shape.data(), os.data(),
+                            is.data());
     K::rearrange(out->data(), in->data(), out->elementSize(), int(out->ndim()), shape.data(), os.data(), is.data(),
                  stream());
 }
@@ -130,7 +150,8 @@ void rmsNorm(const tensor_t &out, const tensor_t &in, const tensor_t &weight, fl
     const size_t d = in->shape().back();
     LLAISYS_CHECK(weight->ndim() == 1 && weight->shape()[0] == d, op << ": weight must be [" << d << "]");
     sameDtype(op, {&out, &in, &weight});
-    onAmd(op, {&out, &in, &weight});
+    if (onHost(op, {&out, &in, &weight}))
+        return C::rmsNorm(out->data(), in->data(), weight->data(), floatType(out, op), in->numel() / d, int(d), eps);
     K::rmsNorm(out->data(), in->data(), weight->data(), floatType(out, op), in->numel() / d, int(d), eps, stream());
 }
 
@@ -142,7 +163,9 @@ void rope(const tensor_t &out, const tensor_t &in, const tensor_t &pos_ids, floa
     LLAISYS_CHECK(pos_ids->ndim() == 1 && pos_ids->shape()[0] == in->shape()[0] && pos_ids->dtype() == LLAISYS_DTYPE_I64,
                   op << ": pos_ids must be I64 [" << in->shape()[0] << "]");
     sameDtype(op, {&out, &in});
-    onAmd(op, {&out, &in, &pos_ids});
+    if (onHost(op, {&out, &in, &pos_ids}))
+        return C::rope(out->data(), in->data(), reinterpret_cast<const int64_t *>(pos_ids->data()), floatType(out, op),
+                       in->shape()[0], int(in->shape()[1]), int(in->shape()[2]), theta);
     K::rope(out->data(), in->data(), reinterpret_cast<const int64_t *>(pos_ids->data()), floatType(out, op),
             in->shape()[0], int(in->shape()[1]), int(in->shape()[2]), theta, stream());
 }
@@ -152,7 +175,8 @@ void swiglu(const tensor_t &out, const tensor_t &gate, const tensor_t &up) {
     LLAISYS_CHECK(out && gate && up, op << ": null tensor");
     LLAISYS_CHECK(out->shape() == gate->shape() && out->shape() == up->shape(), op << ": shapes differ");
     sameDtype(op, {&out, &gate, &up});
-    onAmd(op, {&out, &gate, &up});
+    if (onHost(op, {&out, &gate, &up}))
+        return C::swiglu(out->data(), gate->data(), up->data(), floatType(out, op), out->numel());
     K::swiglu(out->data(), gate->data(), up->data(), floatType(out, op), out->numel(), stream());
 }
 

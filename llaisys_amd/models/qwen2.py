@@ -130,8 +130,21 @@ class Qwen2:
             names += [f"model.layers.{i}.{s}" for s in _LAYER_SLOTS]
         return names
 
-    def load_weight(self, name: str, host_ptr: int):
-        """tensorLoad of contiguous host data (the weight's own dtype and shape)."""
+    def weight_shape(self, name: str) -> tuple:
+        """Shape of an HF-named weight as the model holds it."""
+        h = self.weight_handle(name)
+        n = int(LIB_LLAISYS.tensorGetNdim(h))
+        buf = (c_size_t * max(n, 1))()
+        LIB_LLAISYS.tensorGetShape(h, buf)
+        return tuple(int(buf[i]) for i in range(n))
+
+    def load_weight(self, name: str, host_ptr: int, shape=None):
+        """tensorLoad of contiguous host data (the weight's own dtype and shape).
+        tensorLoad copies as many bytes as the weight holds; pass the source's
+        `shape` to have a mismatch refused before anything is read."""
+        if shape is not None and tuple(shape) != self.weight_shape(name):
+            raise ValueError(f"{name}: source shape {tuple(shape)} does not match the model's "
+                             f"{self.weight_shape(name)}")
         LIB_LLAISYS.tensorLoad(self.weight_handle(name), host_ptr)
         check_last_error()
 
@@ -146,10 +159,10 @@ class Qwen2:
                     if name not in _GLOBAL_SLOTS and ".".join(name.split(".")[3:]) not in _LAYER_SLOTS:
                         continue
                     t = f.get_tensor(name).to(torch.bfloat16).contiguous()
-                    self.load_weight(name, t.data_ptr())
+                    self.load_weight(name, t.data_ptr(), t.shape)
                     seen.add(name)
                     if tied and name == "model.embed_tokens.weight":
-                        self.load_weight("lm_head.weight", t.data_ptr())
+                        self.load_weight("lm_head.weight", t.data_ptr(), t.shape)
                         seen.add("lm_head.weight")
         missing = [n for n in self.weight_names() if n not in seen]
         if missing:

@@ -43,22 +43,26 @@ def test_library_exports_declared_symbol(name):
 
 
 @pytest.mark.parametrize("op", ["add", "argmax", "embedding", "rearrange", "swiglu"])
-def test_model_ops_reject_cpu_tensors(op):
-    # The model ops run on the AMD device only; CPU tensors fail loudly.
+def test_model_ops_on_cpu_tensors_validate_arguments(op):
+    # Host tensors run the CPU implementations; argument errors still fail
+    # loudly (argmax needs an I64 index output, embedding an I64 index).
     t = L.Tensor((2,), dtype=L.DataType.F32)
     args = {"add": 3, "argmax": 3, "embedding": 3, "rearrange": 2, "swiglu": 3}[op]
-    with pytest.raises(L.LlaisysError):
+    if op in ("argmax", "embedding"):
+        with pytest.raises(L.LlaisysError):
+            getattr(L.Ops, op)(*([t] * args))
+    else:
         getattr(L.Ops, op)(*([t] * args))
 
 
-def test_paged_ops_reject_cpu_tensors_and_bad_shapes():
+def test_paged_ops_reject_bad_dtypes_and_shapes():
     pool = L.Tensor((4, 2, 16, 128), dtype=L.DataType.BF16)
     q = L.Tensor((2, 12, 128), dtype=L.DataType.BF16)
     out = L.Tensor((2, 12, 128), dtype=L.DataType.BF16)
     table = L.Tensor((2, 2), dtype=L.DataType.I32)
     ctx = L.Tensor((2,), dtype=L.DataType.I32)
-    with pytest.raises(L.LlaisysError, match="AMD device"):
-        L.Ops.paged_attention(out, q, pool, pool, table, ctx, 0.1)
+    with pytest.raises(L.LlaisysError, match="q must be bf16"):
+        L.Ops.paged_attention(out, L.Tensor((2, 12, 128), dtype=L.DataType.F32), pool, pool, table, ctx, 0.1)
     bad_pool = L.Tensor((4, 2, 8, 128), dtype=L.DataType.BF16)
     with pytest.raises(L.LlaisysError, match="pool must be"):
         L.Ops.paged_attention(out, q, bad_pool, bad_pool, table, ctx, 0.1)

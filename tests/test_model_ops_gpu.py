@@ -162,10 +162,12 @@ def test_rearrange(dtype):
     assert torch.equal(to_torch(dst), src.permute(1, 0, 3, 2))
 
 
-def test_model_ops_reject_cpu_tensors():
+def test_model_ops_refuse_mixed_devices():
+    # Host tensors run the CPU implementations; one op may not mix devices.
     a = L.Tensor((4,), dtype=DataType.F32, device=DeviceType.CPU)
-    with pytest.raises(L.LlaisysError, match="AMD device"):
-        L.Ops.add(a, a, a)
+    g = to_llaisys(torch.zeros(4, device=DEV))
+    with pytest.raises(L.LlaisysError, match="different devices"):
+        L.Ops.add(g, a, g)
 
 
 SKINNY = [(1, 1, 64), (3, 7, 64), (5, 15, 128), (16, 16, 192), (17, 33, 1536), (64, 2048, 1536), (100, 1536, 8960),
