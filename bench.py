@@ -183,68 +183,154 @@ def time_steps_flushed(step, stream, steps, warmup, flush_mib=512):
     return sum(s.elapsed_time(e) for s, e in ev) / steps, wall
 
 
+def host_cpus():
+    """(threads the CPU legs use, CPUs this process may run on, os.cpu_count()).
+    The legs use every CPU of the process's affinity set up to 16, the CPU
+    share of a one-GPU box here (the machine's other cores serve other GPUs)."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    return max(1, min(allowed, 16)), allowed, os.cpu_count()
+
+
+def _timed(fn, budget_s, min_reps=1):
+    """Repeat fn until budget_s has passed (at least min_reps times); seconds per call."""
+    reps, total = 0, 0.0
+    while total < budget_s or reps < min_reps:
+        t0 = time.perf_counter()
+        fn()
+        total += time.perf_counter() - t0
+        reps += 1
+    return total / reps, reps, total
+
+
 def cpu_baseline_decode(inst, budget_s):
-    """The C oracle (OpenMP over sequences) on the first sequences of the batch,
-    as many as fit ~budget_s; GB/s over the same per-token byte count."""
+    """CPU legs of the config-3 workload, on a prefix of its batch sized so one
+    pass takes >= 1 s: the C oracle (oracle/oracle.c, the restatement of the
+    reference's fp32 algorithm; kind "port") on all the legs' threads, and on
+    one thread; the library's own host path (llaisysPagedAttention on CPU
+    tensors, the same page-format pools) beside it. GB/s over the same
+    per-token byte count as the GPU figure. Plus config 1 (the reference's own
+    op, self_attention at L=1, S=513) on the GPU, the library's host path and
+    the oracle."""
     import numpy as np
     import torch
 
     import oracle
+    import llaisys_amd as L
     from llaisys_amd import MemcpyKind, RuntimeAPI, DeviceType
 
+    threads, allowed, ncpu = host_cpus()
     api = RuntimeAPI(DeviceType.AMD)
+    capi = RuntimeAPI(DeviceType.CPU)
 
     def host_copy(lt, dtype, shape):
         t = torch.empty(shape, dtype=dtype)
         api.memcpy_sync(t.data_ptr(), lt.data_ptr(), t.numel() * t.element_size(), MemcpyKind.D2H)
         return t
 
-    kdev = host_copy(inst.k_pool, torch.int16, (inst.nb, 2, 16, 128)).numpy().view(np.uint16)
-    vdev = host_copy(inst.v_pool, torch.int16, (inst.nb, 2, 16, 128)).numpy().view(np.uint16)
+    def cpu_tensor(t, ldtype):
+        t = t.contiguous()
+        lt = L.Tensor(tuple(t.shape), dtype=ldtype, device=DeviceType.CPU)
+        capi.memcpy_sync(lt.data_ptr(), t.data_ptr(), t.numel() * t.element_size(), MemcpyKind.H2H)
+        return lt
+
+    kdev_t = host_copy(inst.k_pool, torch.int16, (inst.nb, 2, 16, 128))
+    vdev_t = host_copy(inst.v_pool, torch.int16, (inst.nb, 2, 16, 128))
+    kdev, vdev = kdev_t.numpy().view(np.uint16), vdev_t.numpy().view(np.uint16)
     k_log = oracle.unpack_pages_np(kdev, False)
     v_log = oracle.unpack_pages_np(vdev, True)
-    q = host_copy(inst.q, torch.int16, (inst.T, 12, 128)).numpy().view(np.uint16)
-    threads = min(os.cpu_count() or 1, 16)
-    # Grow the sample (a prefix of the batch) until one pass takes >= 1 s, then repeat within the budget.
+    q_t = host_copy(inst.q, torch.int16, (inst.T, 12, 128))
+    q = q_t.numpy().view(np.uint16)
+
+    def oracle_pass(n, nt):
+        return oracle.paged_attention(q[:n], k_log, v_log, inst.table_np[:n], inst.ctx[:n], SCALE, nthreads=nt)
+
     nseq = 4
     while True:
         t0 = time.perf_counter()
-        oracle.paged_attention(q[:nseq], k_log, v_log, inst.table_np[:nseq], inst.ctx[:nseq], SCALE, nthreads=threads)
-        dt = time.perf_counter() - t0
-        if dt >= 1.0 or nseq >= len(inst.ctx):
+        oracle_pass(nseq, threads)
+        if time.perf_counter() - t0 >= 1.0 or nseq >= len(inst.ctx):
             break
         nseq = min(len(inst.ctx), nseq * 2)
-    reps, total = 0, 0.0
-    while total < budget_s:
-        t0 = time.perf_counter()
-        ref = oracle.paged_attention(q[:nseq], k_log, v_log, inst.table_np[:nseq], inst.ctx[:nseq], SCALE,
-                                     nthreads=threads)
-        total += time.perf_counter() - t0
-        reps += 1
+    per, reps, total = _timed(lambda: oracle_pass(nseq, threads), budget_s)
+    ref = oracle_pass(nseq, threads)
     sample_bytes = int(inst.ctx[:nseq].sum()) * 1024 + 2 * nseq * 12 * 128 * 2
-    # The same scalar code on one thread, over the first 4 sequences.
-    n1, reps1, total1 = min(4, len(inst.ctx)), 0, 0.0
-    while total1 < budget_s / 4:
-        t0 = time.perf_counter()
-        oracle.paged_attention(q[:n1], k_log, v_log, inst.table_np[:n1], inst.ctx[:n1], SCALE, nthreads=1)
-        total1 += time.perf_counter() - t0
-        reps1 += 1
+    n1 = min(4, len(inst.ctx))
+    per1, reps1, total1 = _timed(lambda: oracle_pass(n1, 1), budget_s / 4)
     bytes1 = int(inst.ctx[:n1].sum()) * 1024 + 2 * n1 * 12 * 128 * 2
-    # Sanity: the GPU result for the sample agrees with the CPU result.
+
+    # The library's host path on the same sample (device page format as is).
+    kp = cpu_tensor(kdev_t.view(torch.bfloat16), L.DataType.BF16)
+    vp = cpu_tensor(vdev_t.view(torch.bfloat16), L.DataType.BF16)
+    qc = cpu_tensor(q_t[:nseq].view(torch.bfloat16), L.DataType.BF16)
+    tab = cpu_tensor(torch.from_numpy(np.ascontiguousarray(inst.table_np[:nseq])), L.DataType.I32)
+    cl = cpu_tensor(torch.from_numpy(np.ascontiguousarray(inst.ctx[:nseq])), L.DataType.I32)
+    oc = L.Tensor((nseq, 12, 128), dtype=L.DataType.F32, device=DeviceType.CPU)
+    perl, repsl, totall = _timed(lambda: L.Ops.paged_attention(oc, qc, kp, vp, tab, cl, SCALE), budget_s / 2)
+    lib_out = torch.empty((nseq, 12, 128), dtype=torch.float32)
+    capi.memcpy_sync(lib_out.data_ptr(), oc.data_ptr(), lib_out.numel() * 4, MemcpyKind.H2H)
+    lib_rel = float(np.max(np.abs(lib_out.numpy() - ref)) / np.max(np.abs(ref)))
+    assert L.device_error_flags() == 0
+
+    # Config 1: the reference's own op at L=1, S=513, 12:2, d=128, fp32.
+    qn, kn, vn = oracle.randn(1, (1, 12, 128)), oracle.randn(2, (513, 2, 128)), oracle.randn(3, (513, 2, 128))
+    c1_bytes = (qn.size + kn.size + vn.size + qn.size) * 4
+    c1_ref = oracle.self_attention(qn, kn, vn, SCALE)
+    cq, ck, cv = (cpu_tensor(torch.from_numpy(x), L.DataType.F32) for x in (qn, kn, vn))
+    co = L.Tensor((1, 12, 128), dtype=L.DataType.F32, device=DeviceType.CPU)
+    c1_lib, c1_lib_reps, _ = _timed(lambda: L.Ops.self_attention(co, cq, ck, cv, SCALE), 1.0, 10)
+    c1_got = torch.empty((1, 12, 128))
+    capi.memcpy_sync(c1_got.data_ptr(), co.data_ptr(), c1_got.numel() * 4, MemcpyKind.H2H)
+    c1_orc, c1_orc_reps, _ = _timed(lambda: oracle.self_attention(qn, kn, vn, SCALE), 1.0, 10)
+    gq, gk, gv = (torch.from_numpy(x).cuda() for x in (qn, kn, vn))
+    go = torch.zeros((1, 12, 128), device="cuda")
+
+    def as_ll(t):
+        lt = L.Tensor(tuple(t.shape), dtype=L.DataType.F32, device=DeviceType.AMD)
+        api.memcpy_sync(lt.data_ptr(), t.data_ptr(), t.numel() * 4, MemcpyKind.D2D)
+        return lt
+
+    lq, lk, lv, lo = as_ll(gq), as_ll(gk), as_ll(gv), as_ll(go)
+    stream = torch.cuda.ExternalStream(L.context_stream())
+    c1_gpu_ms, _ = time_steps(lambda i: L.Ops.self_attention(lo, lq, lk, lv, SCALE), stream, 200, 20)
+    c1_gpu_out = torch.empty((1, 12, 128))
+    api.memcpy_sync(c1_gpu_out.data_ptr(), lo.data_ptr(), c1_gpu_out.numel() * 4, MemcpyKind.D2H)
+
+    def rel(x):
+        return float(np.max(np.abs(x.numpy() - c1_ref)) / np.max(np.abs(c1_ref)))
+
     got = host_copy(inst.out, torch.bfloat16, (inst.T, 12, 128))[:nseq].float().numpy()
     max_err = float(np.max(np.abs(got - ref)))
     return {
-        "value": round(sample_bytes * reps / total / 1e9, 3),
+        "value": round(sample_bytes / per / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle/oracle.c paged attention (fp32) on the first {nseq} of {len(inst.ctx)} sequences "
-                  f"({int(inst.ctx[:nseq].sum())} tokens), {reps} reps in {total:.1f} s; "
-                  f"GPU bf16 vs CPU max|err| {max_err:.2e}",
+        "sample": f"oracle/oracle.c paged attention (fp32, OpenMP over sequences, {threads} threads of the "
+                  f"{allowed} CPUs this process may use; os.cpu_count() = {ncpu}) on the first {nseq} of "
+                  f"{len(inst.ctx)} sequences ({int(inst.ctx[:nseq].sum())} tokens), {reps} reps in "
+                  f"{total:.1f} s; GPU bf16 vs CPU max|err| {max_err:.2e}",
+        "host_cpus": {"used": threads, "affinity": allowed, "os_cpu_count": ncpu},
         "single_thread": {
-            "value": round(bytes1 * reps1 / total1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "value": round(bytes1 / per1 / 1e9, 3), "unit": "GB/s", "cores": 1,
             "sample": f"the same code with one thread on the first {n1} sequences "
                       f"({int(inst.ctx[:n1].sum())} tokens), {reps1} reps in {total1:.1f} s",
+        },
+        "library_host_path": {
+            "value": round(sample_bytes / perl / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "sample": f"llaisysPagedAttention on LLAISYS_DEVICE_CPU tensors (fp32 output), the same {nseq} "
+                      f"sequences, {repsl} reps in {totall:.1f} s; max|err| / max|oracle| {lib_rel:.1e}",
+        },
+        "config1_self_attention": {
+            "shape": "L=1, S=513, 12 q heads / 2 kv heads, d=128, fp32, causal",
+            "bytes_per_call": c1_bytes,
+            "gpu_us": round(c1_gpu_ms * 1e3, 2),
+            "library_host_path_us": round(c1_lib * 1e6, 1),
+            "oracle_one_thread_us": round(c1_orc * 1e6, 1),
+            "host_path_threads": threads,
+            "rel_err_vs_oracle": {"gpu": rel(c1_gpu_out), "library_host_path": rel(c1_got)},
         },
     }
 
@@ -817,6 +903,8 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the KV-cache path "
               "is built and measured on a single MI355X", file=sys.stderr)
         sys.exit(2)
+    # The library's host ops use this many threads (read once, at their first use).
+    os.environ.setdefault("LLAISYS_CPU_THREADS", str(host_cpus()[0]))
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"

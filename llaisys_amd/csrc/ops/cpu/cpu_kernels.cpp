@@ -7,6 +7,9 @@
 
 #include <algorithm>
 #include <atomic>
+#include <condition_variable>
+#include <mutex>
+#include <sched.h>
 #include <cmath>
 #include <cstdlib>
 #include <limits>
@@ -90,30 +93,94 @@ float ldAny(ElemType t, const void *p, size_t i) {
 // Widen n elements of any float type to fp32.
 void widen(float *dst, const void *src, ElemType t, size_t n);
 
-// Run fn(i) for i in [0, n) over the host threads, in contiguous chunks of at
-// least `grain` items. Exceptions inside fn are not allowed (none is thrown).
+// A persistent pool of threads() - 1 workers. One job runs at a time: a job
+// is a range [0, n) handed out in chunks through an atomic cursor; the caller
+// works on it too and returns when every chunk is done. A parallelFor issued
+// while another is running (another host thread, or nested) runs inline.
+class Pool {
+public:
+    static Pool &get() {
+        static Pool *p = new Pool(threads() - 1); // never destroyed: workers may outlive static teardown
+        return *p;
+    }
+
+    template <typename Fn> void run(size_t n, size_t chunk, Fn &fn) {
+        std::unique_lock<std::mutex> busy(busy_, std::try_to_lock);
+        if (!busy.owns_lock() || workers_.empty()) {
+            for (size_t i = 0; i < n; ++i) fn(i);
+            return;
+        }
+        auto body = [](void *ctx, size_t i) { (*static_cast<Fn *>(ctx))(i); };
+        {
+            std::lock_guard<std::mutex> g(m_);
+            job_ = {body, &fn, n, chunk};
+            cursor_.store(0);
+            pending_ = workers_.size();
+            ++generation_;
+        }
+        cv_.notify_all();
+        work(job_);
+        std::unique_lock<std::mutex> g(m_);
+        done_.wait(g, [&] { return pending_ == 0; });
+    }
+
+private:
+    struct Job {
+        void (*body)(void *, size_t);
+        void *ctx;
+        size_t n, chunk;
+    };
+
+    explicit Pool(int nworkers) {
+        for (int i = 0; i < nworkers; ++i) workers_.emplace_back([this] { loop(); });
+        for (auto &w : workers_) w.detach();
+    }
+
+    void work(const Job &j) {
+        for (;;) {
+            const size_t s = cursor_.fetch_add(j.chunk);
+            if (s >= j.n) return;
+            const size_t e = std::min(j.n, s + j.chunk);
+            for (size_t i = s; i < e; ++i) j.body(j.ctx, i);
+        }
+    }
+
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            Job j;
+            {
+                std::unique_lock<std::mutex> g(m_);
+                cv_.wait(g, [&] { return generation_ != seen; });
+                seen = generation_;
+                j = job_;
+            }
+            work(j);
+            std::lock_guard<std::mutex> g(m_);
+            if (--pending_ == 0) done_.notify_one();
+        }
+    }
+
+    std::vector<std::thread> workers_;
+    std::mutex busy_, m_;
+    std::condition_variable cv_, done_;
+    Job job_{};
+    std::atomic<size_t> cursor_{0};
+    size_t pending_ = 0;
+    uint64_t generation_ = 0;
+};
+
+// Run fn(i) for i in [0, n) over the host threads, in chunks of at least
+// `grain` items (one thread when n <= grain).
 template <typename Fn> void parallelFor(size_t n, size_t grain, Fn &&fn) {
     if (n == 0) return;
-    const size_t nt = std::min<size_t>(size_t(threads()), (n + grain - 1) / std::max<size_t>(grain, 1));
-    if (nt <= 1) {
+    grain = std::max<size_t>(grain, 1);
+    if (n <= grain || threads() == 1) {
         for (size_t i = 0; i < n; ++i) fn(i);
         return;
     }
-    std::atomic<size_t> next{0};
-    const size_t chunk = std::max<size_t>(grain, n / (nt * 8) + 1);
-    auto worker = [&] {
-        for (;;) {
-            const size_t s = next.fetch_add(chunk);
-            if (s >= n) return;
-            const size_t e = std::min(n, s + chunk);
-            for (size_t i = s; i < e; ++i) fn(i);
-        }
-    };
-    std::vector<std::thread> pool;
-    pool.reserve(nt - 1);
-    for (size_t t = 1; t < nt; ++t) pool.emplace_back(worker);
-    worker();
-    for (auto &th : pool) th.join();
+    const size_t chunk = std::max(grain, n / (size_t(threads()) * 8) + 1);
+    Pool::get().run(n, chunk, fn);
 }
 
 void widen(float *dst, const void *src, ElemType t, size_t n) {
@@ -256,6 +323,9 @@ int threads() {
             const int v = std::atoi(e);
             if (v > 0) return v;
         }
+        // the CPUs this process may run on (a container's share), not the machine's
+        cpu_set_t set;
+        if (sched_getaffinity(0, sizeof(set), &set) == 0 && CPU_COUNT(&set) > 0) return CPU_COUNT(&set);
         return int(std::max(1u, std::thread::hardware_concurrency()));
     }();
     return n;

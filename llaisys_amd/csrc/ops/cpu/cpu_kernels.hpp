@@ -4,7 +4,7 @@
 // src/ops/add/cpu/add_cpu.cpp:7-33); these are that CPU side. Plain pointers
 // and sizes, as the HIP launchers in kernels/launch.hpp take them. Math is
 // fp32; each result is rounded once to the tensor dtype. Work is split over
-// host threads (LLAISYS_CPU_THREADS, default: all hardware threads).
+// host threads (LLAISYS_CPU_THREADS, default: the CPUs the process may run on).
 #pragma once
 
 #include "../../kernels/launch.hpp"
