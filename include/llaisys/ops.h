@@ -108,6 +108,19 @@ __C {
                                         llaisysTensor_t v_pool, llaisysTensor_t block_table, llaisysTensor_t ctx_len,
                                         float scale);
 
+    /* No counterpart in the reference. llaisysPagedAttention (same arguments,
+     * same results to fp32 rounding, AMD tensors only) for callers that cannot
+     * allocate device memory: HIP graph capture, fixed-memory serving loops.
+     * The split records live in a fixed 16 MiB array that each GPU holds for
+     * the life of the process; a batch whose records need more (2 x W x G x
+     * 130 floats, W = max(1.75 x CUs, pairs / 64)) is refused with an error.
+     * Calls that overlap on one GPU (two streams, two host threads) share the
+     * array and race. The device's set-up (its first library call) allocates
+     * the error word; this entry point itself allocates nothing. */
+    __export void llaisysPagedAttentionNoAlloc(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor_t k_pool,
+                                               llaisysTensor_t v_pool, llaisysTensor_t block_table,
+                                               llaisysTensor_t ctx_len, float scale);
+
     /* New. Mixed chunked-prefill + decode attention over paged KV.
      * q, out [T, nh, 128]; sequence b owns query rows [cu_q[b], cu_q[b+1]) and
      * Lq = cu_q[b+1]-cu_q[b] (>= 1, <= ctx_len[b]) of its ctx_len[b] cached

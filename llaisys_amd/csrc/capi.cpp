@@ -387,6 +387,16 @@ void llaisysPagedAttention(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor
     });
 }
 
+void llaisysPagedAttentionNoAlloc(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor_t k_pool,
+                                  llaisysTensor_t v_pool, llaisysTensor_t block_table, llaisysTensor_t ctx_len,
+                                  float scale) {
+    guardedVoid([&] {
+        const char *w = "paged_attention_no_alloc";
+        llaisys::ops::pagedAttentionNoAlloc(unbox(out, w), unbox(q, w), unbox(k_pool, w), unbox(v_pool, w),
+                                            unbox(block_table, w), unbox(ctx_len, w), scale);
+    });
+}
+
 void llaisysPagedAttentionVarlen(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor_t k_pool,
                                  llaisysTensor_t v_pool, llaisysTensor_t block_table, llaisysTensor_t cu_q,
                                  llaisysTensor_t ctx_len, float scale) {

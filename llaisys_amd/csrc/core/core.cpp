@@ -2,6 +2,7 @@
 
 #include "../common.hpp"
 #include "../device/runtime_api.hpp"
+#include "../kernels/launch.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -27,6 +28,12 @@ Storage::~Storage() {
 Runtime::Runtime(llaisysDeviceType_t type, int id) : type_(type), id_(id), api_(device::getRuntimeAPI(type)) {
     api_->set_device(id_);
     stream_ = api_->create_stream();
+    if (type_ == LLAISYS_DEVICE_AMD) {
+        // Per-device set-up: the error word exists from here on (entry points
+        // never allocate it), and the allocation-free decode finds its scratch.
+        errorWord();
+        kernels::noAllocInit();
+    }
 }
 
 Runtime::~Runtime() {

@@ -54,6 +54,17 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
                  int nkvh, int max_pages, int num_blocks, float scale, const DecodePlan &plan, float *records,
                  int *err, int *slot_headers, void *slot_records, void *stream);
 
+// The decode above with its split records in a fixed per-GPU device array
+// (noAllocScratchBytes() bytes) instead of runtime workspace: no device
+// allocation per call. noAllocInit() looks the array's address up for the
+// current device (once per device; the runtime's set-up calls it). Calls that
+// overlap on one GPU share the array and race.
+void noAllocInit();
+size_t noAllocScratchBytes();
+void pagedDecodeNoAlloc(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                        const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                        int num_blocks, float scale, int *err, void *stream);
+
 // Chunked prefill: the sequences of a varlen batch with >= 2 queries, as
 // (16-column query tile, kv head) units split over pages, then a combine kernel.
 // Copy whole blocks (all kv heads, K and V): pairs[P][2] = (src, dst).

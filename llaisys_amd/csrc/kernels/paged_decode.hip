@@ -484,6 +484,67 @@ int computeUnits() {
 
 } // namespace
 
+// Device workspace of pagedDecodeNoAlloc (llaisysPagedAttentionNoAlloc):
+// split records of the decode kernel, in a fixed array each GPU holds for the
+// life of the process instead of runtime allocations. In host code `scratch`
+// names a host-side stand-in; kernels get the device address that
+// hipGetSymbolAddress returns, looked up once per device by noAllocInit().
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+} // namespace
+
+void noAllocInit() {
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    LLAISYS_CHECK(dev >= 0 && dev < kMaxDevices, "device id " << dev << " beyond " << kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return;
+    void *ptr = nullptr;
+    HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    LLAISYS_CHECK(ptr != nullptr, "hipGetSymbolAddress returned no address for the decode scratch");
+    computeUnits(); // cached per device here, so the entry point's plan only reads it
+    g_scratch_ptr[dev] = ptr;
+}
+
+size_t noAllocScratchBytes() { return kNoAllocScratchBytes; }
+
+void pagedDecodeNoAlloc(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                        const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                        int num_blocks, float scale, int *err, void *stream) {
+    if (B == 0) return;
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    void *ptr = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = dev >= 0 && dev < kMaxDevices ? g_scratch_ptr[dev] : nullptr;
+    }
+    LLAISYS_CHECK(ptr, "paged_attention_no_alloc: device " << dev << " is not set up (noAllocInit)");
+    const int G = nh / nkvh;
+    const size_t esz = out_f32 ? 4 : 2;
+    // Sequences in chunks whose length prefix fits the kernel's LDS; the
+    // chunks run one after another on the stream and reuse the records.
+    for (int b0 = 0; b0 < B; b0 += kDecodeMaxBatch) {
+        const int Bc = std::min(kDecodeMaxBatch, B - b0);
+        DecodePlan plan = planDecode(Bc, nkvh, G, max_pages);
+        plan.slot_headers = 0; // per-wave records only: nothing to keep zeroed between calls
+        plan.slot_record_bytes = 0;
+        LLAISYS_CHECK(plan.record_bytes <= kNoAllocScratchBytes,
+                      "paged_attention_no_alloc: " << Bc << " sequences x " << nkvh << " kv heads x " << max_pages
+                          << " pages need " << plan.record_bytes << " bytes of split records, more than the "
+                          << kNoAllocScratchBytes << "-byte scratch; use llaisysPagedAttention");
+        pagedDecode(static_cast<std::byte *>(out) + size_t(b0) * nh * kHeadDim * esz, out_f32,
+                    q + size_t(b0) * nh * kHeadDim, k_pool, v_pool, block_table + size_t(b0) * max_pages,
+                    ctx_len + b0, nullptr, Bc, Bc, nh, nkvh, max_pages, num_blocks, scale, plan,
+                    static_cast<float *>(ptr), err, nullptr, nullptr, stream);
+    }
+}
+
 DecodePlan planDecode(int B, int nkvh, int group, int max_pages) {
     DecodePlan p{};
     const long long max_pairs = (long long)B * nkvh * ((max_pages + 1) / 2);

@@ -252,9 +252,16 @@ void pagedKVCopyBlocks(const tensor_t &k_pool, const tensor_t &v_pool, const ten
         K::pagedCopyBlocks(kp, vp, pr, P, nkvh, nb, errWord(), streamOf());
 }
 
-void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_pool, const tensor_t &v_pool,
-                    const tensor_t &block_table, const tensor_t &ctx_len, const tensor_t &cu_q, float scale) {
-    const char *op = cu_q ? "paged_attention_varlen" : "paged_attention";
+namespace {
+
+// Shapes, dtypes and layouts of a paged attention call (decode when cu_q is
+// null); returns {T, nh, nkvh, B}.
+struct AttnDims {
+    size_t T, nh, nkvh, B;
+};
+AttnDims checkAttention(const char *op, const tensor_t &out, const tensor_t &q, const tensor_t &k_pool,
+                        const tensor_t &v_pool, const tensor_t &block_table, const tensor_t &ctx_len,
+                        const tensor_t &cu_q) {
     LLAISYS_CHECK(out && q && k_pool && v_pool && block_table && ctx_len, op << ": null tensor");
     checkPool(k_pool, v_pool, op);
     const size_t nkvh = k_pool->shape()[1];
@@ -278,6 +285,15 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
     } else {
         LLAISYS_CHECK(T == B, op << ": q must hold one query per sequence (T=" << T << ", B=" << B << ")");
     }
+    return {T, nh, nkvh, B};
+}
+
+} // namespace
+
+void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_pool, const tensor_t &v_pool,
+                    const tensor_t &block_table, const tensor_t &ctx_len, const tensor_t &cu_q, float scale) {
+    const char *op = cu_q ? "paged_attention_varlen" : "paged_attention";
+    const auto [T, nh, nkvh, B] = checkAttention(op, out, q, k_pool, v_pool, block_table, ctx_len, cu_q);
     const bool host = onHost(op, {&out, &q, &k_pool, &v_pool, &block_table, &ctx_len, &cu_q});
     if (T == 0 || B == 0) return;
     const int max_pages = int(block_table->shape()[1]);
@@ -330,6 +346,25 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
                    scale, dplan, records, rt.errorWord(), slot_hdr, slot_rec, rt.stream());
     K::pagedPrefill(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
                     scale, pplan, records, rt.errorWord(), rt.stream());
+}
+
+// No counterpart in the reference: the decode above for callers that cannot
+// allocate device memory (graph capture, fixed-memory serving loops).
+void pagedAttentionNoAlloc(const tensor_t &out, const tensor_t &q, const tensor_t &k_pool, const tensor_t &v_pool,
+                           const tensor_t &block_table, const tensor_t &ctx_len, float scale) {
+    const char *op = "paged_attention_no_alloc";
+    const auto [T, nh, nkvh, B] = checkAttention(op, out, q, k_pool, v_pool, block_table, ctx_len, nullptr);
+    LLAISYS_CHECK(!onHost(op, {&out, &q, &k_pool, &v_pool, &block_table, &ctx_len}),
+                  op << ": AMD device tensors only (host tensors use llaisysPagedAttention)");
+    if (T == 0 || B == 0) return;
+    const int max_pages = int(block_table->shape()[1]);
+    LLAISYS_CHECK(max_pages > 0, op << ": block_table has no pages");
+    K::pagedDecodeNoAlloc(out->data(), out->dtype() == LLAISYS_DTYPE_F32, reinterpret_cast<const uint16_t *>(q->data()),
+                          reinterpret_cast<const uint16_t *>(k_pool->data()),
+                          reinterpret_cast<const uint16_t *>(v_pool->data()),
+                          reinterpret_cast<const int32_t *>(block_table->data()),
+                          reinterpret_cast<const int32_t *>(ctx_len->data()), int(B), int(nh), int(nkvh), max_pages,
+                          int(k_pool->shape()[0]), scale, errWord(), streamOf());
 }
 
 } // namespace llaisys::ops

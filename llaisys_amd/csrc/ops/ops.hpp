@@ -23,6 +23,11 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
                     const tensor_t &block_table, const tensor_t &ctx_len, const tensor_t &cu_q /* null = decode */,
                     float scale);
 
+// Decode attention (pagedAttention with cu_q null) with no device allocation:
+// split records in the decode kernel's fixed per-GPU scratch. AMD tensors only.
+void pagedAttentionNoAlloc(const tensor_t &out, const tensor_t &q, const tensor_t &k_pool, const tensor_t &v_pool,
+                           const tensor_t &block_table, const tensor_t &ctx_len, float scale);
+
 // Model ops of the reference (README.md:145-292), AMD device.
 void add(const tensor_t &c, const tensor_t &a, const tensor_t &b);
 void argmax(const tensor_t &max_idx, const tensor_t &max_val, const tensor_t &vals);

@@ -28,6 +28,7 @@ def load_ops(lib):
         ("llaisysPagedKVAppendGather", [T, T, T, T, T, T, T, T, T]),
         # out, q, k_pool, v_pool, block_table, ctx_len, scale
         ("llaisysPagedAttention", [T, T, T, T, T, T, c_float]),
+        ("llaisysPagedAttentionNoAlloc", [T, T, T, T, T, T, c_float]),
         # out, q, k_pool, v_pool, block_table, cu_q, ctx_len, scale
         ("llaisysPagedAttentionVarlen", [T, T, T, T, T, T, T, c_float]),
     ]:

@@ -100,6 +100,14 @@ class Ops:
         check_last_error()
 
     @staticmethod
+    def paged_attention_no_alloc(out: Tensor, q: Tensor, k_pool: Tensor, v_pool: Tensor,
+                                 block_table: Tensor, ctx_len: Tensor, scale: float):
+        """paged_attention with no device allocation (fixed per-GPU scratch)."""
+        LIB_LLAISYS.llaisysPagedAttentionNoAlloc(_h(out), _h(q), _h(k_pool), _h(v_pool),
+                                                 _h(block_table), _h(ctx_len), c_float(scale))
+        check_last_error()
+
+    @staticmethod
     def paged_attention_varlen(out: Tensor, q: Tensor, k_pool: Tensor, v_pool: Tensor,
                                block_table: Tensor, cu_q: Tensor, ctx_len: Tensor, scale: float):
         """Mixed chunked-prefill + decode attention over paged KV."""
