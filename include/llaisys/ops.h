@@ -46,6 +46,18 @@ __C {
     /* ops.h:10: out = in . weight^T + bias, weight [out, in], bias may be NULL
      * (README.md:181-198); rocBLAS GEMM, fp32 accumulation. */
     __export void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, llaisysTensor_t bias);
+    /* New; no counterpart in the reference (whose linear is ops.h:10). The
+     * weight of llaisysLinear, rewritten once into the layout the decode GEMM
+     * streams (tiles of 16 rows x 32 columns in MFMA operand order): packed
+     * and weight are [N, K] BF16 on the AMD device, N % 16 == 0, K % 32 == 0. */
+    __export void llaisysLinearPackWeight(llaisysTensor_t packed, llaisysTensor_t weight);
+    /* New; no counterpart in the reference. out = in . W^T + bias (bias may be
+     * NULL) as llaisysLinear computes it (fp32 accumulation, one rounding),
+     * with W given packed by llaisysLinearPackWeight; for decode-sized batches:
+     * in [M, K], out [M, N] BF16 on the AMD device, 1 <= M <= 128, K == 1536,
+     * N % 16 == 0 (other shapes: llaisysLinear). */
+    __export void llaisysLinearPacked(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t packed,
+                                      llaisysTensor_t bias);
     /* ops.h:11: copy between equal shapes with any strides (README.md:286-292). */
     __export void llaisysRearrange(llaisysTensor_t out, llaisysTensor_t in);
     /* ops.h:12: y = w * x / sqrt(mean(x^2) + eps) per row (README.md:202-217). */

@@ -349,6 +349,20 @@ void llaisysSelfAttention(llaisysTensor_t attn_val, llaisysTensor_t q, llaisysTe
     });
 }
 
+void llaisysLinearPackWeight(llaisysTensor_t packed, llaisysTensor_t weight) {
+    guardedVoid([&] {
+        const char *w = "linear_pack_weight";
+        llaisys::ops::linearPackWeight(unbox(packed, w), unbox(weight, w));
+    });
+}
+
+void llaisysLinearPacked(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t packed, llaisysTensor_t bias) {
+    guardedVoid([&] {
+        const char *w = "linear_packed";
+        llaisys::ops::linearPacked(unbox(out, w), unbox(in, w), unbox(packed, w), bias ? unbox(bias, w) : nullptr);
+    });
+}
+
 void llaisysPagedKVAppend(llaisysTensor_t k_pool, llaisysTensor_t v_pool, llaisysTensor_t k_new, llaisysTensor_t v_new,
                           llaisysTensor_t block_table, llaisysTensor_t ctx_len, llaisysTensor_t cu_new) {
     guardedVoid([&] {

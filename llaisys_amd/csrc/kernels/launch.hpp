@@ -110,6 +110,20 @@ void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *s
 void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream,
             bool accumulate = false);
 
+// ---- decode-sized projections (decode_gemm.hip), bf16
+// Y[M, N] (+)= X[M, K] . W[N, K]^T for M <= kDecodeGemmMaxM, K == kDecodeGemmK,
+// N % 16 == 0, with W pre-packed by packWeight (N * K elements, MFMA operand
+// order; fold_g, if given, multiplies column k by fold_g[k] before the one
+// rounding to bf16). accumulate adds the old Y before the one rounding (a
+// bias enters that way: preset Y's rows to it).
+constexpr int kDecodeGemmMaxM = 128;
+constexpr int kDecodeGemmK = 1536;
+bool decodeGemmSupported(int M, int N, int K);
+size_t packedWeightElems(int N, int K);
+void packWeight(uint16_t *packed, const uint16_t *w, const uint16_t *fold_g, int N, int K, void *stream);
+void decodeGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
+                void *stream);
+
 // ---- Qwen2 step glue (qwen2_step.hip), bf16
 // qkv [T, (nh + 2 nkvh) d] + bias -> q [T, nh, d] rotated by position, and k
 // (rotated) and v written

@@ -66,6 +66,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     if (const char *e = std::getenv("LLAISYS_QWEN2_GRAPHS")) use_graphs_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_QWEN2_FOLD_NORM")) fold_norm_ = e[0] != '0';
+    if (const char *e = std::getenv("LLAISYS_DECODE_GEMM")) decode_gemm_ = e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -92,7 +93,14 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
             L.qkv_wf = dev({q + 2 * kv, cfg.hs}, dt, dev_);
             L.gate_up_wf = dev({2 * cfg.di, cfg.hs}, dt, dev_);
         }
+        if (decode_gemm_ && fold_norm_ && K::decodeGemmSupported(1, int(q + 2 * kv), int(cfg.hs)) &&
+            K::decodeGemmSupported(1, int(2 * cfg.di), int(cfg.hs))) {
+            L.qkv_wfp = dev({q + 2 * kv, cfg.hs}, dt, dev_);
+            L.gate_up_wfp = dev({2 * cfg.di, cfg.hs}, dt, dev_);
+        }
+        if (decode_gemm_ && K::decodeGemmSupported(1, int(cfg.hs), int(q))) L.o_wp = dev({cfg.hs, q}, dt, dev_);
     }
+    if (decode_gemm_ && K::decodeGemmSupported(1, int(cfg.voc), int(cfg.hs))) out_embed_p_ = dev({cfg.voc, cfg.hs}, dt, dev_);
     for (size_t l = 0; l < cfg.nlayer; ++l) {
         k_pool_.push_back(dev({num_blocks, cfg.nkvh, size_t(K::kPageTokens), cfg.dh}, LLAISYS_DTYPE_BF16, dev_));
         v_pool_.push_back(dev({num_blocks, cfg.nkvh, size_t(K::kPageTokens), cfg.dh}, LLAISYS_DTYPE_BF16, dev_));
@@ -407,19 +415,36 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
 }
 
 void Qwen2Model::ensureFolded() {
-    if (!fold_norm_) return;
     void *s = core::context().runtime().stream();
+    // Packed copies for the decode GEMM: o_w and the LM head from their own
+    // versions, the folded projections whenever they are refolded below.
+    if (out_embed_p_ && out_embed_->version() != out_embed_packed_from_) {
+        K::packWeight(u16(out_embed_p_), u16(out_embed_), nullptr, int(cfg_.voc), int(cfg_.hs), s);
+        out_embed_packed_from_ = out_embed_->version();
+    }
+    for (auto &L : layers_) {
+        if (L.o_wp && L.o_w->version() != L.o_packed_from) {
+            K::packWeight(u16(L.o_wp), u16(L.o_w), nullptr, int(L.o_w->shape()[0]), int(L.o_w->shape()[1]), s);
+            L.o_packed_from = L.o_w->version();
+        }
+    }
+    if (!fold_norm_) return;
     for (auto &L : layers_) {
         const uint64_t v[4] = {L.qkv_w->version(), L.attn_norm->version(), L.gate_up_w->version(),
                                L.mlp_norm->version()};
         if (v[0] != L.folded_from[0] || v[1] != L.folded_from[1]) {
             K::foldNormColumns(u16(L.qkv_wf), u16(L.qkv_w), u16(L.attn_norm), L.qkv_w->shape()[0], int(cfg_.hs), s);
+            if (L.qkv_wfp)
+                K::packWeight(u16(L.qkv_wfp), u16(L.qkv_wf), nullptr, int(L.qkv_w->shape()[0]), int(cfg_.hs), s);
             L.folded_from[0] = v[0];
             L.folded_from[1] = v[1];
         }
         if (v[2] != L.folded_from[2] || v[3] != L.folded_from[3]) {
             K::foldNormColumns(u16(L.gate_up_wf), u16(L.gate_up_w), u16(L.mlp_norm), L.gate_up_w->shape()[0],
                                int(cfg_.hs), s);
+            if (L.gate_up_wfp)
+                K::packWeight(u16(L.gate_up_wfp), u16(L.gate_up_wf), nullptr, int(L.gate_up_w->shape()[0]),
+                              int(cfg_.hs), s);
             L.folded_from[2] = v[2];
             L.folded_from[3] = v[3];
         }
@@ -447,22 +472,39 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
         const bool fold = fold_norm_ && T <= kFoldMaxRows;
         const uint16_t *xr = fold ? u16(x_) : nullptr;
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
-        gemm(qkv_, fold ? x_ : h_, fold ? L.qkv_wf : L.qkv_w, nullptr, M, q + 2 * kv, hs, false, s);
+        project(qkv_, fold ? x_ : h_, fold ? L.qkv_wf : L.qkv_w, fold ? L.qkv_wfp : nullptr, M, q + 2 * kv, hs, false,
+                s);
         K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
                          i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh), int(cfg_.nkvh),
                          int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), xr, hs,
                          cfg_.epsilon, s);
         ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_, scale);
-        gemm(x_, attn_, L.o_w, nullptr, M, hs, q, true, s);
+        project(x_, attn_, L.o_w, L.o_wp, M, hs, q, true, s);
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
-        gemm(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, nullptr, M, 2 * di, hs, false, s);
+        project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, fold ? L.gate_up_wfp : nullptr, M, 2 * di, hs,
+                false, s);
         K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s);
         gemm(x_, act_, L.down_w, nullptr, M, hs, di, true, s);
     }
     K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);
-    gemm(logits_, hl_, out_embed_, nullptr, int(B), int(cfg_.voc), hs, false, s);
+    project(logits_, hl_, out_embed_, out_embed_p_, int(B), int(cfg_.voc), hs, false, s);
     K::argmax(i64(next_), nullptr, logits_->data(), et, B, int64_t(cfg_.voc),
               rt.scratch(K::argmaxWorkspaceBytes(B, int64_t(cfg_.voc))), s);
+}
+
+// Largest M at which the decode GEMM beats the library GEMM for a weight of
+// N rows (K = 1536, weights cold in HBM, MI355X; bench-measured): the LM head
+// (N = 151936) at every M <= 128, gate-up (N = 17920) up to 96, qkv and o
+// (N = 2048, 1536) up to 64, where the library's own launches win on latency.
+static int decodeGemmMaxM(int N) { return N >= 65536 ? 128 : N >= 8192 ? 96 : 64; }
+
+void Qwen2Model::project(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &packed, int M,
+                         int N, int K, bool accumulate, void *s) const {
+    if (packed && M <= decodeGemmMaxM(N) && K::decodeGemmSupported(M, N, K)) {
+        K::decodeGemm(u16(y), u16(x), u16(packed), M, N, K, accumulate, s);
+        return;
+    }
+    gemm(y, x, w, nullptr, M, N, K, accumulate, s);
 }
 
 tensor_t Qwen2Model::lastLogits() const {

@@ -41,6 +41,10 @@ struct Qwen2LayerWeights {
     // gate_up_w, mlp_norm) they were folded from
     tensor_t qkv_wf, gate_up_wf;
     uint64_t folded_from[4] = {~0ull, ~0ull, ~0ull, ~0ull};
+    // The decode GEMM's packed copies (MFMA operand order) of the folded QKV
+    // and gate-up weights and of o_w; null when the shapes do not qualify.
+    tensor_t qkv_wfp, gate_up_wfp, o_wp;
+    uint64_t o_packed_from = ~0ull;
 };
 
 class Qwen2Model {
@@ -86,6 +90,11 @@ private:
     // Refold each layer whose projection or norm weights were written since
     // their folded copies were made (a check of version counters per step).
     void ensureFolded();
+    // Y[M, N] (+)= X W^T: the hand-written decode GEMM over `packed` when it
+    // exists and M is at most the size where it beats the library for this N,
+    // else the library GEMM over the row-major `w`.
+    void project(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &packed, int M, int N, int K,
+                 bool accumulate, void *s) const;
     void decodeGraph(size_t B, size_t width);
     std::vector<int32_t> reserveAll(const int64_t *ids, size_t B, const size_t *n, std::vector<int32_t> &before);
 
@@ -98,6 +107,9 @@ private:
     bool have0_ = false;
 
     tensor_t in_embed_, out_embed_, out_norm_;
+    tensor_t out_embed_p_; // packed LM head for the decode GEMM (null when the shape does not qualify)
+    uint64_t out_embed_packed_from_ = ~0ull;
+    bool decode_gemm_ = true; // LLAISYS_DECODE_GEMM=0: library GEMMs only
     std::vector<Qwen2LayerWeights> layers_;
     std::vector<tensor_t> k_pool_, v_pool_;
 

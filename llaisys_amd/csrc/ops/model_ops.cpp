@@ -124,6 +124,40 @@ void linear(const tensor_t &out, const tensor_t &in, const tensor_t &weight, con
               int(N), int(Kd), stream());
 }
 
+void linearPackWeight(const tensor_t &packed, const tensor_t &weight) {
+    const char *op = "linear_pack_weight";
+    LLAISYS_CHECK(packed && weight, op << ": null tensor");
+    LLAISYS_CHECK(weight->ndim() == 2 && packed->shape() == weight->shape(),
+                  op << ": packed must have the weight's shape [N, K], got " << shapeOf(packed) << " for "
+                     << shapeOf(weight));
+    LLAISYS_CHECK(weight->dtype() == LLAISYS_DTYPE_BF16 && packed->dtype() == LLAISYS_DTYPE_BF16, op << ": bf16 only");
+    const int N = int(weight->shape()[0]), Kd = int(weight->shape()[1]);
+    LLAISYS_CHECK(N % 16 == 0 && Kd % 32 == 0, op << ": needs N % 16 == 0 and K % 32 == 0");
+    LLAISYS_CHECK(!onHost(op, {&packed, &weight}), op << ": AMD device tensors only");
+    K::packWeight(reinterpret_cast<uint16_t *>(packed->data()), reinterpret_cast<const uint16_t *>(weight->data()),
+                  nullptr, N, Kd, stream());
+}
+
+void linearPacked(const tensor_t &out, const tensor_t &in, const tensor_t &packed, const tensor_t &bias) {
+    const char *op = "linear_packed";
+    LLAISYS_CHECK(out && in && packed, op << ": null tensor");
+    LLAISYS_CHECK(in->ndim() == 2 && packed->ndim() == 2 && out->ndim() == 2, op << ": in, packed, out must be 2-D");
+    const int M = int(in->shape()[0]), Kd = int(in->shape()[1]), N = int(packed->shape()[0]);
+    LLAISYS_CHECK(int(packed->shape()[1]) == Kd, op << ": packed " << shapeOf(packed) << " does not match in " << shapeOf(in));
+    LLAISYS_CHECK(int(out->shape()[0]) == M && int(out->shape()[1]) == N, op << ": out must be [" << M << ", " << N << "]");
+    if (bias) LLAISYS_CHECK(bias->ndim() == 1 && int(bias->shape()[0]) == N, op << ": bias must be [" << N << "]");
+    for (auto *t : {&out, &in, &packed, &bias})
+        if (*t) LLAISYS_CHECK((*t)->dtype() == LLAISYS_DTYPE_BF16, op << ": bf16 only");
+    LLAISYS_CHECK(K::decodeGemmSupported(M, N, Kd), op << ": needs 1 <= M <= " << K::kDecodeGemmMaxM << ", K == "
+                                                       << K::kDecodeGemmK << ", N % 16 == 0 (M=" << M << ", N=" << N
+                                                       << ", K=" << Kd << "); use llaisysLinear");
+    LLAISYS_CHECK(!onHost(op, {&out, &in, &packed, &bias}), op << ": AMD device tensors only");
+    auto *y = reinterpret_cast<uint16_t *>(out->data());
+    if (bias) K::fillRows(y, bias->data(), K::ElemType::BF16, size_t(M), size_t(N), stream());
+    K::decodeGemm(y, reinterpret_cast<const uint16_t *>(in->data()), reinterpret_cast<const uint16_t *>(packed->data()),
+                  M, N, Kd, bias != nullptr, stream());
+}
+
 void rearrange(const tensor_t &out, const tensor_t &in) {
     const char *op = "rearrange";
     LLAISYS_CHECK(out && in, op << ": null tensor");

@@ -34,6 +34,10 @@ void argmax(const tensor_t &max_idx, const tensor_t &max_val, const tensor_t &va
 void embedding(const tensor_t &out, const tensor_t &index, const tensor_t &weight);
 void linear(const tensor_t &out, const tensor_t &in, const tensor_t &weight, const tensor_t &bias /* may be null */);
 void rearrange(const tensor_t &out, const tensor_t &in);
+// linear for decode-sized batches over a weight packed once by linearPackWeight
+// (AMD, bf16; M <= 128, K == 1536, N % 16 == 0).
+void linearPackWeight(const tensor_t &packed, const tensor_t &weight);
+void linearPacked(const tensor_t &out, const tensor_t &in, const tensor_t &packed, const tensor_t &bias);
 void rmsNorm(const tensor_t &out, const tensor_t &in, const tensor_t &weight, float eps);
 void rope(const tensor_t &out, const tensor_t &in, const tensor_t &pos_ids, float theta);
 void swiglu(const tensor_t &out, const tensor_t &gate, const tensor_t &up);

@@ -27,6 +27,8 @@ def load_ops(lib):
         # k_out, v_out, k_pool, v_pool, k_new, v_new, block_table, ctx_len, cu_seqlens
         ("llaisysPagedKVAppendGather", [T, T, T, T, T, T, T, T, T]),
         # out, q, k_pool, v_pool, block_table, ctx_len, scale
+        ("llaisysLinearPackWeight", [T, T]),
+        ("llaisysLinearPacked", [T, T, T, T]),
         ("llaisysPagedAttention", [T, T, T, T, T, T, c_float]),
         ("llaisysPagedAttentionNoAlloc", [T, T, T, T, T, T, c_float]),
         # out, q, k_pool, v_pool, block_table, cu_q, ctx_len, scale

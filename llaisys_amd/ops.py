@@ -35,6 +35,18 @@ class Ops:
         check_last_error()
 
     @staticmethod
+    def linear_pack_weight(packed: Tensor, weight: Tensor):
+        """Rewrite weight [N, K] into the decode GEMM's packed layout (same shape)."""
+        LIB_LLAISYS.llaisysLinearPackWeight(_h(packed), _h(weight))
+        check_last_error()
+
+    @staticmethod
+    def linear_packed(out: Tensor, inp: Tensor, packed: Tensor, bias: Tensor = None):
+        """linear with a packed weight, for decode-sized batches (M <= 128, K == 1536)."""
+        LIB_LLAISYS.llaisysLinearPacked(_h(out), _h(inp), _h(packed), _h(bias))
+        check_last_error()
+
+    @staticmethod
     def rearrange(out: Tensor, inp: Tensor):
         LIB_LLAISYS.llaisysRearrange(_h(out), _h(inp))
         check_last_error()

@@ -190,3 +190,36 @@ def test_linear_bf16_decode_batches(M, N, K, use_bias):
     # one bf16 rounding (2^-9 relative) plus fp32 accumulation of K products
     bound = ref.abs() * 2.0 ** -8 + 1e-6 * (x.double().abs() @ w.double().abs().T) * K ** 0.5 + 1e-30
     assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
+
+
+PACKED = [(1, 16), (7, 2048), (16, 1536), (33, 2048), (64, 4096), (100, 1536), (128, 2048), (128, 17920),
+          (128, 1536), (120, 151936)]
+
+
+@pytest.mark.parametrize("M,N", PACKED, ids=[f"{m}x{n}" for m, n in PACKED])
+@pytest.mark.parametrize("use_bias", [True, False])
+def test_linear_packed_decode_gemm(M, N, use_bias):
+    # The hand-written decode GEMM (llaisysLinearPacked over a weight packed by
+    # llaisysLinearPackWeight) against float64 torch, to the same bound as the
+    # library path: one bf16 rounding plus fp32 accumulation.
+    K = 1536
+    x, w = rnd((M, K), torch.bfloat16, 0.5, seed=M + 3), rnd((N, K), torch.bfloat16, 0.05, seed=N + 5)
+    b = rnd((N,), torch.bfloat16, seed=19) if use_bias else None
+    packed = to_llaisys(torch.zeros(N, K, dtype=torch.bfloat16, device=DEV))
+    L.Ops.linear_pack_weight(packed, to_llaisys(w))
+    out = to_llaisys(torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV))
+    L.Ops.linear_packed(out, to_llaisys(x), packed, to_llaisys(b) if use_bias else None)
+    ref = x.double() @ w.double().T
+    if use_bias:
+        ref += b.double()
+    got = to_torch(out).double()
+    bound = ref.abs() * 2.0 ** -8 + 1e-6 * (x.double().abs() @ w.double().abs().T) * K ** 0.5 + 1e-30
+    assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
+
+
+def test_linear_packed_refuses_unsupported_shapes():
+    x = to_llaisys(torch.zeros(129, 1536, dtype=torch.bfloat16, device=DEV))
+    w = to_llaisys(torch.zeros(32, 1536, dtype=torch.bfloat16, device=DEV))
+    out = to_llaisys(torch.zeros(129, 32, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(L.LlaisysError, match="M <= 128"):
+        L.Ops.linear_packed(out, x, w)
