@@ -46,6 +46,7 @@ struct GemmArgs {
     const uint16_t *x;
     const u32x4 *wp;     // packed W
     int M, N, K, nblocks, accumulate;
+    int mgroups; // workgroups per row block, each on its own 16 MB rows of X and Y
 };
 
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
@@ -63,7 +64,13 @@ decodeGemmKernel(GemmArgs a) {
     const int lane = threadIdx.x & 63;
     const int KT = a.K / 32; // tiles per row block
     const int kb0 = wave * KS;
-    const int first = blockIdx.x, stride = gridDim.x;
+    // M split over mgroups workgroups per row block (small N, large M: the
+    // weights are read mgroups times, each workgroup's X is that much smaller).
+    const int mg = int(blockIdx.x) % a.mgroups;
+    const int first = int(blockIdx.x) / a.mgroups, stride = int(gridDim.x) / a.mgroups;
+    a.x += size_t(mg) * 16 * MB * a.K;
+    a.y += size_t(mg) * 16 * MB * a.N;
+    a.M = min(16 * MB, a.M - mg * 16 * MB);
 
     // X for the wave's k range and all 16 MB rows, loaded before anything
     // else (loads complete in order, so a later wait on the W ring never has
@@ -202,7 +209,17 @@ template <int MB> void launchGemm(const GemmArgs &a, hipStream_t s) {
         hipLaunchKernelGGL((decodeGemmKernel<MB, KS, false, W>), dim3(grid), dim3(64 * W), lds, s, a);
 }
 
-void launchByM(const GemmArgs &a, hipStream_t s) {
+// Weights of fewer rows than this are latency-bound: past 64 rows of X the
+// M range splits over workgroups (4 m blocks each) instead of growing the
+// per-workgroup X.
+constexpr int kSplitMaxN = 8192;
+
+void launchByM(GemmArgs a, hipStream_t s) {
+    if (a.M > 64 && a.N < kSplitMaxN) {
+        a.mgroups = (a.M + 63) / 64;
+        return launchGemm<4>(a, s);
+    }
+    a.mgroups = 1;
     switch ((a.M + 15) / 16) {
     case 1: return launchGemm<1>(a, s);
     case 2: return launchGemm<2>(a, s);
@@ -236,7 +253,7 @@ void decodeGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, i
                 void *stream) {
     LLAISYS_CHECK(decodeGemmSupported(M, N, K),
                   "decodeGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
-    GemmArgs a{y, x, reinterpret_cast<const u32x4 *>(packed), M, N, K, N / 16, accumulate ? 1 : 0};
+    GemmArgs a{y, x, reinterpret_cast<const u32x4 *>(packed), M, N, K, N / 16, accumulate ? 1 : 0, 1};
     launchByM(a, static_cast<hipStream_t>(stream));
     HIP_CHECK(hipGetLastError());
 }
