@@ -205,6 +205,45 @@ def _timed(fn, budget_s, min_reps=1):
     return total / reps, reps, total
 
 
+def host_tensor(t, ldtype):
+    """A LLAISYS_DEVICE_CPU tensor holding a copy of torch tensor t (any device)."""
+    import llaisys_amd as L
+
+    t = t.detach().contiguous().cpu()
+    lt = L.Tensor(tuple(t.shape), dtype=ldtype, device=L.DeviceType.CPU)
+    if t.numel():
+        L.RuntimeAPI(L.DeviceType.CPU).memcpy_sync(lt.data_ptr(), t.data_ptr(), t.numel() * t.element_size(),
+                                                   L.MemcpyKind.H2H)
+    return lt
+
+
+def host_copy_of(lt):
+    """A LLAISYS_DEVICE_CPU tensor with the contents of device tensor lt."""
+    import llaisys_amd as L
+
+    h = L.Tensor(lt.shape(), dtype=lt.dtype(), device=L.DeviceType.CPU)
+    n = 1
+    for d in lt.shape():
+        n *= d
+    esz = {L.DataType.BF16: 2, L.DataType.F16: 2, L.DataType.F32: 4, L.DataType.I32: 4, L.DataType.I64: 8}[lt.dtype()]
+    if n:
+        L.RuntimeAPI(L.DeviceType.AMD).memcpy_sync(h.data_ptr(), lt.data_ptr(), n * esz, L.MemcpyKind.D2H)
+    return h
+
+
+def time_host(fn, budget_s=2.0, warmup=10, repeat=100):
+    """The reference harness's pattern (test/test_utils.py:163-183): warm-up
+    calls, then up to `repeat` timed calls (fewer if budget_s runs out);
+    seconds per call."""
+    for _ in range(warmup):
+        fn()
+    n, t0 = 0, time.perf_counter()
+    while n < repeat and (n == 0 or time.perf_counter() - t0 < budget_s):
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
 def cpu_baseline_decode(inst, budget_s):
     """CPU legs of the config-3 workload, on a prefix of its batch sized so one
     pass takes >= 1 s: the C oracle (oracle/oracle.c, the restatement of the
@@ -414,8 +453,11 @@ def run_decode(args):
             "config2_append_gather": {"GB/s": ag["value"], "frac_of_hbm_peak": ag["roofline"]["frac"],
                                       "kernel_ms": ag["kernel_ms"], "entry_point": ag["config"]["entry_point"],
                                       "same_bytes_device_copy_ms": ag["same_bytes_device_copy"]["kernel_ms"],
+                                      "cpu_host_path_ms": (ag["cpu_host_path"] or {}).get("ms"),
                                       "two_calls_kernel_ms": (ag["two_calls"] or {}).get("kernel_ms")},
-            "config4_mixed_prefill_decode": {"TFLOP/s": mx["value"], "kernel_ms": mx["kernel_ms"]},
+            "config4_mixed_prefill_decode": {"TFLOP/s": mx["value"], "kernel_ms": mx["kernel_ms"],
+                                             "frac_of_mfma_peak": mx["roofline"]["frac"],
+                                             "cpu_host_path_ms": (mx["cpu_host_path"] or {}).get("ms")},
         }
     return line
 
@@ -437,6 +479,15 @@ def run_mixed(args):
     # Causal (query, key) pairs: prefill chunk queries see prior + i + 1 keys; decode queries see ctx keys.
     pairs = sum(int(p) * 512 + 512 * 513 // 2 for p in priors) + int(dec.sum())
     flops = pairs * 12 * 128 * 4
+    host = None
+    if not getattr(args, "no_cpu", False):
+        i0 = insts[0]
+        hq, hk, hv, ho, ht, hc, hcu = (host_copy_of(t) for t in (i0.q, i0.k_pool, i0.v_pool, i0.out, i0.table,
+                                                                  i0.ctx_t, i0.cu_q))
+        per, reps = time_host(lambda: L.Ops.paged_attention_varlen(ho, hq, hk, hv, ht, hcu, hc, SCALE),
+                              budget_s=5.0, warmup=1, repeat=10)
+        host = {"ms": round(per * 1e3, 2), "GFLOP/s": round(flops / per / 1e9, 1), "threads": host_cpus()[0],
+                "reps": reps, "what": "llaisysPagedAttentionVarlen on LLAISYS_DEVICE_CPU tensors, same inputs"}
     return {
         "metric": "mixed chunked-prefill + decode paged attention TFLOP/s, 1 GPU",
         "value": round(flops / (kern_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
@@ -444,6 +495,7 @@ def run_mixed(args):
         "kernel_ms": round(kern_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "BASELINE config 4: 4x512 prefill chunks over priors {0,1024,2048,4096} + 60 decode"},
+        "cpu_host_path": host,
         "roofline": {"bound": "mfma", "achieved": round(flops / (kern_ms * 1e-3) / 1e12, 3), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(flops / (kern_ms * 1e-3) / 1e12 / 2500.0, 4), "traffic": None},
     }
@@ -625,8 +677,9 @@ def run_append_gather(args):
     from utils import to_llaisys
 
     kp, vp = to_llaisys(pool_k), to_llaisys(pool_v)
-    kn = to_llaisys(torch.randn((B, 2, 128), device="cuda").to(torch.bfloat16))
-    vn = to_llaisys(torch.randn((B, 2, 128), device="cuda").to(torch.bfloat16))
+    kn_t = torch.randn((B, 2, 128), device="cuda").to(torch.bfloat16)
+    vn_t = torch.randn((B, 2, 128), device="cuda").to(torch.bfloat16)
+    kn, vn = to_llaisys(kn_t), to_llaisys(vn_t)
     tab = to_llaisys(torch.from_numpy(table))
     ctx = to_llaisys(torch.from_numpy(lens))
     cu = np.concatenate([[0], np.cumsum(lens + 1)]).astype(np.int32)
@@ -653,6 +706,18 @@ def run_append_gather(args):
         two_warm_ms, _ = time_steps(step_two_calls, stream, args.steps, args.warmup)
     nbytes = 2 * T * 1024 + 2 * B * 1024
     gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    host = None
+    if not getattr(args, "no_cpu", False):
+        # The library's host path on the same data (CPU tensors, page format).
+        hk, hv = host_tensor(pool_k, L.DataType.BF16), host_tensor(pool_v, L.DataType.BF16)
+        hargs = [host_tensor(torch.zeros((T, 2, 128), dtype=torch.bfloat16), L.DataType.BF16) for _ in range(2)]
+        hkn, hvn = host_tensor(kn_t, L.DataType.BF16), host_tensor(vn_t, L.DataType.BF16)
+        htab, hctx = host_tensor(torch.from_numpy(table), L.DataType.I32), host_tensor(torch.from_numpy(lens), L.DataType.I32)
+        hcu = host_tensor(torch.from_numpy(cu), L.DataType.I32)
+        per, reps = time_host(lambda: L.Ops.paged_kv_append_gather(hargs[0], hargs[1], hk, hv, hkn, hvn, htab, hctx, hcu))
+        host = {"ms": round(per * 1e3, 4), "GB/s": round((2 * T * 1024 + 2 * B * 1024) / per / 1e9, 2),
+                "threads": host_cpus()[0], "reps": reps,
+                "what": "llaisysPagedKVAppendGather on LLAISYS_DEVICE_CPU tensors, same inputs"}
     # The practical ceiling at this size: torch's contiguous device copy of the
     # same bytes (half read, half written), timed the same two ways.
     src = torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")
@@ -675,6 +740,7 @@ def run_append_gather(args):
             "entry_points": "llaisysPagedKVAppend then llaisysPagedKVGather",
             "kernel_ms": round(two_ms, 5), "GB/s": round(nbytes / (two_ms * 1e-3) / 1e9, 2),
             "mall_resident_kernel_ms": round(two_warm_ms, 5)},
+        "cpu_host_path": host,
         "same_bytes_device_copy": {
             "what": "torch copy_ of nbytes/2 contiguous bytes (reads + writes = the step's bytes)",
             "kernel_ms": round(copy_ms, 5), "mall_resident_kernel_ms": round(copy_warm_ms, 5),
