@@ -232,6 +232,177 @@ void launchByM(GemmArgs a, hipStream_t s) {
     }
 }
 
+
+// ---- Split-K variant for long K (the down projection, K = 8960).
+//
+// With K long and N short the 16-row blocks are too few to fill the chip, so
+// K splits over workgroups instead: workgroup (t, s) computes the partial
+// C[128 rows of N, all M] over k tiles [s KT / S, (s + 1) KT / S) into fp32
+// partials part[s][m][n], and a reduce kernel sums the S partials in order
+// (deterministic), adds the old Y when accumulating and rounds once to bf16.
+//  * Each of the 4 waves (one per SIMD) owns 2 of the 8 row blocks of the
+//    tile and streams their packed W tiles through a register ring of kRing
+//    k steps (2 tiles each), issued first.
+//  * X for the workgroup's k range and all M rows is then copied into LDS by
+//    global_load_lds, one instruction per row (no registers, no index
+//    arithmetic): a row is 64 chunks of 16 B (up to 16 k tiles), chunk c of
+//    row m holding k chunk c ^ (m % 16), so the B-operand reads of one k step
+//    (16 rows, one chunk column) hit 16 different bank groups.
+//  * Per k step a wave reads the next step's MB B operands from LDS, issues
+//    2 MB MFMAs on the current ones, then refills the ring slot.
+constexpr int kSplitTileRows = 128; // rows of W (N) per workgroup
+constexpr int kRing = 8;            // k steps of W in flight per wave
+constexpr int kSplitMaxTiles = 16;  // k tiles per split: one 1 KiB LDS row of X
+
+struct SplitKArgs {
+    const uint16_t *x;
+    const u32x4 *wp;
+    float *part;
+    int M, N, K, KT, S;
+};
+
+template <int MB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) splitKGemmKernel(SplitKArgs a) {
+    extern __shared__ u32x4 xs[]; // [16 MB][64] chunks, swizzled
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int t = int(blockIdx.x) / a.S, s = int(blockIdx.x) % a.S;
+    const int kt0 = s * a.KT / a.S, nk = (s + 1) * a.KT / a.S - kt0;
+
+    // W ring: row blocks nb0 and nb0 + 1, k step j in slot j % kRing. Past
+    // the range a slot re-reads the last step (an L2 hit), so every step
+    // issues the same loads.
+    const int nb0 = (kSplitTileRows / 16) * t + 2 * wave;
+    const u32x4 *w0 = a.wp + (size_t(nb0) * a.KT + kt0) * 64 + lane;
+    const u32x4 *w1 = w0 + size_t(a.KT) * 64;
+    u32x4 r0[kRing], r1[kRing];
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) {
+        const int jj = min(j, nk - 1);
+        r0[j] = __builtin_nontemporal_load(w0 + size_t(jj) * 64);
+        r1[j] = __builtin_nontemporal_load(w1 + size_t(jj) * 64);
+    }
+    // X rows (clamped to M - 1: their columns are computed and dropped);
+    // wave w copies rows w, w + 4, ... Lanes past the range fetch the row's
+    // first chunk into an unused slot.
+    for (int row = wave; row < 16 * MB; row += 4) {
+        const int kc = lane ^ (row & 15); // lane l fills chunk l of the row
+        const int m = min(row, a.M - 1);
+        const int k = 32 * kt0 + 8 * (kc < 4 * nk ? kc : 0);
+        __builtin_amdgcn_global_load_lds((const void *)(a.x + size_t(m) * a.K + k),
+                                         (__attribute__((address_space(3))) void *)(xs + 64 * row), 16, 0, 0);
+    }
+    // The compiler does not track these copies: wait for every load of this
+    // wave (the ring's too, needed first anyway), then the barrier covers
+    // every wave's copies.
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+    f32x4 acc[2][MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[0][mb] = acc[1][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const u32x4 *xrow = xs + (lane & 15) * 64;
+    auto readX = [&](int j, u32x4 (&xv)[MB]) {
+        const int c = (4 * j + (lane >> 4)) ^ (lane & 15);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) xv[mb] = xrow[16 * 64 * mb + c];
+    };
+    // Step j: read step j + 1's B operands, the MFMAs of step j on ring slot
+    // r, then the slot's refill with step j + kRing into the same registers
+    // (pinned in this order: a refill issued before the MFMAs read the slot
+    // would need a second register set, and the loop latch would then copy
+    // in-flight load results, draining the ring).
+    auto stepK = [&](int j, u32x4 &s0, u32x4 &s1, const u32x4 (&xc)[MB], u32x4 (&xn)[MB]) {
+        readX(min(j + 1, nk - 1), xn);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            acc[0][mb] = mfma(s0, xc[mb], acc[0][mb]);
+            acc[1][mb] = mfma(s1, xc[mb], acc[1][mb]);
+        }
+        const int jn = min(j + kRing, nk - 1);
+        s0 = __builtin_nontemporal_load(w0 + size_t(jn) * 64);
+        s1 = __builtin_nontemporal_load(w1 + size_t(jn) * 64);
+        __builtin_amdgcn_sched_group_barrier(0x100, MB, 0);     // next step's B operands
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * MB, 0); // the MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);      // then the refill
+    };
+    static_assert(kRing % 2 == 0, "B-operand buffers alternate by slot parity");
+    u32x4 xa[MB], xb[MB];
+    readX(0, xa);
+    // Whole ring passes with no guard, then the remainder.
+    const int nfull = nk - nk % kRing;
+    for (int j0 = 0; j0 < nfull; j0 += kRing) {
+#pragma unroll
+        for (int r = 0; r < kRing; r += 2) {
+            stepK(j0 + r, r0[r], r1[r], xa, xb);
+            stepK(j0 + r + 1, r0[r + 1], r1[r + 1], xb, xa);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRing; r += 2) {
+        if (nfull + r < nk) stepK(nfull + r, r0[r], r1[r], xa, xb);
+        if (nfull + r + 1 < nk) stepK(nfull + r + 1, r0[r + 1], r1[r + 1], xb, xa);
+    }
+    // Lane holds C rows n0 + 0..3 (of row block nb0 + h) for column m.
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int n0 = 16 * (nb0 + h) + 4 * (lane >> 4);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+            const int m = 16 * mb + (lane & 15);
+            if (m < a.M) *reinterpret_cast<f32x4 *>(a.part + (size_t(s) * a.M + m) * a.N + n0) = acc[h][mb];
+        }
+    }
+}
+
+// Y[m, n .. n + 3] = (old Y +) sum over s of part[s][m][n .. n + 3], rounded
+// once. Loads of 16 partials are in flight at a time; the sum runs in split
+// order.
+constexpr int kReduceBatch = 16;
+
+__global__ void splitKReduceKernel(uint16_t *y, const float *part, int M, int N, int S, int accumulate) {
+    const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int n4 = N / 4;
+    if (idx >= size_t(M) * n4) return;
+    const int m = int(idx / n4), n = 4 * int(idx % n4);
+    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+    if (accumulate) {
+        const uint2 old = *reinterpret_cast<const uint2 *>(y + size_t(m) * N + n);
+        sum = f32x4{__uint_as_float(old.x << 16), __uint_as_float(old.x & 0xffff0000u), __uint_as_float(old.y << 16),
+                    __uint_as_float(old.y & 0xffff0000u)};
+    }
+    const size_t stride = size_t(M) * N;
+    const float *p = part + size_t(m) * N + n;
+    for (int s0 = 0; s0 < S; s0 += kReduceBatch) {
+        f32x4 v[kReduceBatch];
+#pragma unroll
+        for (int i = 0; i < kReduceBatch; ++i)
+            v[i] = *reinterpret_cast<const f32x4 *>(p + size_t(min(s0 + i, S - 1)) * stride);
+#pragma unroll
+        for (int i = 0; i < kReduceBatch; ++i)
+            if (s0 + i < S) sum += v[i];
+    }
+    auto pack = [](float a0, float a1) {
+        const __bf16 b0 = (__bf16)a0, b1 = (__bf16)a1;
+        return uint32_t(__builtin_bit_cast(uint16_t, b0)) | (uint32_t(__builtin_bit_cast(uint16_t, b1)) << 16);
+    };
+    *reinterpret_cast<uint2 *>(y + size_t(m) * N + n) = make_uint2(pack(sum[0], sum[1]), pack(sum[2], sum[3]));
+}
+
+// About one workgroup per CU, at most kSplitMaxTiles k tiles per split (one
+// LDS row of X). (Splitting further for small M, so that a workgroup's whole
+// W range is in flight at once, measured slower: more partials to reduce.)
+int splitsFor(int M, int N, int K) {
+    (void)M;
+    const int tiles = N / kSplitTileRows, KT = K / 32;
+    const int for_cus = (computeUnitsOf() + tiles / 2) / tiles;
+    const int for_lds = (KT + kSplitMaxTiles - 1) / kSplitMaxTiles;
+    return std::max(1, std::min(KT, std::max(for_cus, for_lds)));
+}
+
+template <int MB> void launchSplitK(const SplitKArgs &a, hipStream_t st) {
+    const size_t lds = size_t(16) * MB * 64 * sizeof(u32x4);
+    hipLaunchKernelGGL((splitKGemmKernel<MB>), dim3((a.N / kSplitTileRows) * a.S), dim3(256), lds, st, a);
+}
 } // namespace
 
 bool decodeGemmSupported(int M, int N, int K) {
@@ -255,6 +426,36 @@ void decodeGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, i
                   "decodeGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
     GemmArgs a{y, x, reinterpret_cast<const u32x4 *>(packed), M, N, K, N / 16, accumulate ? 1 : 0, 1};
     launchByM(a, static_cast<hipStream_t>(stream));
+    HIP_CHECK(hipGetLastError());
+}
+
+bool splitKGemmSupported(int M, int N, int K) {
+    return M >= 1 && M <= kDecodeGemmMaxM && N >= kSplitTileRows && N % kSplitTileRows == 0 && K % 32 == 0 &&
+           K > kDecodeGemmK && K <= kSplitKMaxK;
+}
+
+size_t splitKWorkspaceBytes(int M, int N, int K) {
+    return splitKGemmSupported(M, N, K) ? size_t(splitsFor(M, N, K)) * M * N * sizeof(float) : 0;
+}
+
+void splitKGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
+                float *partials, void *stream) {
+    LLAISYS_CHECK(splitKGemmSupported(M, N, K), "splitKGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
+    auto st = static_cast<hipStream_t>(stream);
+    SplitKArgs a{x, reinterpret_cast<const u32x4 *>(packed), partials, M, N, K, K / 32, splitsFor(M, N, K)};
+    switch ((M + 15) / 16) {
+    case 1: launchSplitK<1>(a, st); break;
+    case 2: launchSplitK<2>(a, st); break;
+    case 3: launchSplitK<3>(a, st); break;
+    case 4: launchSplitK<4>(a, st); break;
+    case 5: launchSplitK<5>(a, st); break;
+    case 6: launchSplitK<6>(a, st); break;
+    case 7: launchSplitK<7>(a, st); break;
+    default: launchSplitK<8>(a, st); break;
+    }
+    const size_t threads = size_t(M) * (N / 4);
+    hipLaunchKernelGGL(splitKReduceKernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, st, y, partials, M, N,
+                       a.S, accumulate ? 1 : 0);
     HIP_CHECK(hipGetLastError());
 }
 

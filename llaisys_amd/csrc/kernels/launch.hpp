@@ -123,6 +123,16 @@ size_t packedWeightElems(int N, int K);
 void packWeight(uint16_t *packed, const uint16_t *w, const uint16_t *fold_g, int N, int K, void *stream);
 void decodeGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
                 void *stream);
+// The same product for long K (kDecodeGemmK < K <= kSplitKMaxK, K % 32 == 0,
+// N % 128 == 0, M <= kDecodeGemmMaxM), same packed W: K splits over
+// workgroups into fp32 partials (splitKWorkspaceBytes of device memory),
+// summed in a fixed order by a second kernel that also adds the old Y
+// (accumulate) and rounds once.
+constexpr int kSplitKMaxK = 16384;
+bool splitKGemmSupported(int M, int N, int K);
+size_t splitKWorkspaceBytes(int M, int N, int K);
+void splitKGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
+                float *partials, void *stream);
 
 // ---- Qwen2 step glue (qwen2_step.hip), bf16
 // qkv [T, (nh + 2 nkvh) d] + bias -> q [T, nh, d] rotated by position, and k

@@ -42,9 +42,10 @@ struct Qwen2LayerWeights {
     tensor_t qkv_wf, gate_up_wf;
     uint64_t folded_from[4] = {~0ull, ~0ull, ~0ull, ~0ull};
     // The decode GEMM's packed copies (MFMA operand order) of the folded QKV
-    // and gate-up weights and of o_w; null when the shapes do not qualify.
-    tensor_t qkv_wfp, gate_up_wfp, o_wp;
-    uint64_t o_packed_from = ~0ull;
+    // and gate-up weights, of o_w and of down_w (split-K kernel); null when
+    // the shapes do not qualify.
+    tensor_t qkv_wfp, gate_up_wfp, o_wp, down_wp;
+    uint64_t o_packed_from = ~0ull, down_packed_from = ~0ull;
 };
 
 class Qwen2Model {

@@ -148,14 +148,23 @@ void linearPacked(const tensor_t &out, const tensor_t &in, const tensor_t &packe
     if (bias) LLAISYS_CHECK(bias->ndim() == 1 && int(bias->shape()[0]) == N, op << ": bias must be [" << N << "]");
     for (auto *t : {&out, &in, &packed, &bias})
         if (*t) LLAISYS_CHECK((*t)->dtype() == LLAISYS_DTYPE_BF16, op << ": bf16 only");
-    LLAISYS_CHECK(K::decodeGemmSupported(M, N, Kd), op << ": needs 1 <= M <= " << K::kDecodeGemmMaxM << ", K == "
-                                                       << K::kDecodeGemmK << ", N % 16 == 0 (M=" << M << ", N=" << N
-                                                       << ", K=" << Kd << "); use llaisysLinear");
+    const bool split = !K::decodeGemmSupported(M, N, Kd) && K::splitKGemmSupported(M, N, Kd);
+    LLAISYS_CHECK(K::decodeGemmSupported(M, N, Kd) || split,
+                  op << ": needs 1 <= M <= " << K::kDecodeGemmMaxM << " and either K == " << K::kDecodeGemmK
+                     << ", N % 16 == 0, or " << K::kDecodeGemmK << " < K <= " << K::kSplitKMaxK
+                     << ", K % 32 == 0, N % 128 == 0 (M=" << M << ", N=" << N << ", K=" << Kd
+                     << "); use llaisysLinear");
     LLAISYS_CHECK(!onHost(op, {&out, &in, &packed, &bias}), op << ": AMD device tensors only");
     auto *y = reinterpret_cast<uint16_t *>(out->data());
+    const auto *x = reinterpret_cast<const uint16_t *>(in->data());
+    const auto *w = reinterpret_cast<const uint16_t *>(packed->data());
     if (bias) K::fillRows(y, bias->data(), K::ElemType::BF16, size_t(M), size_t(N), stream());
-    K::decodeGemm(y, reinterpret_cast<const uint16_t *>(in->data()), reinterpret_cast<const uint16_t *>(packed->data()),
-                  M, N, Kd, bias != nullptr, stream());
+    if (split) {
+        auto *part = static_cast<float *>(core::context().runtime().scratch(K::splitKWorkspaceBytes(M, N, Kd)));
+        K::splitKGemm(y, x, w, M, N, Kd, bias != nullptr, part, stream());
+    } else {
+        K::decodeGemm(y, x, w, M, N, Kd, bias != nullptr, stream());
+    }
 }
 
 void rearrange(const tensor_t &out, const tensor_t &in) {

@@ -217,9 +217,46 @@ def test_linear_packed_decode_gemm(M, N, use_bias):
     assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
 
 
+SPLIT_K = [(1, 1536, 8960), (16, 1536, 8960), (37, 128, 4096), (100, 1536, 8960), (128, 1536, 8960),
+           (128, 256, 16384)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_K, ids=[f"{m}x{n}x{k}" for m, n, k in SPLIT_K])
+@pytest.mark.parametrize("use_bias", [True, False])
+def test_linear_packed_split_k(M, N, K, use_bias):
+    # Long K (the down projection's 8960): llaisysLinearPacked takes the
+    # split-K kernel (fp32 partials summed in a fixed order, one rounding),
+    # to the same bound as above. Twice in a row: the second call must not
+    # depend on partials the first left behind.
+    x, w = rnd((M, K), torch.bfloat16, 0.5, seed=M + 7), rnd((N, K), torch.bfloat16, 0.05, seed=N + K)
+    b = rnd((N,), torch.bfloat16, seed=23) if use_bias else None
+    packed = to_llaisys(torch.zeros(N, K, dtype=torch.bfloat16, device=DEV))
+    L.Ops.linear_pack_weight(packed, to_llaisys(w))
+    ref = x.double() @ w.double().T
+    if use_bias:
+        ref += b.double()
+    bound = ref.abs() * 2.0 ** -8 + 1e-6 * (x.double().abs() @ w.double().abs().T) * K ** 0.5 + 1e-30
+    first = None
+    for _ in range(2):
+        out = to_llaisys(torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV))
+        L.Ops.linear_packed(out, to_llaisys(x), packed, to_llaisys(b) if use_bias else None)
+        got = to_torch(out).double()
+        assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
+        if first is None:
+            first = got.clone()
+        else:
+            assert torch.equal(first, got), "split-K result differs between identical calls"
+
+
 def test_linear_packed_refuses_unsupported_shapes():
     x = to_llaisys(torch.zeros(129, 1536, dtype=torch.bfloat16, device=DEV))
     w = to_llaisys(torch.zeros(32, 1536, dtype=torch.bfloat16, device=DEV))
     out = to_llaisys(torch.zeros(129, 32, dtype=torch.bfloat16, device=DEV))
     with pytest.raises(L.LlaisysError, match="M <= 128"):
+        L.Ops.linear_packed(out, x, w)
+    # Long K needs N % 128 == 0.
+    x = to_llaisys(torch.zeros(4, 8960, dtype=torch.bfloat16, device=DEV))
+    w = to_llaisys(torch.zeros(48, 8960, dtype=torch.bfloat16, device=DEV))
+    out = to_llaisys(torch.zeros(4, 48, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(L.LlaisysError, match="N % 128 == 0"):
         L.Ops.linear_packed(out, x, w)
