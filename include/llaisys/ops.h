@@ -54,8 +54,10 @@ __C {
     /* New; no counterpart in the reference. out = in . W^T + bias (bias may be
      * NULL) as llaisysLinear computes it (fp32 accumulation, one rounding),
      * with W given packed by llaisysLinearPackWeight; for decode-sized batches:
-     * in [M, K], out [M, N] BF16 on the AMD device, 1 <= M <= 128, K == 1536,
-     * N % 16 == 0 (other shapes: llaisysLinear). */
+     * in [M, K], out [M, N] BF16 on the AMD device, 1 <= M <= 128, and
+     * either K == 1536, N % 16 == 0, or 1536 < K <= 16384, K % 32 == 0,
+     * N % 128 == 0 (split over K into fp32 partials in the runtime's device
+     * workspace, summed in a fixed order); other shapes: llaisysLinear. */
     __export void llaisysLinearPacked(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t packed,
                                       llaisysTensor_t bias);
     /* ops.h:11: copy between equal shapes with any strides (README.md:286-292). */
