@@ -54,6 +54,14 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
                  int nkvh, int max_pages, int num_blocks, float scale, const DecodePlan &plan, float *records,
                  int *err, int *slot_headers, void *slot_records, void *stream);
 
+// The same attention (cu_q null: query row b is sequence b) with one
+// workgroup of 4 waves per (sequence, kv head), merging in LDS: no records,
+// one launch. For batches whose contexts are of similar length (the waves
+// of a long sequence's workgroup would otherwise finish last).
+void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                      const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                      int num_blocks, float scale, int *err, void *stream);
+
 // The decode above with its split records in a fixed per-GPU device array
 // (noAllocScratchBytes() bytes) instead of runtime workspace: no device
 // allocation per call. noAllocInit() looks the array's address up for the

@@ -466,6 +466,119 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
     for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, orow, i, grp, o[i] * inv);
 }
 
+
+// Decode attention with one workgroup per (sequence, kv head) unit: its
+// kUnitWaves waves split the unit's page pairs evenly, stream them through a
+// register ring into the same MFMA step as the stream-K kernel, and merge
+// their (O, m, l) in LDS; wave 0 writes the normalised output. No records and
+// no second launch, no length scan: each workgroup reads its own length.
+// Balanced only when the units have similar lengths, which the caller
+// decides (a decode batch of similar contexts); query row b is sequence b.
+constexpr int kUnitWaves = 4;
+
+template <bool OUT_F32, int NSTAGE>
+__global__ void __launch_bounds__(64 * kUnitWaves)
+    __attribute__((amdgpu_waves_per_eu(NSTAGE == 2 ? 2 : 1, NSTAGE == 2 ? 2 : 1))) decodeUnitKernel(DecodeArgs a) {
+    __shared__ f32x4 part_o[kUnitWaves - 1][8][64];
+    __shared__ float part_ml[kUnitWaves - 1][2][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15;
+    const int grp = lane >> 4;
+    const int G = a.G;
+    const int u = blockIdx.x;
+    const int b = u / a.nkvh;
+    const int h = u - b * a.nkvh;
+    int c = a.ctx[b];
+    if (c < 1 || c > a.max_pages * 16) { // invalid length: zero output, error flag
+        if (threadIdx.x == 0) atomicOr(a.err, kErrTooLong);
+        c = 0;
+    }
+    c = __builtin_amdgcn_readfirstlane(c);
+    const int np = (c + 15) >> 4;
+    const int npr = (np + 1) >> 1;
+    const int p0 = wave * npr / kUnitWaves, p1 = (wave + 1) * npr / kUnitWaves;
+    Acc acc;
+    acc.reset();
+    bool bad_block = false;
+    if (p1 > p0) {
+        u32x4 qop[4];
+        const uint16_t *qrow = a.q + (size_t(b) * a.nh + h * G + min(n, G - 1)) * kHeadDim + grp * 8;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            qop[t] = *reinterpret_cast<const u32x4 *>(qrow + 32 * t);
+            qop[t] = n < G ? qop[t] : u32x4{0, 0, 0, 0};
+        }
+        const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
+        const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
+        const int32_t *row = a.table + size_t(b) * a.max_pages;
+        // Windows of up to 64 pairs: lane i holds the block ids of pair
+        // base + i. Loads are never conditional: past the window's end they
+        // re-read its last pair (an L2 hit).
+        for (int base = p0; base < p1; base += kPairsPerWave) {
+            const int cnt = min(kPairsPerWave, p1 - base);
+            int bidA, bidB;
+            {
+                const int pa = 2 * (base + min(lane, cnt - 1));
+                bidA = row[pa];
+                bidB = row[min(pa + 1, np - 1)];
+            }
+            PagePair ring[NSTAGE];
+            auto issue = [&](int st, int k) {
+                const int kk = min(k, cnt - 1);
+                int bA = __builtin_amdgcn_readlane(bidA, kk);
+                int bB = __builtin_amdgcn_readlane(bidB, kk);
+                const bool bad = unsigned(bA) >= unsigned(a.num_blocks) || unsigned(bB) >= unsigned(a.num_blocks);
+                bad_block |= bad;
+                bA = bad ? 0 : bA;
+                bB = bad ? 0 : bB;
+                loadPair(ring[st], kp, vp, (size_t(bA) * a.nkvh + h) * 256, (size_t(bB) * a.nkvh + h) * 256);
+            };
+#pragma unroll
+            for (int st = 0; st < NSTAGE; ++st) issue(st, st);
+            for (int k0 = 0; k0 < cnt; k0 += NSTAGE) {
+#pragma unroll
+                for (int st = 0; st < NSTAGE; ++st) {
+                    const int k = k0 + st;
+                    if (k < cnt) {
+                        const int j = base + k;
+                        consumePair<OUT_F32>(acc, ring[st], qop, 32 * j, c - 1, c, 2 * j + 1 < np, grp, a.scale_log2);
+                    }
+                    issue(st, k + NSTAGE);
+                }
+            }
+        }
+    }
+    if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
+    float lt = acc.l + __shfl_xor(acc.l, 16);
+    lt += __shfl_xor(lt, 32);
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part_o[wave - 1][i][lane] = acc.o[i];
+        part_ml[wave - 1][0][lane] = acc.m;
+        part_ml[wave - 1][1][lane] = lt;
+    }
+    __syncthreads();
+    if (wave > 0 || n >= G) return;
+    float M = acc.m, L = lt;
+#pragma unroll
+    for (int v = 0; v < kUnitWaves - 1; ++v) {
+        const float mv = part_ml[v][0][lane];
+        if (mv == -INFINITY) continue;
+        const float Mn = fmaxf(M, mv);
+        const float sa = exp2Fast(M - Mn);
+        const float sb = exp2Fast(mv - Mn);
+        L = L * sa + part_ml[v][1][lane] * sb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc.o[i] = acc.o[i] * sa + part_o[v][i][lane] * sb;
+        M = Mn;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f; // no keys (invalid length): zeros
+    const size_t orow = (size_t(b) * a.nh + h * G + n) * kHeadDim;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, orow, i, grp, acc.o[i] * inv);
+}
+
 int envInt(const char *name, int fallback) {
     const char *v = std::getenv(name);
     return (v && *v) ? std::atoi(v) : fallback;
@@ -609,6 +722,43 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
         else
             hipLaunchKernelGGL((decodeKernel<false, 2>), grid, block, lds, s, a);
         hipLaunchKernelGGL((decodeCombineKernel<false>), comb, comb_block, lds, s, a);
+    }
+    HIP_CHECK(hipGetLastError());
+}
+
+void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                      const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                      int num_blocks, float scale, int *err, void *stream) {
+    if (B == 0) return;
+    DecodeArgs a{};
+    a.q = q;
+    a.out = out;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.table = block_table;
+    a.ctx = ctx_len;
+    a.err = err;
+    a.B = B;
+    a.T = B;
+    a.nh = nh;
+    a.nkvh = nkvh;
+    a.G = nh / nkvh;
+    a.max_pages = max_pages;
+    a.num_blocks = num_blocks;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    static const int stages = envInt("LLAISYS_UNIT_STAGES", 2) >= 3 ? 3 : 2;
+    auto s = static_cast<hipStream_t>(stream);
+    const dim3 grid(unsigned(B) * unsigned(nkvh)), block(64 * kUnitWaves);
+    if (out_f32) {
+        if (stages == 3)
+            hipLaunchKernelGGL((decodeUnitKernel<true, 3>), grid, block, 0, s, a);
+        else
+            hipLaunchKernelGGL((decodeUnitKernel<true, 2>), grid, block, 0, s, a);
+    } else {
+        if (stages == 3)
+            hipLaunchKernelGGL((decodeUnitKernel<false, 3>), grid, block, 0, s, a);
+        else
+            hipLaunchKernelGGL((decodeUnitKernel<false, 2>), grid, block, 0, s, a);
     }
     HIP_CHECK(hipGetLastError());
 }

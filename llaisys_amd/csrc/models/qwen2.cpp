@@ -67,6 +67,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     if (const char *e = std::getenv("LLAISYS_QWEN2_GRAPHS")) use_graphs_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_QWEN2_FOLD_NORM")) fold_norm_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_DECODE_GEMM")) decode_gemm_ = e[0] != '0';
+    if (const char *e = std::getenv("LLAISYS_DECODE_UNITS")) unit_decode_allowed_ = e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -143,14 +144,27 @@ Qwen2Model::DecodeGraph Qwen2Model::capture(const std::function<void()> &work, s
     g.width = width;
     g.gen = ws_gen_;
     g.ws = rt.workspaceGeneration();
+    g.unit = unit_decode_;
     return g;
+}
+
+// Decode steps (B > 0) of at least kUnitDecodeMinUnits units whose lengths
+// stay within 2x: every unit's workgroup then finishes at about the same
+// time, and the one-launch kernel saves the stream-K kernel's length scan,
+// split records and combine launch. Other batches (mixed lengths, few
+// sequences, prefill) keep the stream-K kernel.
+static constexpr size_t kUnitDecodeMinUnits = 128;
+
+void Qwen2Model::chooseDecodeAttention(size_t B, int32_t min_ctx, int32_t max_ctx) {
+    unit_decode_ = unit_decode_allowed_ && B > 0 && B * cfg_.nkvh >= kUnitDecodeMinUnits && min_ctx >= 1 &&
+                   max_ctx <= 2 * min_ctx;
 }
 
 void Qwen2Model::decodeGraph(size_t B, size_t width) {
     auto &rt = core::context().runtime();
     auto s = static_cast<hipStream_t>(rt.stream());
     DecodeGraph &g = graphs_[B];
-    if (g.exec && g.width == width && g.gen == ws_gen_ && g.ws == rt.workspaceGeneration()) {
+    if (g.exec && g.width == width && g.gen == ws_gen_ && g.ws == rt.workspaceGeneration() && g.unit == unit_decode_) {
         HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(g.exec), s));
         return;
     }
@@ -274,6 +288,7 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
         cu[i + 1] = cu[i] + int32_t(ntokens[i]);
     }
     std::copy(cow.begin(), cow.end(), cu + B + 1);
+    chooseDecodeAttention(T == B ? B : 0, *std::min_element(ca, ca + B), *std::max_element(ca, ca + B));
     // int64 staging: tokens | last row of each sequence
     int64_t *h64 = reinterpret_cast<int64_t *>(host64_->memory());
     std::memcpy(h64, tokens, T * sizeof(int64_t));
@@ -354,6 +369,10 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     }
     h32[o_cu + B] = int32_t(B);
     h32[o_cnt] = 0;
+    // Every step of the call runs one captured graph: choose for the range
+    // of lengths the call spans.
+    chooseDecodeAttention(B, *std::min_element(before.begin(), before.end()) + 1,
+                          *std::max_element(before.begin(), before.end()) + int32_t(nsteps));
     std::copy(cow.begin(), cow.end(), h32 + o_cnt + 1);
     int64_t *h64 = reinterpret_cast<int64_t *>(host64_->memory());
     for (size_t i = 0; i < B; ++i) {
@@ -388,7 +407,8 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     size_t done = 0;
     if (use_graphs_) {
         DecodeGraph &g = multi_graphs_[B];
-        const bool valid = g.exec && g.width == width && g.gen == ws_gen_ && g.ws == rt.workspaceGeneration();
+        const bool valid = g.exec && g.width == width && g.gen == ws_gen_ && g.ws == rt.workspaceGeneration() &&
+                           g.unit == unit_decode_;
         if (!valid) {
             if (g.exec) HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(g.exec)));
             g.exec = nullptr;
@@ -485,7 +505,13 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
                          i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh), int(cfg_.nkvh),
                          int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), xr, hs,
                          cfg_.epsilon, s);
-        ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_, scale);
+        if (decode_only && unit_decode_)
+            K::pagedDecodeUnits(a3->data(), false, u16(q3), u16(k_pool_[l]), u16(v_pool_[l]), i32(table_),
+                                i32(ctx_after_), int(B), int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]),
+                                int(num_blocks_), scale, rt.errorWord(), s);
+        else
+            ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_,
+                                scale);
         project(x_, attn_, L.o_w, L.o_wp, M, hs, q, true, s);
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
         project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, fold ? L.gate_up_wfp : nullptr, M, 2 * di, hs,

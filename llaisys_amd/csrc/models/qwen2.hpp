@@ -128,10 +128,18 @@ private:
         size_t width = 0;     // block-table width it was captured with
         uint64_t gen = 0;     // workspace generation it was captured with
         uint64_t ws = 0; // runtime workspace generation it was captured with
+        bool unit = false; // captured with the one-workgroup-per-unit decode attention
     };
     DecodeGraph capture(const std::function<void()> &work, size_t width);
     bool use_graphs_ = true;
     bool fold_norm_ = true; // LLAISYS_QWEN2_FOLD_NORM=0: separate rms_norm launches instead
+    // Decode steps whose contexts are within 2x of each other, with at least
+    // kUnitDecodeMinUnits (sequence, kv head) units, run the decode attention
+    // with one workgroup per unit (no split records, one launch).
+    // LLAISYS_DECODE_UNITS=0 keeps the stream-K kernel for every step.
+    bool unit_decode_allowed_ = true;
+    bool unit_decode_ = false; // the choice for the step being built
+    void chooseDecodeAttention(size_t B, int32_t min_ctx, int32_t max_ctx);
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
     std::map<size_t, DecodeGraph> graphs_;       // one step (step())
     std::map<size_t, DecodeGraph> multi_graphs_; // advance + step + record (decode())

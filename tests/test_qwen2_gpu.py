@@ -123,6 +123,38 @@ def test_wide_decode_batches_match(nseq):
         check_token(nxt[r], ref, check_logits(logits[r], ref))
 
 
+@pytest.mark.parametrize("units", ["1", "0"])
+def test_decode_attention_one_workgroup_per_unit(monkeypatch, units):
+    # 70 sequences x 2 kv heads = 140 units of 300-590 context tokens: within
+    # 2x of each other, so decode steps take the one-workgroup-per-unit
+    # attention (LLAISYS_DECODE_UNITS=1) instead of the stream-K kernel (=0).
+    # Both against transformers; a multi-step decode call (one captured
+    # graph, lengths growing) against single steps.
+    monkeypatch.setenv("LLAISYS_DECODE_UNITS", units)
+    nseq = 70
+    model, hf = build("tiny", num_blocks=nseq * 40 + 8)
+    lens = [300 + (i * 37) % 291 for i in range(nseq)]
+    prompts = [prompt(n, model.meta.voc, 500 + i) for i, n in enumerate(lens)]
+    ids = [model.create_sequence()[0] for _ in prompts]
+    nxt = []
+    for s in range(0, nseq, 10):
+        nxt += model.step(ids[s:s + 10], prompts[s:s + 10])
+    hist = [p + [t] for p, t in zip(prompts, nxt)]
+    nxt = model.step(ids, [[h[-1]] for h in hist])
+    logits = to_torch(model.logits())
+    for r in range(0, nseq, 13):
+        ref = hf_logits(hf, hist[r])[-1]
+        check_token(nxt[r], ref, check_logits(logits[r], ref))
+    forks = [model.fork(i) for i in ids]
+    multi = model.decode(ids, nxt, 5)
+    single, cur = [], nxt
+    for _ in range(5):
+        cur = model.step(forks, [[t] for t in cur])
+        single.append(cur)
+    assert L.device_error_flags() == 0
+    assert np.array_equal(np.asarray(multi), np.asarray(single, np.int64))
+
+
 def test_infer_restarts_on_a_new_history_and_reuses_cached_blocks():
     model, hf = build("tiny")
     a = prompt(50, model.meta.voc, 2)
