@@ -746,20 +746,15 @@ void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t
     a.max_pages = max_pages;
     a.num_blocks = num_blocks;
     a.scale_log2 = scale * 1.4426950408889634f;
-    static const int stages = envInt("LLAISYS_UNIT_STAGES", 2) >= 3 ? 3 : 2;
+    // Two page pairs in flight per wave, two waves per SIMD: measured best
+    // in the config-5 step (3.37 ms; three in flight at one wave per SIMD:
+    // 3.47 ms; 8 waves per unit: 3.46 ms).
     auto s = static_cast<hipStream_t>(stream);
     const dim3 grid(unsigned(B) * unsigned(nkvh)), block(64 * kUnitWaves);
-    if (out_f32) {
-        if (stages == 3)
-            hipLaunchKernelGGL((decodeUnitKernel<true, 3>), grid, block, 0, s, a);
-        else
-            hipLaunchKernelGGL((decodeUnitKernel<true, 2>), grid, block, 0, s, a);
-    } else {
-        if (stages == 3)
-            hipLaunchKernelGGL((decodeUnitKernel<false, 3>), grid, block, 0, s, a);
-        else
-            hipLaunchKernelGGL((decodeUnitKernel<false, 2>), grid, block, 0, s, a);
-    }
+    if (out_f32)
+        hipLaunchKernelGGL((decodeUnitKernel<true, 2>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((decodeUnitKernel<false, 2>), grid, block, 0, s, a);
     HIP_CHECK(hipGetLastError());
 }
 
