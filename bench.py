@@ -57,8 +57,9 @@ def parse():
     p.add_argument("--profiles-dir", default=str(ROOT / "profiles"), help="where the --summarize* outputs go")
     p.add_argument("--summarize-step", nargs=2, metavar=("TRACE_DIR", "TAG"),
                    help="per-step kernel table of a --workload qwen2 kernel trace into profiles/TAG.md")
-    p.add_argument("--summarize-mfma", nargs=4, metavar=("STATS_DIR", "UTIL_DIR", "MOPS_DIR", "TAG"),
-                   help="per-kernel MFMA use from a kernel trace and two counter runs into profiles/TAG.md")
+    p.add_argument("--summarize-mfma", nargs="+", metavar="DIR",
+                   help="STATS_DIR UTIL_DIR MOPS_DIR [INSTS_DIR] TAG: per-kernel MFMA use from a kernel trace and "
+                        "two (three) counter runs into profiles/TAG.md")
     p.add_argument("--profiled-args", default="--no-cpu --no-model --steps 200",
                    help="bench arguments of the kernel-trace run")
     p.add_argument("--pmc-args", default="--no-cpu --no-model --steps 20 --warmup 5",
@@ -901,19 +902,27 @@ def summarize_step(args):
 def summarize_mfma(args):
     """MFMA use per kernel of a workload from three rocprofv3 runs.
 
-    --summarize-mfma STATS_DIR UTIL_DIR MOPS_DIR TAG: STATS_DIR holds a
-    --kernel-trace --stats run (average duration per kernel), UTIL_DIR a
-    `--pmc MfmaUtil` run (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs,
-    percent), MOPS_DIR a `--pmc SQ_INSTS_VALU_MFMA_MOPS_BF16` run (bf16 MFMA
-    math ops / 512 per dispatch). Writes profiles/TAG.md with, per kernel, the
+    --summarize-mfma STATS_DIR UTIL_DIR MOPS_DIR [INSTS_DIR] TAG: STATS_DIR
+    holds a --kernel-trace --stats run (average duration per kernel), UTIL_DIR
+    a `--pmc MfmaUtil` run (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x
+    SIMDs, percent), MOPS_DIR a `--pmc SQ_INSTS_VALU_MFMA_MOPS_BF16` run (bf16
+    MFMA math ops / 512 per dispatch), INSTS_DIR (optional) a `--pmc
+    SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_VALU_TRANS_F32` run (instructions per
+    dispatch; MFMA instructions are VALU instructions, so the non-MFMA VALU
+    count is their difference). Writes profiles/TAG.md with, per kernel, the
     MFMA-busy percentage, the bf16 MFMA FLOP per dispatch and FLOP/s over the
-    average duration, against the 2.5 PFLOP/s dense bf16 peak.
+    average duration against the 2.5 PFLOP/s dense bf16 peak, and the
+    instruction mix.
     """
     import csv
     import glob
     from collections import defaultdict
 
-    stats_dir, util_dir, mops_dir, tag = args.summarize_mfma
+    if len(args.summarize_mfma) not in (4, 5):
+        raise SystemExit("--summarize-mfma takes STATS_DIR UTIL_DIR MOPS_DIR [INSTS_DIR] TAG")
+    stats_dir, util_dir, mops_dir = args.summarize_mfma[:3]
+    insts_dir = args.summarize_mfma[3] if len(args.summarize_mfma) == 5 else None
+    tag = args.summarize_mfma[-1]
 
     def counters(d):
         acc = defaultdict(list)
@@ -930,16 +939,21 @@ def summarize_mfma(args):
         for r in csv.DictReader(open(f)):
             durations[r["Name"]] = float(r["AverageNs"])
     util, mops = counters(util_dir), counters(mops_dir)
+    insts = counters(insts_dir) if insts_dir else {}
     cmd = f"python3 bench.py {args.profiled_args}"
     lines = [f"# {tag}: MFMA use (rocprofv3 counters)", "", "Commands (from the repo root, on the MI355X box):", "",
              "```",
              f"rocprofv3 --kernel-trace --stats --output-format csv -d {stats_dir} -o run -- {cmd}",
              f"rocprofv3 --pmc MfmaUtil --output-format csv -d {util_dir} -o run -- {cmd}",
-             f"rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16 --output-format csv -d {mops_dir} -o run -- {cmd}",
-             f"python3 bench.py --summarize-mfma {' '.join(args.summarize_mfma)} --profiled-args '{args.profiled_args}'",
-             "```", "",
-             "| kernel | avg us | MFMA busy % | bf16 MFMA GFLOP / dispatch | TFLOP/s | % of 2.5 PFLOP/s |",
-             "|---|---|---|---|---|---|"]
+             f"rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16 --output-format csv -d {mops_dir} -o run -- {cmd}"]
+    if insts_dir:
+        lines.append(f"rocprofv3 --pmc SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_VALU_TRANS_F32 --output-format csv "
+                     f"-d {insts_dir} -o run -- {cmd}")
+    lines += [f"python3 bench.py --summarize-mfma {' '.join(args.summarize_mfma)} --profiled-args '{args.profiled_args}'",
+              "```", "",
+              "| kernel | avg us | MFMA busy % | bf16 MFMA GFLOP / dispatch | TFLOP/s | % of 2.5 PFLOP/s |"
+              + (" VALU instr. | MFMA instr. | non-MFMA VALU per MFMA | transcendental per MFMA |" if insts_dir else ""),
+              "|---|---|---|---|---|---|" + ("---|---|---|---|" if insts_dir else "")]
     for name, ns in sorted(durations.items(), key=lambda kv: -kv[1]):
         if "llaisys" not in name:
             continue
@@ -947,9 +961,16 @@ def summarize_mfma(args):
         m = mops.get((name, "SQ_INSTS_VALU_MFMA_MOPS_BF16"))
         flop = m * 512 if m is not None else None
         tf = flop / ns / 1e3 if flop else None
-        lines.append(f"| `{short(name)}` | {ns / 1e3:.2f} | {'' if u is None else f'{u:.1f}'} | "
-                     f"{'' if flop is None else f'{flop / 1e9:.2f}'} | {'' if tf is None else f'{tf:.1f}'} | "
-                     f"{'' if tf is None else f'{100 * tf / 2500:.1f}'} |")
+        row = (f"| `{short(name)}` | {ns / 1e3:.2f} | {'' if u is None else f'{u:.1f}'} | "
+               f"{'' if flop is None else f'{flop / 1e9:.2f}'} | {'' if tf is None else f'{tf:.1f}'} | "
+               f"{'' if tf is None else f'{100 * tf / 2500:.1f}'} |")
+        if insts_dir:
+            v, mf, tr = (insts.get((name, c)) for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_TRANS_F32"))
+            ratio = (v - mf) / mf if v is not None and mf else None
+            trr = tr / mf if tr is not None and mf else None
+            row += (f" {'' if v is None else f'{v:.0f}'} | {'' if mf is None else f'{mf:.0f}'} | "
+                    f"{'' if ratio is None else f'{ratio:.2f}'} | {'' if trr is None else f'{trr:.2f}'} |")
+        lines.append(row)
     print("\n".join(lines))
     outdir = Path(args.profiles_dir)
     outdir.mkdir(parents=True, exist_ok=True)
