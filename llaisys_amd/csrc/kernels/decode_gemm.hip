@@ -66,8 +66,19 @@ decodeGemmKernel(GemmArgs a) {
     const int kb0 = wave * KS;
     // M split over mgroups workgroups per row block (small N, large M: the
     // weights are read mgroups times, each workgroup's X is that much smaller).
-    const int mg = int(blockIdx.x) % a.mgroups;
-    const int first = int(blockIdx.x) / a.mgroups, stride = int(gridDim.x) / a.mgroups;
+    // The mgroups workgroups of one row-block walk sit on one XCD (ids
+    // congruent mod 8), so the walk's W tiles come from HBM once and from
+    // that XCD's L2 for the other row groups.
+    int mg, first;
+    const int stride = int(gridDim.x) / a.mgroups;
+    if (stride % 8 == 0) {
+        const int j = int(blockIdx.x) / 8;
+        mg = j % a.mgroups;
+        first = (j / a.mgroups) * 8 + int(blockIdx.x) % 8;
+    } else {
+        mg = int(blockIdx.x) % a.mgroups;
+        first = int(blockIdx.x) / a.mgroups;
+    }
     a.x += size_t(mg) * 16 * MB * a.K;
     a.y += size_t(mg) * 16 * MB * a.N;
     a.M = min(16 * MB, a.M - mg * 16 * MB);
