@@ -109,34 +109,48 @@ struct PairP {
     bf16x8 hi, lo;
 };
 
-// Raw scores of one page pair (K pages a, b) against the lane's column, with
-// keys the column may not see set to -inf. first_key = key position of page
-// A's token 0; pos = last key this lane's column may see (-1: none); hasB =
-// page B exists. full = every key of the pair is visible to every column of
-// the wave (wave-uniform): no per-key mask.
-__device__ __forceinline__ void pairScores(float (&sv)[8], const u32x4 (&ka)[4], const u32x4 (&kb)[4],
-                                           const u32x4 (&qop)[4], int first_key, int pos, bool hasB, int grp,
-                                           bool full = false) {
-    f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+// Raw scores of one page pair (K pages a, b) against the lane's column of
+// each of NT query tiles, with keys a column may not see set to -inf.
+// first_key = key position of page A's token 0; pos[k] = last key tile k's
+// column may see (-1: none); hasB = page B exists. full = every key of the
+// pair is visible to every column of the wave (wave-uniform): no per-key mask.
+// A 16x16x32 MFMA's result reaches a dependent MFMA ~48 cycles after issue
+// and MFMAs issue 16 cycles apart, so the NT tiles' page-A and page-B
+// accumulator chains are interleaved (4 chains in flight with two tiles).
+// (With one tile, splitting each page's 4 k steps over two chains, summed at
+// the end, measured no faster in the memory-bound decode kernel.)
+template <int NT>
+__device__ __forceinline__ void pairScoresN(float (&sv)[NT][8], const u32x4 (&ka)[4], const u32x4 (&kb)[4],
+                                            const u32x4 (&qop)[NT][4], int first_key, const int (&pos)[NT], bool hasB,
+                                            int grp, bool full = false) {
+    f32x4 sa[NT], sb[NT];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        sa = mfma(asBf16(ka[s]), asBf16(qop[s]), sa);
-        sb = mfma(asBf16(kb[s]), asBf16(qop[s]), sb);
-    }
+    for (int k = 0; k < NT; ++k) sa[k] = sb[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        sv[i] = sa[i];
-        sv[4 + i] = sb[i];
-    }
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int k = 0; k < NT; ++k) {
+            sa[k] = mfma(asBf16(ka[s]), asBf16(qop[k][s]), sa[k]);
+            sb[k] = mfma(asBf16(kb[s]), asBf16(qop[k][s]), sb[k]);
+        }
+#pragma unroll
+    for (int k = 0; k < NT; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sv[k][i] = sa[k][i];
+            sv[k][4 + i] = sb[k][i];
+        }
     // A branch of its own: folded into the selects, the wave-uniform `full`
     // would still leave every compare and select on the path.
     if (!full) {
         const int kbase = first_key + grp * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sv[i] = kbase + i <= pos ? sv[i] : -INFINITY;
-            sv[4 + i] = (hasB && kbase + 16 + i <= pos) ? sv[4 + i] : -INFINITY;
-        }
+        for (int k = 0; k < NT; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sv[k][i] = kbase + i <= pos[k] ? sv[k][i] : -INFINITY;
+                sv[k][4 + i] = (hasB && kbase + 16 + i <= pos[k]) ? sv[k][4 + i] : -INFINITY;
+            }
     }
 }
 
@@ -185,7 +199,9 @@ template <bool SPLIT_P>
 __device__ __forceinline__ PairP scorePair(Acc &acc, const u32x4 (&ka)[4], const u32x4 (&kb)[4], const u32x4 (&qop)[4],
                                           int first_key, int pos, bool hasB, int grp, float scale_log2) {
     float sv[1][8];
-    pairScores(sv[0], ka, kb, qop, first_key, pos, hasB, grp);
+    const u32x4(&q1)[1][4] = *reinterpret_cast<const u32x4(*)[1][4]>(&qop);
+    const int p1[1] = {pos};
+    pairScoresN<1>(sv, ka, kb, q1, first_key, p1, hasB, grp);
     PairP P[1];
     softmaxUpdate<SPLIT_P, 1>(acc, sv, P, scale_log2);
     return P[0];

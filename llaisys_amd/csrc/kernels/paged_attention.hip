@@ -295,9 +295,15 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                         ka[s] = src[(0 * 4 + s) * 64 + lane];
                         kb[s] = src[(1 * 4 + s) * 64 + lane];
                     }
+                    int lim[kTiles];
+#pragma unroll
+                    for (int k = 0; k < kTiles; ++k) lim[k] = hasA ? pos[k] : -1;
+                    float svj[kTiles][8];
+                    pairScoresN<kTiles>(svj, ka, kb, qop, pp * 16, lim, hasB, grp, full);
 #pragma unroll
                     for (int k = 0; k < kTiles; ++k)
-                        pairScores(sv[k][j], ka, kb, qop[k], pp * 16, hasA ? pos[k] : -1, hasB, grp, full);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) sv[k][j][e] = svj[k][e];
                 }
                 PairP P[kTiles][kSoft];
 #pragma unroll
