@@ -211,8 +211,7 @@ template <int MB> constexpr int wavesFor() { return MB <= 4 ? 8 : 4; }
 template <int MB> void launchGemm(const GemmArgs &a, hipStream_t s) {
     constexpr int W = wavesFor<MB>();
     constexpr int KS = kDecodeGemmK / (32 * W);
-    static const int gdiv = std::getenv("LLAISYS_GEMM_GDIV") ? std::atoi(std::getenv("LLAISYS_GEMM_GDIV")) : 1;
-    const int grid = std::max(1, std::min(a.nblocks / gdiv, computeUnitsOf()));
+    const int grid = std::max(1, std::min(a.nblocks, computeUnitsOf()));
     const size_t lds = size_t(2) * W * MB * 64 * sizeof(f32x4);
     if (a.accumulate)
         hipLaunchKernelGGL((decodeGemmKernel<MB, KS, true, W>), dim3(grid), dim3(64 * W), lds, s, a);
