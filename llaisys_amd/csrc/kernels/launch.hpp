@@ -62,6 +62,19 @@ void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t
                       const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
                       int num_blocks, float scale, int *err, void *stream);
 
+// pagedDecodeUnits with the decode step's QKV epilogue fused in (one token per
+// sequence): from qkv [B, (nh + 2 nkvh) * 128] (projection rows before bias)
+// each workgroup forms its unit's query heads and k/v head as qkvRopeAppend
+// does (x: residual rows whose RMSNorm is folded into the projection, or
+// null; position ctx_len[b] - 1), stores k/v into their page slot and attends
+// with q straight from LDS. Needs nh / nkvh <= 6 and head dim 128
+// (decodeUnitsRopeSupported).
+bool decodeUnitsRopeSupported(int nh, int nkvh, int d);
+void pagedDecodeUnitsRope(void *out, bool out_f32, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv,
+                          const uint16_t *bias, const uint16_t *x, int hs, float eps, float theta,
+                          const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                          int num_blocks, float scale, int *err, void *stream);
+
 // The decode above with its split records in a fixed per-GPU device array
 // (noAllocScratchBytes() bytes) instead of runtime workspace: no device
 // allocation per call. noAllocInit() looks the array's address up for the

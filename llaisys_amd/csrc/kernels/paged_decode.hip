@@ -30,8 +30,11 @@
 // Per pair a wave reads 16 KiB of K/V plus the unit's query rows (1 KiB per
 // 16 columns, from L2) and issues 24 MFMAs (mfma_common.hpp has the layout).
 #include "mfma_common.hpp"
+#include "step_common.hpp"
 
 #include "../device/hip_check.hpp"
+
+#include <hip/hip_bf16.h>
 
 #include <algorithm>
 #include <cstddef>
@@ -474,11 +477,66 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
 // no second launch, no length scan: each workgroup reads its own length.
 // Balanced only when the units have similar lengths, which the caller
 // decides (a decode batch of similar contexts); query row b is sequence b.
+//
+// With ROPE the kernel also does the step's QKV epilogue for its unit (the
+// work of qkvRopeAppend for one decode token): each wave forms the G query
+// heads in its own MFMA operand registers from the projection row (scaled by
+// the row's 1/rms when the RMSNorm is folded into the weights, plus bias,
+// rotated by position ctx - 1). Wave 0, which holds the fewest pairs, also
+// forms the new k and v before starting its pages, stores them into their
+// page slot for later steps and leaves them in LDS; the last wave, which
+// holds the unit's last pair, consumes that pair after a barrier at the end
+// of the loop with the new token patched into its registers, so no load
+// waits for the stores. The other waves start their first pages before the
+// epilogue's arithmetic.
 constexpr int kUnitWaves = 4;
+constexpr int kRopeMaxGroup = 16; // query heads per kv head in the fused epilogue: one MFMA column each
 
-template <bool OUT_F32, int NSTAGE>
+// The new token (slot tok of the last page) written into a loaded page pair's
+// registers from wave 0's LDS copy (kf, vf: bf16 by dim): its page is A when
+// the pair's first page is the last one (then B repeats A and is masked),
+// else B. K: lane L holds token L % 16's chunks [d / 8 = L / 16 + 4 s]; V:
+// lanes with L / 16 == tok / 4 hold element (d / 16 % 2) * 4 + tok % 4 of
+// dims d = 32 s + 16 p + L % 16 in word 2 p + (tok % 4) / 2 (chosen by
+// select: a runtime index into a vector register would go through scratch).
+__device__ __forceinline__ void patchNewToken(PagePair &pp, const uint16_t *kf, const uint16_t *vf, int tok,
+                                              bool in_a, int lane) {
+    if ((lane & 15) == tok) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const u32x4 kn = *reinterpret_cast<const u32x4 *>(kf + 8 * ((lane >> 4) + 4 * s));
+            if (in_a) pp.ka[s] = kn;
+            pp.kb[s] = kn;
+        }
+    }
+    if ((lane >> 4) == (tok >> 2)) {
+        const int wd0 = (tok & 3) >> 1, sh = 16 * (tok & 1);
+        const uint32_t keep = ~(0xffffu << sh);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd) {
+                const bool hit = (wd & 1) == wd0;
+                const uint32_t val = uint32_t(vf[32 * s + 16 * (wd >> 1) + (lane & 15)]) << sh;
+                pp.va[s][wd] = hit && in_a ? (pp.va[s][wd] & keep) | val : pp.va[s][wd];
+                pp.vb[s][wd] = hit ? (pp.vb[s][wd] & keep) | val : pp.vb[s][wd];
+            }
+    }
+}
+
+struct RopeArgs {
+    const uint16_t *qkv;  // [B, (nh + 2 nkvh) * 128] projection rows, before bias
+    const uint16_t *bias; // [(nh + 2 nkvh) * 128]
+    const uint16_t *x;    // [B, hs] residual rows whose RMSNorm is folded in; null: none
+    uint16_t *k_pool, *v_pool;
+    int hs;
+    float eps, theta;
+};
+
+template <bool OUT_F32, int NSTAGE, bool ROPE>
 __global__ void __launch_bounds__(64 * kUnitWaves)
-    __attribute__((amdgpu_waves_per_eu(NSTAGE == 2 ? 2 : 1, NSTAGE == 2 ? 2 : 1))) decodeUnitKernel(DecodeArgs a) {
+    __attribute__((amdgpu_waves_per_eu(NSTAGE == 2 ? 2 : 1, NSTAGE == 2 ? 2 : 1)))
+        decodeUnitKernel(DecodeArgs a, RopeArgs r) {
     __shared__ f32x4 part_o[kUnitWaves - 1][8][64];
     __shared__ float part_ml[kUnitWaves - 1][2][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -489,6 +547,33 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
     const int u = blockIdx.x;
     const int b = u / a.nkvh;
     const int h = u - b * a.nkvh;
+    // Fused epilogue (ROPE) inputs, none of which depends on the length: the
+    // projection row's query head h G + n (4 x 16 B of the lane's dims) and
+    // its bias; the new token's k dims (lane, lane + 64), v dims (2 lane,
+    // 2 lane + 1) and their biases; the row's x for its 1/rms (the
+    // projection row stands in when no norm is folded: read, not used).
+    // Issued first, before the length is known.
+    const uint16_t *prow = ROPE ? r.qkv + size_t(b) * (a.nh + 2 * a.nkvh) * kHeadDim : nullptr;
+    u32x4 qw[4], qb[4];
+    uint32_t kw0 = 0, kw1 = 0, kb0 = 0, kb1 = 0, vw = 0, vb = 0;
+    RowChunks xr;
+    const int xd = r.x ? r.hs : 8;
+    if constexpr (ROPE) {
+        const int qcol = (h * G + min(n, G - 1)) * kHeadDim + grp * 8;
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+            qw[t4] = *reinterpret_cast<const u32x4 *>(prow + qcol + 32 * t4);
+            qb[t4] = *reinterpret_cast<const u32x4 *>(r.bias + qcol + 32 * t4);
+        }
+        const int kcol = (a.nh + h) * kHeadDim, vcol = (a.nh + a.nkvh + h) * kHeadDim;
+        kw0 = prow[kcol + lane];
+        kw1 = prow[kcol + lane + 64];
+        kb0 = r.bias[kcol + lane];
+        kb1 = r.bias[kcol + lane + 64];
+        vw = *reinterpret_cast<const uint32_t *>(prow + vcol + 2 * lane);
+        vb = *reinterpret_cast<const uint32_t *>(r.bias + vcol + 2 * lane);
+        xr.load(r.x ? r.x + size_t(b) * r.hs : prow, xd);
+    }
     int c = a.ctx[b];
     if (c < 1 || c > a.max_pages * 16) { // invalid length: zero output, error flag
         if (threadIdx.x == 0) atomicOr(a.err, kErrTooLong);
@@ -501,52 +586,166 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
     Acc acc;
     acc.reset();
     bool bad_block = false;
-    if (p1 > p0) {
-        u32x4 qop[4];
+    const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
+    const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
+    const int32_t *row = a.table + size_t(b) * a.max_pages;
+
+    // Window state: lane i holds the block ids of pair base + i (windows of
+    // up to 64 pairs). Loads are never conditional: past the window's end
+    // they re-read its last pair (an L2 hit).
+    int base = p0, cnt = min(kPairsPerWave, p1 - p0), bidA = 0, bidB = 0;
+    auto loadWindow = [&]() { // (clamped reads of row[0] when the wave has no pairs)
+        const int pa = max(2 * (base + min(lane, cnt - 1)), 0);
+        bidA = row[pa];
+        bidB = row[max(min(pa + 1, np - 1), 0)];
+    };
+    PagePair ring[NSTAGE];
+    auto issue = [&](int st, int k) {
+        const int kk = max(min(k, cnt - 1), 0);
+        int bA = __builtin_amdgcn_readlane(bidA, kk);
+        int bB = __builtin_amdgcn_readlane(bidB, kk);
+        const bool bad = unsigned(bA) >= unsigned(a.num_blocks) || unsigned(bB) >= unsigned(a.num_blocks);
+        bad_block |= bad && cnt > 0; // a wave with no pairs loads a stand-in
+        bA = bad ? 0 : bA;
+        bB = bad ? 0 : bB;
+        loadPair(ring[st], kp, vp, (size_t(bA) * a.nkvh + h) * 256, (size_t(bB) * a.nkvh + h) * 256);
+    };
+    if (!ROPE && p1 > p0) loadWindow();
+
+    u32x4 qop[4];
+    // Fused epilogue (ROPE): wave 0 forms the new token's k and v and leaves
+    // them in LDS (kflat, vflat: bf16 by dim) for the last wave, which holds
+    // the unit's last pair.
+    __shared__ __align__(16) uint16_t kflat[ROPE ? kHeadDim : 8], vflat[ROPE ? kHeadDim : 8];
+    const bool last_wave = ROPE && p1 > p0 && p1 == npr;
+    const int tok = (c - 1) & 15;
+    bool issued = false; // the first window's first stages already in flight
+    if constexpr (ROPE) {
+        // The epilogue's inputs are in flight since the kernel's start; the
+        // block-table window, the new token's block id and the first pages
+        // follow with no branch in between (loads clamped to valid addresses,
+        // results selected afterwards), so the epilogue's waits count only
+        // its own loads, not the pages behind them.
+        __shared__ float2 trig[kUnitWaves][64];
+        const int pos = c - 1;
+        loadWindow();
+        const bool qlive = c > 0 && n < G;
+        // The new token's page (the index goes through a vector register, so
+        // the block id stays per lane: moved to a scalar right after its load
+        // it would make the wave wait for every load issued before it).
+        int slot_page = max(pos, 0) >> 4;
+        asm volatile("" : "+v"(slot_page));
+        const int blk = row[slot_page];
+#pragma unroll
+        for (int st = 0; st < NSTAGE; ++st) issue(st, st);
+        issued = true;
+        // (sin, cos) of the 64 rotation angles of position pos: lane (n, grp)
+        // works out j = grp * 8 + 32 (n / 8) + n % 8 (the lane's own dims
+        // below d/2 are grp * 8 + 32 t + e, t < 2), shared through LDS.
+        {
+            const int j = grp * 8 + 32 * (n >> 3) + (n & 7);
+            float sn, cs;
+            sincosf(ropePhi(pos, j, kHeadDim, r.theta), &sn, &cs);
+            trig[wave][lane] = make_float2(sn, cs);
+        }
+        const float ss = xr.sumSquares(r.x ? r.x + size_t(b) * r.hs : prow, xd);
+        const float rs = r.x ? rsqrtf(ss / float(r.hs) + r.eps) : 1.f;
+        __builtin_amdgcn_wave_barrier();
+        // Query: rotate (j, j + 64) for the lane's 16 j; word w of chunk t4
+        // holds dims grp * 8 + 32 t4 + 2 w, + 1, chunk t4 + 2 their partners.
+#pragma unroll
+        for (int t4 = 0; t4 < 2; ++t4)
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd) {
+                uint32_t lo_out = 0, hi_out = 0;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float2 sc = trig[wave][grp * 16 + t4 * 8 + 2 * wd + e];
+                    const int sh = e ? 0 : 16;
+                    const float x0 = rs * __uint_as_float((qw[t4][wd] << sh) & 0xffff0000u) +
+                                     __uint_as_float((qb[t4][wd] << sh) & 0xffff0000u);
+                    const float x1 = rs * __uint_as_float((qw[t4 + 2][wd] << sh) & 0xffff0000u) +
+                                     __uint_as_float((qb[t4 + 2][wd] << sh) & 0xffff0000u);
+                    const uint32_t r0 = __builtin_bit_cast(uint16_t, __float2bfloat16(x0 * sc.y - x1 * sc.x));
+                    const uint32_t r1 = __builtin_bit_cast(uint16_t, __float2bfloat16(x1 * sc.y + x0 * sc.x));
+                    lo_out |= r0 << (16 * e);
+                    hi_out |= r1 << (16 * e);
+                }
+                qop[t4][wd] = lo_out;
+                qop[t4 + 2][wd] = hi_out;
+            }
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) qop[t4] = qlive ? qop[t4] : u32x4{0, 0, 0, 0};
+        if (wave == 0 && c > 0) {
+            // k: lane j rotates (j, j + 64) with the angle lane
+            // (j / 8 % 4) * 16 + (j / 32) * 8 + j % 8 worked out; v: 2 dims.
+            const float2 sc = trig[0][((lane >> 3) & 3) * 16 + (lane >> 5) * 8 + (lane & 7)];
+            const float x0 = rs * __uint_as_float(kw0 << 16) + __uint_as_float(kb0 << 16);
+            const float x1 = rs * __uint_as_float(kw1 << 16) + __uint_as_float(kb1 << 16);
+            const uint16_t k0 = __builtin_bit_cast(uint16_t, __float2bfloat16(x0 * sc.y - x1 * sc.x));
+            const uint16_t k1 = __builtin_bit_cast(uint16_t, __float2bfloat16(x1 * sc.y + x0 * sc.x));
+            const uint16_t v0 = __builtin_bit_cast(
+                uint16_t, __float2bfloat16(rs * __uint_as_float(vw << 16) + __uint_as_float(vb << 16)));
+            const uint16_t v1 = __builtin_bit_cast(
+                uint16_t, __float2bfloat16(rs * __uint_as_float(vw & 0xffff0000u) + __uint_as_float(vb & 0xffff0000u)));
+            kflat[lane] = k0;
+            kflat[lane + 64] = k1;
+            vflat[2 * lane] = v0;
+            vflat[2 * lane + 1] = v1;
+            // Stores into the page slot for later steps: lanes 0-15 the k
+            // chunks [d / 8][tok] (16 B each), every lane its 2 v dims.
+            if (unsigned(blk) >= unsigned(a.num_blocks)) {
+                if (lane == 0) atomicOr(a.err, kErrBadBlock);
+            } else {
+                const size_t page = (size_t(blk) * a.nkvh + h) * kPageElems;
+                __builtin_amdgcn_wave_barrier();
+                if (lane < 16)
+                    *reinterpret_cast<u32x4 *>(r.k_pool + page + kPageIndex(tok, 8 * lane)) =
+                        *reinterpret_cast<const u32x4 *>(&kflat[8 * lane]);
+                r.v_pool[page + vPageIndex(tok, 2 * lane)] = v0;
+                r.v_pool[page + vPageIndex(tok, 2 * lane + 1)] = v1;
+            }
+        }
+    } else {
         const uint16_t *qrow = a.q + (size_t(b) * a.nh + h * G + min(n, G - 1)) * kHeadDim + grp * 8;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            qop[t] = *reinterpret_cast<const u32x4 *>(qrow + 32 * t);
-            qop[t] = n < G ? qop[t] : u32x4{0, 0, 0, 0};
+        for (int t4 = 0; t4 < 4; ++t4) {
+            qop[t4] = *reinterpret_cast<const u32x4 *>(qrow + 32 * t4);
+            qop[t4] = n < G ? qop[t4] : u32x4{0, 0, 0, 0};
         }
-        const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
-        const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
-        const int32_t *row = a.table + size_t(b) * a.max_pages;
-        // Windows of up to 64 pairs: lane i holds the block ids of pair
-        // base + i. Loads are never conditional: past the window's end they
-        // re-read its last pair (an L2 hit).
-        for (int base = p0; base < p1; base += kPairsPerWave) {
-            const int cnt = min(kPairsPerWave, p1 - base);
-            int bidA, bidB;
-            {
-                const int pa = 2 * (base + min(lane, cnt - 1));
-                bidA = row[pa];
-                bidB = row[min(pa + 1, np - 1)];
-            }
-            PagePair ring[NSTAGE];
-            auto issue = [&](int st, int k) {
-                const int kk = min(k, cnt - 1);
-                int bA = __builtin_amdgcn_readlane(bidA, kk);
-                int bB = __builtin_amdgcn_readlane(bidB, kk);
-                const bool bad = unsigned(bA) >= unsigned(a.num_blocks) || unsigned(bB) >= unsigned(a.num_blocks);
-                bad_block |= bad;
-                bA = bad ? 0 : bA;
-                bB = bad ? 0 : bB;
-                loadPair(ring[st], kp, vp, (size_t(bA) * a.nkvh + h) * 256, (size_t(bB) * a.nkvh + h) * 256);
-            };
+    }
+    for (; base < p1; base += kPairsPerWave) {
+        cnt = min(kPairsPerWave, p1 - base);
+        if (base != p0) loadWindow();
+        if (!issued) {
 #pragma unroll
             for (int st = 0; st < NSTAGE; ++st) issue(st, st);
-            for (int k0 = 0; k0 < cnt; k0 += NSTAGE) {
+        }
+        issued = false;
+        // The fused epilogue's last wave leaves the unit's last pair to the
+        // tail below (the patch stays out of the loop's registers).
+        const int cnt_c = cnt - (last_wave && base + cnt == npr ? 1 : 0);
+        for (int k0 = 0; k0 < cnt; k0 += NSTAGE) {
 #pragma unroll
-                for (int st = 0; st < NSTAGE; ++st) {
-                    const int k = k0 + st;
-                    if (k < cnt) {
-                        const int j = base + k;
-                        consumePair<OUT_F32>(acc, ring[st], qop, 32 * j, c - 1, c, 2 * j + 1 < np, grp, a.scale_log2);
-                    }
-                    issue(st, k + NSTAGE);
+            for (int st = 0; st < NSTAGE; ++st) {
+                const int k = k0 + st;
+                if (k < cnt_c) {
+                    const int j = base + k;
+                    consumePair<OUT_F32>(acc, ring[st], qop, 32 * j, c - 1, c, 2 * j + 1 < np, grp, a.scale_log2);
                 }
+                issue(st, k + NSTAGE);
             }
+        }
+    }
+    if constexpr (ROPE) {
+        // Wave 0's stash is visible after this barrier. Past the window's end
+        // every ring slot re-reads its last pair, so slot 0 holds the unit's
+        // last pair: patch in the new token, consume.
+        __syncthreads();
+        if (last_wave) {
+            const int j = npr - 1;
+            patchNewToken(ring[0], kflat, vflat, tok, 2 * j == np - 1, lane);
+            consumePair<OUT_F32>(acc, ring[0], qop, 32 * j, c - 1, c, 2 * j + 1 < np, grp, a.scale_log2);
         }
     }
     if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
@@ -726,9 +925,10 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
     HIP_CHECK(hipGetLastError());
 }
 
-void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
-                      const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                      int num_blocks, float scale, int *err, void *stream) {
+namespace {
+void launchDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                       const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                       int num_blocks, float scale, int *err, const RopeArgs *rope, void *stream) {
     if (B == 0) return;
     DecodeArgs a{};
     a.q = q;
@@ -746,16 +946,49 @@ void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t
     a.max_pages = max_pages;
     a.num_blocks = num_blocks;
     a.scale_log2 = scale * 1.4426950408889634f;
+    const RopeArgs r = rope ? *rope : RopeArgs{};
     // Two page pairs in flight per wave, two waves per SIMD: measured best
     // in the config-5 step (3.37 ms; three in flight at one wave per SIMD:
     // 3.47 ms; 8 waves per unit: 3.46 ms).
     auto s = static_cast<hipStream_t>(stream);
     const dim3 grid(unsigned(B) * unsigned(nkvh)), block(64 * kUnitWaves);
-    if (out_f32)
-        hipLaunchKernelGGL((decodeUnitKernel<true, 2>), grid, block, 0, s, a);
-    else
-        hipLaunchKernelGGL((decodeUnitKernel<false, 2>), grid, block, 0, s, a);
+    if (rope) {
+        if (out_f32)
+            hipLaunchKernelGGL((decodeUnitKernel<true, 2, true>), grid, block, 0, s, a, r);
+        else
+            hipLaunchKernelGGL((decodeUnitKernel<false, 2, true>), grid, block, 0, s, a, r);
+    } else {
+        if (out_f32)
+            hipLaunchKernelGGL((decodeUnitKernel<true, 2, false>), grid, block, 0, s, a, r);
+        else
+            hipLaunchKernelGGL((decodeUnitKernel<false, 2, false>), grid, block, 0, s, a, r);
+    }
     HIP_CHECK(hipGetLastError());
+}
+} // namespace
+
+void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
+                      const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                      int num_blocks, float scale, int *err, void *stream) {
+    launchDecodeUnits(out, out_f32, q, k_pool, v_pool, block_table, ctx_len, B, nh, nkvh, max_pages, num_blocks,
+                      scale, err, nullptr, stream);
+}
+
+bool decodeUnitsRopeSupported(int nh, int nkvh, int d) {
+    return d == kHeadDim && nkvh > 0 && nh % nkvh == 0 && nh / nkvh <= kRopeMaxGroup;
+}
+
+void pagedDecodeUnitsRope(void *out, bool out_f32, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv,
+                          const uint16_t *bias, const uint16_t *x, int hs, float eps, float theta,
+                          const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
+                          int num_blocks, float scale, int *err, void *stream) {
+    LLAISYS_CHECK(decodeUnitsRopeSupported(nh, nkvh, kHeadDim),
+                  "pagedDecodeUnitsRope: " << nh << " query heads over " << nkvh << " kv heads exceed "
+                                           << kRopeMaxGroup << " per kv head");
+    LLAISYS_CHECK(!x || (hs > 0 && hs % 8 == 0), "pagedDecodeUnitsRope: hidden size must be a positive multiple of 8");
+    const RopeArgs r{qkv, bias, x, k_pool, v_pool, hs, eps, theta};
+    launchDecodeUnits(out, out_f32, nullptr, k_pool, v_pool, block_table, ctx_len, B, nh, nkvh, max_pages,
+                      num_blocks, scale, err, &r, stream);
 }
 
 } // namespace llaisys::kernels

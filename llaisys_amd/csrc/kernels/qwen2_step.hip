@@ -16,6 +16,7 @@
 //    output (qkvRopeAppend, swigluRows take the residual rows x for it), so
 //    the layer runs no separate rms_norm launch.
 #include "launch.hpp"
+#include "step_common.hpp"
 
 #include "../common.hpp"
 #include "../device/hip_check.hpp"
@@ -34,22 +35,10 @@ constexpr int kThreads = 256;
 __device__ __forceinline__ float f(bf16 v) { return __bfloat162float(v); }
 
 // 1/sqrt(mean(x^2) + eps) of one row of d (% 8 == 0) bf16 values, computed
-// by the whole 64-lane wave (every lane gets the result), as rmsNormRows does.
-__device__ __forceinline__ float rowInvRms(const bf16 *xrow, int d, float eps) {
-    const int lane = threadIdx.x & 63;
-    const uint4 *src = reinterpret_cast<const uint4 *>(xrow);
-    float ss = 0.f;
-    for (int c = lane; c < d / 8; c += 64) {
-        const uint4 v = src[c];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t u = (&v.x)[e];
-            const float lo = __uint_as_float(u << 16), hi = __uint_as_float(u & 0xffff0000u);
-            ss += lo * lo + hi * hi;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+// by the whole 64-lane wave (every lane gets the result), as rmsNormRows
+// does, from a RowChunks load the caller issued beside its other loads.
+__device__ __forceinline__ float rowInvRms(const RowChunks &xr, const bf16 *xrow, int d, float eps) {
+    const float ss = xr.sumSquares(reinterpret_cast<const uint16_t *>(xrow), d);
     return rsqrtf(ss / float(d) + eps);
 }
 
@@ -80,11 +69,16 @@ __global__ void __launch_bounds__(kThreads) swigluRowsKernel(bf16 *act, const bf
                                                              float eps) {
     const int nv = di / 8;
     const size_t r = blockIdx.y;
-    const float rs = x ? rowInvRms(x + r * hs, hs, eps) : 1.f;
     const int c = blockIdx.x * kThreads + threadIdx.x;
+    // Every load first (gate, up and the row's x, clamped rather than
+    // branched), so the latencies overlap.
+    const int cc = min(c, nv - 1);
+    const uint4 g = reinterpret_cast<const uint4 *>(gu + r * 2 * di)[cc];
+    const uint4 u = reinterpret_cast<const uint4 *>(gu + r * 2 * di + di)[cc];
+    RowChunks xr; // (without x the gate row stands in: read, not used)
+    xr.load(reinterpret_cast<const uint16_t *>(x ? x + r * hs : gu + r * 2 * di), x ? hs : 8);
+    const float rs = x ? rowInvRms(xr, x + r * hs, hs, eps) : 1.f;
     if (c < nv) {
-        const uint4 g = reinterpret_cast<const uint4 *>(gu + r * 2 * di)[c];
-        const uint4 u = reinterpret_cast<const uint4 *>(gu + r * 2 * di + di)[c];
         uint4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -99,10 +93,6 @@ __global__ void __launch_bounds__(kThreads) swigluRowsKernel(bf16 *act, const bf
     }
 }
 
-__device__ __forceinline__ int kPageIndex(int t, int d) { return (d >> 3) * 128 + t * 8 + (d & 7); }
-__device__ __forceinline__ int vPageIndex(int t, int d) {
-    return (d >> 5) * 512 + (t >> 2) * 128 + (d & 15) * 8 + ((d >> 4) & 1) * 4 + (t & 3);
-}
 
 // One 64-lane block per (token row r, head h) over the nh query, nkvh key and
 // nkvh value heads; row r belongs to sequence b (cu: varlen offsets, else
@@ -114,8 +104,19 @@ __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
     const int32_t *ctx, const int32_t *cu, int B, int nh, int nkvh, int d, int max_pages, int num_blocks, float theta,
     int *err, const bf16 *x, int hs, float eps) {
     const int r = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
-    // Row factor of the RMSNorm folded into the QKV weights (x null: none).
-    const float rs = x ? rowInvRms(x + size_t(r) * hs, hs, eps) : 1.f;
+    const int half = d / 2;
+    const bf16 *row = qkv + size_t(r) * (nh + 2 * nkvh) * d;
+    // Every load that depends on no other is issued first: the row's x for
+    // the 1/rms of the RMSNorm folded into the QKV weights (x null: none),
+    // this lane's two projection values and biases (q/k: dims j and j + d/2;
+    // v: dims 2j and 2j + 1), then the sequence's length.
+    // (Without x the projection row stands in: read, not used; a branch
+    // around the load would make later waits count conservatively.)
+    RowChunks xr;
+    xr.load(reinterpret_cast<const uint16_t *>(x ? x + size_t(r) * hs : row), x ? hs : 8);
+    const int c0 = h < nh + nkvh ? h * d + j : (nh + nkvh) * d + (h - nh - nkvh) * d + 2 * j;
+    const int c1 = h < nh + nkvh ? c0 + half : c0 + 1;
+    const float p0 = f(row[c0]), p1 = f(row[c1]), b0 = f(bias[c0]), b1 = f(bias[c1]);
     int b = r;
     if (cu) {
         int lo = 0, hi = B - 1;
@@ -126,21 +127,15 @@ __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
         b = lo;
     }
     const int pos = ctx[b] + (cu ? r - cu[b] : 0);
-    const int half = d / 2;
-    const bf16 *row = qkv + size_t(r) * (nh + 2 * nkvh) * d;
-    if (h < nh + nkvh) {
-        const float phi = float(pos) / powf(theta, float(2 * j) / float(d));
+    const float rs = x ? rowInvRms(xr, x + size_t(r) * hs, hs, eps) : 1.f;
+    const float a = rs * p0 + b0, bb = rs * p1 + b1;
+    if (h < nh) {
         float sn, cs;
-        sincosf(phi, &sn, &cs);
-        const int c = h * d + j;
-        const float a = rs * f(row[c]) + f(bias[c]), bb = rs * f(row[c + half]) + f(bias[c + half]);
-        const bf16 ra = __float2bfloat16(a * cs - bb * sn), rb = __float2bfloat16(bb * cs + a * sn);
-        if (h < nh) {
-            bf16 *dst = q + (size_t(r) * nh + h) * d;
-            dst[j] = ra;
-            dst[j + half] = rb;
-            return;
-        }
+        sincosf(ropePhi(pos, j, d, theta), &sn, &cs);
+        bf16 *dst = q + (size_t(r) * nh + h) * d;
+        dst[j] = __float2bfloat16(a * cs - bb * sn);
+        dst[j + half] = __float2bfloat16(bb * cs + a * sn);
+        return;
     }
     // k or v head: find the page slot
     const int page = pos >> 4, slot = pos & 15;
@@ -151,21 +146,15 @@ __global__ void __launch_bounds__(64) qkvRopeAppendKernel(
         return;
     }
     if (h < nh + nkvh) {
-        const int c = h * d + j;
-        const float a = rs * f(row[c]) + f(bias[c]), bb = rs * f(row[c + half]) + f(bias[c + half]);
-        const float phi = float(pos) / powf(theta, float(2 * j) / float(d));
         float sn, cs;
-        sincosf(phi, &sn, &cs);
+        sincosf(ropePhi(pos, j, d, theta), &sn, &cs);
         uint16_t *pg = k_pool + (size_t(blk) * nkvh + (h - nh)) * kPageElems;
         pg[kPageIndex(slot, j)] = __builtin_bit_cast(uint16_t, __float2bfloat16(a * cs - bb * sn));
         pg[kPageIndex(slot, j + half)] = __builtin_bit_cast(uint16_t, __float2bfloat16(bb * cs + a * sn));
     } else {
-        const int hv = h - nh - nkvh;
-        uint16_t *pg = v_pool + (size_t(blk) * nkvh + hv) * kPageElems;
-        for (int dd = 2 * j; dd < 2 * j + 2; ++dd) {
-            const int c = (nh + nkvh) * d + hv * d + dd;
-            pg[vPageIndex(slot, dd)] = __builtin_bit_cast(uint16_t, __float2bfloat16(rs * f(row[c]) + f(bias[c])));
-        }
+        uint16_t *pg = v_pool + (size_t(blk) * nkvh + (h - nh - nkvh)) * kPageElems;
+        pg[vPageIndex(slot, 2 * j)] = __builtin_bit_cast(uint16_t, __float2bfloat16(a));
+        pg[vPageIndex(slot, 2 * j + 1)] = __builtin_bit_cast(uint16_t, __float2bfloat16(bb));
     }
 }
 

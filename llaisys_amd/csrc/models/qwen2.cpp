@@ -68,6 +68,8 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     if (const char *e = std::getenv("LLAISYS_QWEN2_FOLD_NORM")) fold_norm_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_DECODE_GEMM")) decode_gemm_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_DECODE_UNITS")) unit_decode_allowed_ = e[0] != '0';
+    unit_rope_ = K::decodeUnitsRopeSupported(int(cfg.nh), int(cfg.nkvh), int(cfg.dh));
+    if (const char *e = std::getenv("LLAISYS_DECODE_UNIT_ROPE")) unit_rope_ = unit_rope_ && e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -501,17 +503,26 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
         project(qkv_, fold ? x_ : h_, fold ? L.qkv_wf : L.qkv_w, fold ? L.qkv_wfp : nullptr, M, q + 2 * kv, hs, false,
                 s);
-        K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
-                         i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh), int(cfg_.nkvh),
-                         int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta, rt.errorWord(), xr, hs,
-                         cfg_.epsilon, s);
-        if (decode_only && unit_decode_)
-            K::pagedDecodeUnits(a3->data(), false, u16(q3), u16(k_pool_[l]), u16(v_pool_[l]), i32(table_),
-                                i32(ctx_after_), int(B), int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]),
-                                int(num_blocks_), scale, rt.errorWord(), s);
-        else
-            ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_,
-                                scale);
+        if (decode_only && unit_decode_ && unit_rope_) {
+            // QKV epilogue (bias, 1/rms, RoPE, k/v append) inside the attention
+            // launch: one kernel fewer per layer.
+            K::pagedDecodeUnitsRope(a3->data(), false, u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), xr,
+                                    hs, cfg_.epsilon, cfg_.theta, i32(table_), i32(ctx_after_), int(B),
+                                    int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]), int(num_blocks_), scale,
+                                    rt.errorWord(), s);
+        } else {
+            K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
+                             i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh),
+                             int(cfg_.nkvh), int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta,
+                             rt.errorWord(), xr, hs, cfg_.epsilon, s);
+            if (decode_only && unit_decode_)
+                K::pagedDecodeUnits(a3->data(), false, u16(q3), u16(k_pool_[l]), u16(v_pool_[l]), i32(table_),
+                                    i32(ctx_after_), int(B), int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]),
+                                    int(num_blocks_), scale, rt.errorWord(), s);
+            else
+                ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_,
+                                    scale);
+        }
         project(x_, attn_, L.o_w, L.o_wp, M, hs, q, true, s);
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
         project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, fold ? L.gate_up_wfp : nullptr, M, 2 * di, hs,

@@ -139,6 +139,10 @@ private:
     // LLAISYS_DECODE_UNITS=0 keeps the stream-K kernel for every step.
     bool unit_decode_allowed_ = true;
     bool unit_decode_ = false; // the choice for the step being built
+    // With the unit attention, the QKV epilogue runs inside it
+    // (pagedDecodeUnitsRope) when the head grouping allows;
+    // LLAISYS_DECODE_UNIT_ROPE=0 keeps the separate qkvRopeAppend launch.
+    bool unit_rope_ = true;
     void chooseDecodeAttention(size_t B, int32_t min_ctx, int32_t max_ctx);
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
     std::map<size_t, DecodeGraph> graphs_;       // one step (step())

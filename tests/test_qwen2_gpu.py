@@ -123,16 +123,21 @@ def test_wide_decode_batches_match(nseq):
         check_token(nxt[r], ref, check_logits(logits[r], ref))
 
 
-@pytest.mark.parametrize("units", ["1", "0"])
-def test_decode_attention_one_workgroup_per_unit(monkeypatch, units):
+@pytest.mark.parametrize("shape,units,rope", [("tiny", "1", "1"), ("tiny", "1", "0"), ("tiny", "0", "1"),
+                                               ("gqa12", "1", "1")])
+def test_decode_attention_one_workgroup_per_unit(monkeypatch, shape, units, rope):
     # 70 sequences x 2 kv heads = 140 units of 300-590 context tokens: within
     # 2x of each other, so decode steps take the one-workgroup-per-unit
-    # attention (LLAISYS_DECODE_UNITS=1) instead of the stream-K kernel (=0).
-    # Both against transformers; a multi-step decode call (one captured
-    # graph, lengths growing) against single steps.
+    # attention (LLAISYS_DECODE_UNITS=1) instead of the stream-K kernel (=0),
+    # with the QKV epilogue (bias, 1/rms, RoPE, k/v append) inside it
+    # (LLAISYS_DECODE_UNIT_ROPE=1) or in its own launch (=0); gqa12 has the
+    # 1.5B model's 6 query heads per kv head. Each against transformers; a
+    # multi-step decode call (one captured graph, lengths growing) against
+    # single steps.
     monkeypatch.setenv("LLAISYS_DECODE_UNITS", units)
+    monkeypatch.setenv("LLAISYS_DECODE_UNIT_ROPE", rope)
     nseq = 70
-    model, hf = build("tiny", num_blocks=nseq * 40 + 8)
+    model, hf = build(shape, num_blocks=nseq * 40 + 8)
     lens = [300 + (i * 37) % 291 for i in range(nseq)]
     prompts = [prompt(n, model.meta.voc, 500 + i) for i, n in enumerate(lens)]
     ids = [model.create_sequence()[0] for _ in prompts]
@@ -153,6 +158,35 @@ def test_decode_attention_one_workgroup_per_unit(monkeypatch, units):
         single.append(cur)
     assert L.device_error_flags() == 0
     assert np.array_equal(np.asarray(multi), np.asarray(single, np.int64))
+
+
+def test_fused_qkv_epilogue_matches_separate_launch(monkeypatch):
+    # The unit attention with the QKV epilogue fused in against the same
+    # model with qkvRopeAppend in its own launch, step by step over 4 decode
+    # steps of 66 sequences (132 units): the k/v each step appends feed every
+    # later step, so a wrong slot, rotation or scale shows up in the logits.
+    # The row 1/rms is summed in a different order, so logits agree to bf16
+    # rounding, not bit for bit.
+    monkeypatch.setenv("LLAISYS_DECODE_UNITS", "1")
+    nseq = 66
+    lens = [200 + (i * 53) % 190 for i in range(nseq)]
+    runs = []
+    for rope in ("1", "0"):
+        monkeypatch.setenv("LLAISYS_DECODE_UNIT_ROPE", rope)
+        model, _ = build("gqa12", num_blocks=nseq * 30 + 8)
+        prompts = [prompt(n, model.meta.voc, 900 + i) for i, n in enumerate(lens)]
+        ids = [model.create_sequence()[0] for _ in prompts]
+        for s in range(0, nseq, 11):
+            model.step(ids[s:s + 11], prompts[s:s + 11])
+        steps = []
+        for k in range(4):  # the same fed tokens in both runs
+            model.step(ids, [[t] for t in prompt(nseq, model.meta.voc, 950 + k)])
+            steps.append(to_torch(model.logits()).float().clone())
+        assert L.device_error_flags() == 0
+        runs.append(steps)
+        del model
+    for lg_a, lg_b in zip(*runs):
+        assert (lg_a - lg_b).abs().max().item() <= 1e-2 * lg_b.abs().max().item()
 
 
 def test_infer_restarts_on_a_new_history_and_reuses_cached_blocks():
