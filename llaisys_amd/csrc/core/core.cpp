@@ -44,6 +44,7 @@ Runtime::~Runtime() {
         if (slot_hdr_) api_->free_device(slot_hdr_);
         if (slot_rec_) api_->free_device(slot_rec_);
         if (error_word_) api_->free_device(error_word_);
+        if (queue_counters_) api_->free_device(queue_counters_);
         api_->destroy_stream(stream_);
     } catch (...) {
     }
@@ -111,6 +112,16 @@ int *Runtime::errorWord() {
         api_->device_synchronize();
     }
     return error_word_;
+}
+
+int *Runtime::queueCounters() {
+    LLAISYS_CHECK(type_ == LLAISYS_DEVICE_AMD, "device workspace exists on AMD runtimes only");
+    if (!queue_counters_) {
+        queue_counters_ = static_cast<int *>(api_->malloc_device(2 * sizeof(int)));
+        if (hipMemset(queue_counters_, 0, 2 * sizeof(int)) != hipSuccess) LLAISYS_RAISE("hipMemset failed");
+        api_->device_synchronize();
+    }
+    return queue_counters_;
 }
 
 int Runtime::takeErrorFlags() {

@@ -91,6 +91,9 @@ public:
     // One int32 of kernel-side error bits (device memory on AMD; on CPU a host
     // word the host ops raise bits in, read and cleared the same way).
     int *errorWord();
+    // Two int32 work-queue counters for persistent kernels, zeroed once; the
+    // kernels return them to zero before they end.
+    int *queueCounters();
     int takeErrorFlags();
     // Zero the error word in stream order, without waiting: a caller that
     // checks its own launches' flags afterwards is not failed by bits an
@@ -108,6 +111,7 @@ private:
     void *scratch_ = nullptr;
     size_t scratch_bytes_ = 0;
     int *error_word_ = nullptr;
+    int *queue_counters_ = nullptr;
     int host_error_word_ = 0;
     int *slot_hdr_ = nullptr;
     size_t slot_hdr_ints_ = 0;

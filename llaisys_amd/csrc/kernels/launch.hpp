@@ -102,10 +102,13 @@ struct PagedAttentionPlan {
     size_t partial_bytes; // workspace for split records
 };
 PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages);
+// queue: two zeroed int32 counters that persist between calls (the
+// persistent kernel's work queue, left zero when it ends), or null for one
+// workgroup per (block, split) slot.
 void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                   const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                   int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
-                  float *records, int *err, void *stream);
+                  float *records, int *err, int *queue, void *stream);
 
 // ---- model ops (model_ops.hip, linear.cpp)
 constexpr int kMaxDims = 8;

@@ -28,6 +28,8 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
+#include <vector>
 
 namespace llaisys::kernels {
 
@@ -51,6 +53,7 @@ struct Args {
     const int32_t *cu_q;
     float *records;
     int *err;
+    int *queue; // prefillQueueKernel: {next item, workgroups done}, zero between launches
     int B, T, nh, nkvh, G, max_pages, num_blocks, pps, max_splits, units, block_units, block_units_padded;
     float scale_log2;
 };
@@ -134,35 +137,25 @@ template <bool OUT_F32> __device__ __forceinline__ f32x4 loadRecordO(const float
     }
 }
 
+typedef u32x4 StageBuf[2][kStagePairs * 16 * 64]; // page pairs: K a, K b, V a, V b quarters
+
+// One (block, split) of a unit: kv head h of sequence b's query block `block`
+// (groups block * kWaves .. + kWaves - 1 of its groups_b; group_base groups
+// before the sequence), pages [split * pps, ...) of its t.npages. Called by
+// every wave of the workgroup with the same arguments (it has barriers).
 template <bool OUT_F32>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) prefillKernel(Args a) {
-    __shared__ u32x4 kvs[2][kStagePairs * 16 * 64]; // page pairs: K a, K b, V a, V b quarters
+__device__ __forceinline__ void prefillItem(const Args &a, StageBuf &kvs, int b, int block, int group_base, int h,
+                                            int split, int groups_b, const TileGeom &t) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // uniform: scalar branches on it
     const int lane = threadIdx.x & 63;
     const int n = lane & 15;
     const int grp = lane >> 4;
-    const int split = blockIdx.x / a.block_units_padded;
-    const int wunit = blockIdx.x - split * a.block_units_padded;
-    if (wunit >= a.block_units) return;
-    const int h = wunit % a.nkvh;
-    int b, block, group_base;
-    if (!locate(a, wunit / a.nkvh, true, b, block, group_base)) return;
-    b = __builtin_amdgcn_readfirstlane(b);
-    block = __builtin_amdgcn_readfirstlane(block);
-    group_base = __builtin_amdgcn_readfirstlane(group_base);
-    TileGeom t;
-    if (!blockGeom(a, b, block, t, split == 0 && wave == 0)) return;
-    // The geometry is wave-uniform: scalar registers, scalar branches.
-    t.q0 = __builtin_amdgcn_readfirstlane(t.q0);
-    t.Lq = __builtin_amdgcn_readfirstlane(t.Lq);
-    t.ctx = __builtin_amdgcn_readfirstlane(t.ctx);
-    t.npages = __builtin_amdgcn_readfirstlane(t.npages);
     const int G = a.G;
     const int p0 = split * a.pps;
     if (p0 >= t.npages) return;
     const int p1 = min(t.npages, p0 + a.pps);
     const int group = block * kWaves + wave;        // this wave's group in the sequence
-    const bool active = group < __builtin_amdgcn_readfirstlane(groupsOf(a, b));
+    const bool active = group < groups_b;
 
     // Columns of the wave's tiles.
     int qi[kTiles], g[kTiles], pos[kTiles];
@@ -352,6 +345,181 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
 }
 
+template <bool OUT_F32>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) prefillKernel(Args a) {
+    __shared__ StageBuf kvs;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int split = blockIdx.x / a.block_units_padded;
+    const int wunit = blockIdx.x - split * a.block_units_padded;
+    if (wunit >= a.block_units) return;
+    const int h = wunit % a.nkvh;
+    int b, block, group_base;
+    if (!locate(a, wunit / a.nkvh, true, b, block, group_base)) return;
+    b = __builtin_amdgcn_readfirstlane(b);
+    block = __builtin_amdgcn_readfirstlane(block);
+    group_base = __builtin_amdgcn_readfirstlane(group_base);
+    TileGeom t;
+    if (!blockGeom(a, b, block, t, split == 0 && wave == 0)) return;
+    // The geometry is wave-uniform: scalar registers, scalar branches.
+    t.q0 = __builtin_amdgcn_readfirstlane(t.q0);
+    t.Lq = __builtin_amdgcn_readfirstlane(t.Lq);
+    t.ctx = __builtin_amdgcn_readfirstlane(t.ctx);
+    t.npages = __builtin_amdgcn_readfirstlane(t.npages);
+    prefillItem<OUT_F32>(a, kvs, b, block, group_base, h, split, __builtin_amdgcn_readfirstlane(groupsOf(a, b)), t);
+}
+
+// Exclusive prefix sum of v[0..n) in place (n <= 64 * 64), by the whole
+// workgroup; returns the total. tmp: 65 ints of LDS. Barriers inside.
+__device__ int blockExclusiveScan(int *v, int n, int *tmp) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nch = (n + 63) >> 6;
+    for (int ch = wave; ch < nch; ch += kWaves) {
+        const int i = ch * 64 + lane;
+        const int x = i < n ? v[i] : 0;
+        const int incl = waveInclusiveSum(x);
+        if (i < n) v[i] = incl - x;
+        if (lane == 63) tmp[ch] = incl;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int x = lane < nch ? tmp[lane] : 0;
+        const int incl = waveInclusiveSum(x);
+        if (lane < nch) tmp[lane] = incl - x;
+        if (lane == 63) tmp[64] = incl;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 64 * kWaves) v[i] += tmp[i >> 6];
+    const int total = tmp[64];
+    __syncthreads();
+    return total;
+}
+
+// Largest i in [0, n) with v[i] <= x, for non-decreasing v with v[0] <= x.
+__device__ __forceinline__ int lastAtMost(const int *v, int n, int x) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (v[mid] <= x)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+// Persistent prefill: one workgroup per CU works through the (unit, split)
+// items of the batch instead of one workgroup per grid slot. A grid sized for
+// the host's upper bound of units (it cannot see the lengths) is mostly
+// empty workgroups, each spending a length lookup before it exits, and they
+// delay the dispatch of real ones; per-item lookups cost dependent global
+// round trips. Here every workgroup reads cu_q and ctx once and builds the
+// item tables in LDS (per sequence: unit and group prefix sums; per unit: its
+// split count and prefix of full splits; the units whose last split is
+// partial), then takes items from a device counter: all full (pps-page)
+// splits first in unit order, then the partial last splits, so the longest
+// items start earliest. The last workgroup to finish returns the counter and
+// the done count to zero for the next launch. Items are the old kernel's
+// (block, split) workgroups, run by the same code with the same records.
+constexpr int kQueueMaxSeqs = 1024;
+constexpr int kQueueMaxUnits = 4000; // the unit scans (U + 1 entries) fit blockExclusiveScan
+
+__host__ __device__ constexpr size_t queueTableInts(int B, int units) {
+    return size_t(4) * (B + 1) + size_t(4) * (units + 1);
+}
+
+template <bool OUT_F32>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    prefillQueueKernel(Args a) {
+    __shared__ StageBuf kvs;
+    __shared__ int scan_tmp[65];
+    __shared__ int s_item[2];
+    extern __shared__ int tables[];
+    const int B = a.B, tid = threadIdx.x, nthreads = 64 * kWaves;
+    int *cu = tables, *ctx = cu + (B + 1), *ubase = ctx + (B + 1), *gbase = ubase + (B + 1);
+    int *nspl = gbase + (B + 1), *fpre = nspl + (a.block_units + 1), *ppos = fpre + (a.block_units + 1);
+    int *punit = ppos + (a.block_units + 1);
+    for (int i = tid; i <= B; i += nthreads) {
+        cu[i] = a.cu_q[i];
+        ctx[i] = i < B ? a.ctx[i] : 0;
+    }
+    __syncthreads();
+    // Per sequence: units (blocks x kv heads) and groups, as groupsOf counts
+    // them (sequences with bad geometry keep their slots but get no items).
+    for (int b = tid; b <= B; b += nthreads) {
+        int ng = 0;
+        if (b < B) {
+            const int lq = cu[b + 1] - cu[b];
+            ng = lq >= 2 ? (((lq * a.G + 15) >> 4) + kTiles - 1) / kTiles : 0;
+        }
+        gbase[b] = ng;
+        ubase[b] = (ng + kWaves - 1) / kWaves * a.nkvh;
+    }
+    __syncthreads();
+    blockExclusiveScan(gbase, B + 1, scan_tmp);
+    const int U = min(blockExclusiveScan(ubase, B + 1, scan_tmp), a.block_units);
+    // Per unit: splits, full splits, partial flag.
+    for (int u = tid; u <= U; u += nthreads) {
+        int ns = 0, full = 0;
+        if (u < U) {
+            const int b = lastAtMost(ubase, B, u);
+            const int j = (u - ubase[b]) / a.nkvh;
+            const int q0 = cu[b], lq = cu[b + 1] - q0, c = ctx[b];
+            if (q0 < 0 || q0 + lq > a.T || c > a.max_pages * 16 || lq > c) {
+                if (blockIdx.x == 0 && u == ubase[b]) atomicOr(a.err, kErrTooLong);
+            } else {
+                const int qi_max = min(lq - 1, ((j + 1) * kWaves * kTiles * 16 - 1) / a.G);
+                const int np = (c - lq + qi_max + 1 + 15) >> 4;
+                ns = (np + a.pps - 1) / a.pps;
+                full = np - (ns - 1) * a.pps == a.pps ? ns : ns - 1;
+            }
+        }
+        nspl[u] = ns;
+        fpre[u] = full;
+        ppos[u] = ns > full ? 1 : 0;
+    }
+    __syncthreads();
+    const int n_full = blockExclusiveScan(fpre, U + 1, scan_tmp);
+    const int n_part = blockExclusiveScan(ppos, U + 1, scan_tmp);
+    for (int u = tid; u < U; u += nthreads)
+        if (nspl[u] > fpre[u + 1] - fpre[u]) punit[ppos[u]] = u;
+    __syncthreads();
+    const int n_items = n_full + n_part;
+    for (int it = 0;; ++it) {
+        if (tid == 0) s_item[it & 1] = atomicAdd(a.queue, 1);
+        __syncthreads();
+        const int item = __builtin_amdgcn_readfirstlane(s_item[it & 1]);
+        if (item >= n_items) break;
+        int u, split;
+        if (item < n_full) {
+            u = lastAtMost(fpre, U, item);
+            split = item - fpre[u];
+        } else {
+            u = punit[item - n_full];
+            split = nspl[u] - 1;
+        }
+        u = __builtin_amdgcn_readfirstlane(u);
+        split = __builtin_amdgcn_readfirstlane(split);
+        const int b = __builtin_amdgcn_readfirstlane(lastAtMost(ubase, B, u));
+        const int local = u - ubase[b];
+        const int block = local / a.nkvh, h = local - block * a.nkvh;
+        TileGeom t;
+        t.b = b;
+        t.q0 = __builtin_amdgcn_readfirstlane(cu[b]);
+        t.Lq = __builtin_amdgcn_readfirstlane(cu[b + 1]) - t.q0;
+        t.ctx = __builtin_amdgcn_readfirstlane(ctx[b]);
+        const int qi_max = min(t.Lq - 1, ((block + 1) * kWaves * kTiles * 16 - 1) / a.G);
+        t.npages = (t.ctx - t.Lq + qi_max + 1 + 15) >> 4;
+        t.nsplit = __builtin_amdgcn_readfirstlane(nspl[u]);
+        const int group_base = __builtin_amdgcn_readfirstlane(gbase[b]);
+        const int groups_b = __builtin_amdgcn_readfirstlane(gbase[b + 1]) - group_base;
+        prefillItem<OUT_F32>(a, kvs, b, block, group_base, h, split, groups_b, t);
+    }
+    if (tid == 0 && atomicAdd(a.queue + 1, 1) == int(gridDim.x) - 1) {
+        atomicExch(a.queue, 0);
+        atomicExch(a.queue + 1, 0);
+    }
+}
+
 // Merge the split records of each unit with more than one split.
 constexpr int kMergeBatch = 4;
 
@@ -416,6 +584,21 @@ int envInt(const char *name, int fallback) {
     return std::atoi(v);
 }
 
+// LDS left for the persistent kernel's item tables beside its 64 KiB of
+// stages (160 KiB per CU on gfx950, one workgroup per CU).
+constexpr size_t kQueueTableBytes = size_t(80) << 10;
+
+int cuCount() {
+    static std::mutex mu;
+    static std::vector<int> cache;
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    if (size_t(dev) >= cache.size()) cache.resize(dev + 1, 0);
+    if (!cache[dev]) HIP_CHECK(hipDeviceGetAttribute(&cache[dev], hipDeviceAttributeMultiprocessorCount, dev));
+    return cache[dev];
+}
+
 } // namespace
 
 PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages) {
@@ -437,7 +620,7 @@ PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages)
 void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                   const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                   int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
-                  float *records, int *err, void *stream) {
+                  float *records, int *err, int *queue, void *stream) {
     if (B == 0 || T == 0) return;
     Args a;
     a.q = q;
@@ -449,6 +632,7 @@ void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_
     a.cu_q = cu_q;
     a.records = records;
     a.err = err;
+    a.queue = queue;
     a.B = B;
     a.T = T;
     a.nh = nh;
@@ -464,11 +648,24 @@ void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_
     a.scale_log2 = scale * 1.4426950408889634f;
     const dim3 grid(plan.block_units_padded * plan.max_splits), block(64 * kWaves), cblock(64);
     auto s = static_cast<hipStream_t>(stream);
+    // The persistent kernel whenever its item tables fit in LDS beside the
+    // stages (and a counter buffer is given); otherwise one workgroup per
+    // grid slot.
+    const size_t table_bytes = queueTableInts(B, plan.block_units) * sizeof(int);
+    const bool queued = queue && envInt("LLAISYS_PREFILL_QUEUE", 1) != 0 && B <= kQueueMaxSeqs &&
+                        plan.block_units <= kQueueMaxUnits && table_bytes <= kQueueTableBytes;
+    const dim3 qgrid(unsigned(std::min<long long>(cuCount(), (long long)plan.block_units * plan.max_splits)));
     if (out_f32) {
-        hipLaunchKernelGGL((prefillKernel<true>), grid, block, 0, s, a);
+        if (queued)
+            hipLaunchKernelGGL((prefillQueueKernel<true>), qgrid, block, unsigned(table_bytes), s, a);
+        else
+            hipLaunchKernelGGL((prefillKernel<true>), grid, block, 0, s, a);
         if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<true>), dim3(plan.units * kTiles), cblock, 0, s, a);
     } else {
-        hipLaunchKernelGGL((prefillKernel<false>), grid, block, 0, s, a);
+        if (queued)
+            hipLaunchKernelGGL((prefillQueueKernel<false>), qgrid, block, unsigned(table_bytes), s, a);
+        else
+            hipLaunchKernelGGL((prefillKernel<false>), grid, block, 0, s, a);
         if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<false>), dim3(plan.units * kTiles), cblock, 0, s, a);
     }
     HIP_CHECK(hipGetLastError());

@@ -345,7 +345,7 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
     K::pagedDecode(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
                    scale, dplan, records, rt.errorWord(), slot_hdr, slot_rec, rt.stream());
     K::pagedPrefill(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
-                    scale, pplan, records, rt.errorWord(), rt.stream());
+                    scale, pplan, records, rt.errorWord(), rt.queueCounters(), rt.stream());
 }
 
 // No counterpart in the reference: the decode above for callers that cannot

@@ -124,6 +124,54 @@ def test_varlen_split_invariance(pps, monkeypatch):
     check(run_varlen(case, q, cu_q, torch.float32), run_varlen(case, q, cu_q, torch.bfloat16), ref)
 
 
+@pytest.mark.parametrize("pps", ["2", "16", "64"])
+def test_prefill_work_queue_matches_one_workgroup_per_split(pps, monkeypatch):
+    # The persistent prefill kernel (item tables built in LDS, items taken
+    # from a device counter, full splits first) runs the same per-item code
+    # as the kernel with one workgroup per (block, split) grid slot: outputs
+    # are bit-identical, also over repeated calls (the counter and the done
+    # count return to zero at the end of each launch).
+    ctx = np.array([700, 33, 1300, 90, 2049, 18], np.int32)
+    lq = np.array([300, 1, 257, 90, 2, 18], np.int32)
+    case = make_case(27, ctx)
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = queries(28, int(cu_q[-1]), 12)
+    monkeypatch.setenv("LLAISYS_PAGES_PER_SPLIT", pps)
+    monkeypatch.setenv("LLAISYS_PREFILL_QUEUE", "0")
+    grid = [run_varlen(case, q, cu_q, dt) for dt in (torch.float32, torch.bfloat16)]
+    monkeypatch.setenv("LLAISYS_PREFILL_QUEUE", "1")
+    for _ in range(3):
+        for dt, want in zip((torch.float32, torch.bfloat16), grid):
+            assert np.array_equal(run_varlen(case, q, cu_q, dt), want)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE, cu_q=cu_q)
+    check(grid[0], grid[1], ref)
+
+
+def test_prefill_bad_geometry_flags_error():
+    # A multi-query sequence with more new tokens than context (Lq > ctx) is
+    # skipped with error bit 2; the other sequences' rows come out as when
+    # that sequence is valid.
+    ctx = np.array([64, 10, 80], np.int32)
+    lq = np.array([16, 12, 20], np.int32)
+    case = make_case(29, ctx)
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = to_llaisys(from_bits(queries(30, int(cu_q[-1]), 12)))
+    kp, vp = case.device_pools()
+    table, _ = case.device_meta()
+    rows = np.r_[cu_q[0]:cu_q[1], cu_q[2]:cu_q[3]]
+    outs = []
+    for c1 in (10, 12):  # 12 new tokens over a 10-token context, then over 12
+        out = to_llaisys(torch.zeros((int(cu_q[-1]), 12, 128), dtype=torch.float32, device="cuda"))
+        c = ctx.copy()
+        c[1] = c1
+        L.Ops.paged_attention_varlen(out, q, kp, vp, table, to_llaisys(torch.from_numpy(cu_q)),
+                                     to_llaisys(torch.from_numpy(c)), SCALE)
+        flags = L.device_error_flags()
+        assert bool(flags & 2) == (c1 == 10)
+        outs.append(to_torch(out).cpu().numpy()[rows])
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_decode_ignores_stale_nan_slots():
     ctx = np.array([5, 16, 33, 70, 129], np.int32)
     case = make_case(31, ctx, stale_nan=True, extra_pages=2)
