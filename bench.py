@@ -413,8 +413,11 @@ def run_decode(args):
             "batch": B, "ctx_range": [512, 8192], "ctx_total": int(ctx.sum()), "block_size": 16,
             "q_heads": 12, "kv_heads": 2, "head_dim": 128, "accumulate": "fp32",
             "split": "stream-K over page pairs, log-sum-exp combine kernel",
-            "waves": int(os.environ.get("LLAISYS_DECODE_WAVES",
-                                        torch.cuda.get_device_properties(0).multi_processor_count * 7 // 4)),
+            # the kernel's grid: 1.75 waves per CU, or more when the longest
+            # context needs them (a wave's slice is at most 64 page pairs)
+            "waves": max(int(os.environ.get("LLAISYS_DECODE_WAVES",
+                                            torch.cuda.get_device_properties(0).multi_processor_count * 7 // 4)),
+                         -(-B * 2 * ((insts[0].maxp + 1) // 2) // 64)),
         },
         "roofline": {
             "bound": "hbm",
