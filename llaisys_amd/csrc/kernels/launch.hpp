@@ -177,12 +177,13 @@ void swigluRows(uint16_t *act, const uint16_t *gate_up, const uint16_t *x, size_
 // out[r, c] = w[r, c] * g[c] (bf16, one rounding): an RMSNorm weight folded
 // into the columns of the projection that consumes the normalised rows.
 void foldNormColumns(uint16_t *out, const uint16_t *w, const uint16_t *g, size_t rows, int cols, void *stream);
-// Multi-step decode bookkeeping on the device (s = *counter): before a step,
-// ctx_before = base + s, ctx_after = base + s + 1, tok = s ? next : first;
-// after it, history[s][:] = next and *counter = s + 1.
-void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, const int32_t *base, const int64_t *first,
-                   const int64_t *next, const int32_t *counter, int B, void *stream);
-void decodeRecord(int64_t *history, const int64_t *next, int32_t *counter, int B, void *stream);
+// Multi-step decode bookkeeping on the device (s = *counter, the steps
+// started): before step s, history[s - 1][:] = next (s > 0), ctx_before =
+// base + s, ctx_after = base + s + 1, tok = s ? next : first, *counter = s + 1;
+// after the last step, decodeRecordLast sets history[*counter - 1][:] = next.
+void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, int64_t *history, const int32_t *base,
+                   const int64_t *first, const int64_t *next, int32_t *counter, int B, void *stream);
+void decodeRecordLast(int64_t *history, const int64_t *next, const int32_t *counter, int B, void *stream);
 // out [R, d] = rms_norm(x[rows ? rows[r] : r]) * w; d % 8 == 0.
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
                  void *stream);

@@ -207,41 +207,45 @@ __global__ void __launch_bounds__(64) rmsNormRowsKernel(uint16_t *out, const bf1
 }
 constexpr int kRowMaxVecs = 16; // d <= 16 * 64 * 8 = 8192
 
-// Multi-step decode: step s reads s from a device counter. Before the step:
-// lengths = base + s (before) and base + s + 1 (after), tokens = first at
-// s = 0 else the previous step's argmax. After it: history[s] = argmax, s + 1.
-// One block each (the counter is read by every thread before it moves).
+// Multi-step decode: step s reads s from a device counter (steps started).
+// Advance, at the start of step s: the previous step's argmax (next) goes
+// into history[s - 1], lengths = base + s (before) and base + s + 1 (after),
+// tokens = first at s = 0 else next, then the counter moves to s + 1 (after
+// every thread has read it). After the last step, decodeRecordLast writes
+// the final argmax into history[counter - 1]. One block each.
 __global__ void __launch_bounds__(kThreads) decodeAdvanceKernel(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok,
-                                                                const int32_t *base, const int64_t *first,
-                                                                const int64_t *next, const int32_t *counter, int B) {
+                                                                int64_t *history, const int32_t *base,
+                                                                const int64_t *first, const int64_t *next,
+                                                                int32_t *counter, int B) {
     const int s = *counter;
     for (int b = threadIdx.x; b < B; b += kThreads) {
+        if (s > 0) history[size_t(s - 1) * B + b] = next[b];
         ctx_before[b] = base[b] + s;
         ctx_after[b] = base[b] + s + 1;
         tok[b] = s == 0 ? first[b] : next[b];
     }
-}
-
-__global__ void __launch_bounds__(kThreads) decodeRecordKernel(int64_t *history, const int64_t *next, int32_t *counter,
-                                                               int B) {
-    const int s = *counter;
-    for (int b = threadIdx.x; b < B; b += kThreads) history[size_t(s) * B + b] = next[b];
     __syncthreads();
     if (threadIdx.x == 0) *counter = s + 1;
 }
 
+__global__ void __launch_bounds__(kThreads) decodeRecordLastKernel(int64_t *history, const int64_t *next,
+                                                                   const int32_t *counter, int B) {
+    const int s = *counter;
+    for (int b = threadIdx.x; b < B; b += kThreads) history[size_t(s - 1) * B + b] = next[b];
+}
+
 } // namespace
 
-void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, const int32_t *base, const int64_t *first,
-                   const int64_t *next, const int32_t *counter, int B, void *stream) {
+void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, int64_t *history, const int32_t *base,
+                   const int64_t *first, const int64_t *next, int32_t *counter, int B, void *stream) {
     hipLaunchKernelGGL(decodeAdvanceKernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), ctx_before,
-                       ctx_after, tok, base, first, next, counter, B);
+                       ctx_after, tok, history, base, first, next, counter, B);
     HIP_CHECK(hipGetLastError());
 }
 
-void decodeRecord(int64_t *history, const int64_t *next, int32_t *counter, int B, void *stream) {
-    hipLaunchKernelGGL(decodeRecordKernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), history, next,
-                       counter, B);
+void decodeRecordLast(int64_t *history, const int64_t *next, const int32_t *counter, int B, void *stream) {
+    hipLaunchKernelGGL(decodeRecordLastKernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), history,
+                       next, counter, B);
     HIP_CHECK(hipGetLastError());
 }
 

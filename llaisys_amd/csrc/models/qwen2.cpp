@@ -330,9 +330,10 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
 
 // Multi-step greedy decode: nsteps single-token steps of the batch with the
 // next token fed back on the device. Pages for all steps are reserved up
-// front and the table is uploaded once; each step is decodeAdvance (lengths,
-// tokens from a device step counter), forward(), decodeRecord (argmax into
-// the history, counter + 1) - one captured graph replayed nsteps times.
+// front and the table is uploaded once; each step is decodeAdvance (the
+// previous step's argmax into the history, lengths and tokens from a device
+// step counter, counter + 1) and forward() - one captured graph replayed
+// nsteps times - and one decodeRecordLast after the last step.
 void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, size_t nsteps, int64_t *out) {
     LLAISYS_CHECK(nseq > 0 && nsteps > 0, "qwen2 decode: no sequences or no steps");
     LLAISYS_CHECK(ids && first && out, "qwen2 decode: null argument");
@@ -402,9 +403,9 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
 
     void *s = rt.stream();
     auto oneStep = [&] {
-        K::decodeAdvance(i32(ctx_before_), i32(ctx_after_), i64(tok_), base, first_d, i64(next_), counter, int(B), s);
+        K::decodeAdvance(i32(ctx_before_), i32(ctx_after_), i64(tok_), history, base, first_d, i64(next_), counter,
+                         int(B), s);
         forward(B, B, true);
-        K::decodeRecord(history, i64(next_), counter, int(B), s);
     };
     size_t done = 0;
     if (use_graphs_) {
@@ -422,6 +423,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     } else {
         for (; done < nsteps; ++done) oneStep();
     }
+    K::decodeRecordLast(history, i64(next_), counter, int(B), s);
 
     int64_t *hout = h64 + 3 * B;
     api->memcpy_async(hout, history, nsteps * B * sizeof(int64_t), LLAISYS_MEMCPY_D2H, s);
