@@ -102,6 +102,12 @@ struct PagedAttentionPlan {
     size_t partial_bytes; // workspace for split records
 };
 PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages);
+// Whether pagedPrefill runs its persistent kernel (the work-queue counters
+// given, the batch's tables fit its LDS) and, then, whether that kernel also
+// takes the batch's single-query sequences (T != B), in which case the
+// caller runs no pagedDecode for them.
+bool prefillQueueUsable(int B, const PagedAttentionPlan &plan, const int *queue);
+bool prefillTakesDecode(int B, int T, const PagedAttentionPlan &plan, const int *queue);
 // queue: two zeroed int32 counters that persist between calls (the
 // persistent kernel's work queue, left zero when it ends), or null for one
 // workgroup per (block, split) slot.

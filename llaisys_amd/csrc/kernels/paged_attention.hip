@@ -54,6 +54,7 @@ struct Args {
     float *records;
     int *err;
     int *queue; // prefillQueueKernel: {next item, workgroups done}, zero between launches
+    int with_decode; // pagedPrefill runs prefillQueueKernel<, true>: the single-query sequences too
     int B, T, nh, nkvh, G, max_pages, num_blocks, pps, max_splits, units, block_units, block_units_padded;
     float scale_log2;
 };
@@ -368,6 +369,103 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     prefillItem<OUT_F32>(a, kvs, b, block, group_base, h, split, __builtin_amdgcn_readfirstlane(groupsOf(a, b)), t);
 }
 
+// One single-query sequence's kv head h (query row `row`, c keys) in the
+// persistent kernel: the workgroup's kWaves waves split its page pairs
+// evenly, stream them through a two-stage register ring into the decode MFMA
+// step, and merge their (O, m, l) through LDS (the stage buffers, idle
+// during this item); wave 0 writes the row. The decode kernel's math with
+// kWaves partial states instead of per-wave records.
+constexpr int kDecWindow = 64; // pairs per block-id window (one per lane)
+template <bool OUT_F32>
+__device__ __forceinline__ void decodeItem(const Args &a, StageBuf &kvs, int b, int h, int row, int c) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15;
+    const int grp = lane >> 4;
+    const int G = a.G;
+    const int np = (c + 15) >> 4;
+    const int npr = (np + 1) >> 1;
+    const int p0 = wave * npr / kWaves, p1 = (wave + 1) * npr / kWaves;
+    Acc acc;
+    acc.reset();
+    bool bad_block = false;
+    if (p1 > p0) {
+        u32x4 qop[4];
+        const uint16_t *qrow = a.q + (size_t(row) * a.nh + h * G + min(n, G - 1)) * kHeadDim + grp * 8;
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+            qop[t4] = *reinterpret_cast<const u32x4 *>(qrow + 32 * t4);
+            qop[t4] = n < G ? qop[t4] : u32x4{0, 0, 0, 0};
+        }
+        const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
+        const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
+        const int32_t *trow = a.table + size_t(b) * a.max_pages;
+        for (int base = p0; base < p1; base += kDecWindow) {
+            const int cnt = min(kDecWindow, p1 - base);
+            int bidA, bidB;
+            {
+                const int pa = 2 * (base + min(lane, cnt - 1));
+                bidA = trow[pa];
+                bidB = trow[min(pa + 1, np - 1)];
+            }
+            PagePair ring[2];
+            auto issue = [&](int st, int k) {
+                const int kk = min(k, cnt - 1);
+                int bA = __builtin_amdgcn_readlane(bidA, kk);
+                int bB = __builtin_amdgcn_readlane(bidB, kk);
+                const bool bad = unsigned(bA) >= unsigned(a.num_blocks) || unsigned(bB) >= unsigned(a.num_blocks);
+                bad_block |= bad;
+                bA = bad ? 0 : bA;
+                bB = bad ? 0 : bB;
+                loadPair(ring[st], kp, vp, (size_t(bA) * a.nkvh + h) * 256, (size_t(bB) * a.nkvh + h) * 256);
+            };
+            issue(0, 0);
+            issue(1, 1);
+            for (int k0 = 0; k0 < cnt; k0 += 2) {
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const int k = k0 + st;
+                    if (k < cnt) {
+                        const int j = base + k;
+                        consumePair<OUT_F32>(acc, ring[st], qop, 32 * j, c - 1, c, 2 * j + 1 < np, grp, a.scale_log2);
+                    }
+                    issue(st, k + 2);
+                }
+            }
+        }
+    }
+    if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
+    float lt = acc.l + __shfl_xor(acc.l, 16);
+    lt += __shfl_xor(lt, 32);
+    f32x4 *part_o = reinterpret_cast<f32x4 *>(&kvs[0][0]);                 // [kWaves - 1][8][64]
+    float *part_ml = reinterpret_cast<float *>(part_o + (kWaves - 1) * 8 * 64); // [kWaves - 1][2][64]
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) part_o[((wave - 1) * 8 + i) * 64 + lane] = acc.o[i];
+        part_ml[((wave - 1) * 2 + 0) * 64 + lane] = acc.m;
+        part_ml[((wave - 1) * 2 + 1) * 64 + lane] = lt;
+    }
+    __syncthreads();
+    if (wave == 0 && n < G) {
+        float M = acc.m, L = lt;
+        for (int v = 0; v < kWaves - 1; ++v) {
+            const float mv = part_ml[(v * 2 + 0) * 64 + lane];
+            if (mv == -INFINITY) continue;
+            const float Mn = fmaxf(M, mv);
+            const float sa = exp2Fast(M - Mn);
+            const float sb = exp2Fast(mv - Mn);
+            L = L * sa + part_ml[(v * 2 + 1) * 64 + lane] * sb;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc.o[i] = acc.o[i] * sa + part_o[(v * 8 + i) * 64 + lane] * sb;
+            M = Mn;
+        }
+        const float inv = 1.f / L;
+        const size_t orow = (size_t(row) * a.nh + h * G + n) * kHeadDim;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, orow, i, grp, acc.o[i] * inv);
+    }
+}
+
 // Exclusive prefix sum of v[0..n) in place (n <= 64 * 64), by the whole
 // workgroup; returns the total. tmp: 65 ints of LDS. Barriers inside.
 __device__ int blockExclusiveScan(int *v, int n, int *tmp) {
@@ -420,14 +518,20 @@ __device__ __forceinline__ int lastAtMost(const int *v, int n, int x) {
 // items start earliest. The last workgroup to finish returns the counter and
 // the done count to zero for the next launch. Items are the old kernel's
 // (block, split) workgroups, run by the same code with the same records.
+// WITH_DECODE: the batch's single-query sequences are items too, one per kv
+// head (decodeItem), placed between the full and the partial splits, longest
+// context first; their HBM-bound streams then run beside the splits' MFMA
+// work, and no decode kernel or decode combine runs for them. (Ordering the
+// whole tail by an estimated time instead measured no better with decode
+// items and 4 us worse for prefill-only batches.)
 constexpr int kQueueMaxSeqs = 1024;
 constexpr int kQueueMaxUnits = 4000; // the unit scans (U + 1 entries) fit blockExclusiveScan
 
 __host__ __device__ constexpr size_t queueTableInts(int B, int units) {
-    return size_t(4) * (B + 1) + size_t(4) * (units + 1);
+    return size_t(6) * (B + 1) + size_t(4) * (units + 1);
 }
 
-template <bool OUT_F32>
+template <bool OUT_F32, bool WITH_DECODE>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
     prefillQueueKernel(Args a) {
     __shared__ StageBuf kvs;
@@ -437,7 +541,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const int B = a.B, tid = threadIdx.x, nthreads = 64 * kWaves;
     int *cu = tables, *ctx = cu + (B + 1), *ubase = ctx + (B + 1), *gbase = ubase + (B + 1);
     int *nspl = gbase + (B + 1), *fpre = nspl + (a.block_units + 1), *ppos = fpre + (a.block_units + 1);
-    int *punit = ppos + (a.block_units + 1);
+    int *punit = ppos + (a.block_units + 1), *dkey = punit + (a.block_units + 1), *dseq = dkey + (B + 1);
+    __shared__ int s_ndec;
     for (int i = tid; i <= B; i += nthreads) {
         cu[i] = a.cu_q[i];
         ctx[i] = i < B ? a.ctx[i] : 0;
@@ -453,9 +558,40 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         }
         gbase[b] = ng;
         ubase[b] = (ng + kWaves - 1) / kWaves * a.nkvh;
+        // Single-query sequences (with_decode) with a valid query row and
+        // length are decode items (nkvh each; else error bit 2, no items):
+        // key = their length, -1 for the rest.
+        int key = -1;
+        if (WITH_DECODE && b < B && cu[b + 1] - cu[b] == 1) {
+            const int row = cu[b], c = ctx[b];
+            if (row < 0 || row >= a.T || c < 1 || c > a.max_pages * 16) {
+                if (blockIdx.x == 0) atomicOr(a.err, kErrTooLong);
+            } else {
+                key = c;
+            }
+        }
+        if (b < B) dkey[b] = key;
     }
+    if (tid == 0) s_ndec = 0;
     __syncthreads();
     blockExclusiveScan(gbase, B + 1, scan_tmp);
+    // Decode sequences longest first: dseq[rank] = b, the rank of b being
+    // the number of valid sequences with a longer context, or as long and
+    // listed earlier (deterministic, so every workgroup builds the same order).
+    for (int b = tid; WITH_DECODE && b < B; b += nthreads) {
+        const int kb = dkey[b];
+        if (kb < 0) continue;
+        int rank = 0;
+        for (int o = 0; o < B; ++o) {
+            const int ko = dkey[o];
+            rank += (ko > kb || (ko == kb && o < b)) ? 1 : 0;
+        }
+        dseq[rank] = b;
+        atomicAdd(&s_ndec, 1);
+    }
+    __syncthreads();
+    const int n_dec_seqs = s_ndec;
+    const int n_dec = n_dec_seqs * a.nkvh;
     const int U = min(blockExclusiveScan(ubase, B + 1, scan_tmp), a.block_units);
     // Per unit: splits, full splits, partial flag.
     for (int u = tid; u <= U; u += nthreads) {
@@ -483,36 +619,47 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     for (int u = tid; u < U; u += nthreads)
         if (nspl[u] > fpre[u + 1] - fpre[u]) punit[ppos[u]] = u;
     __syncthreads();
-    const int n_items = n_full + n_part;
+    const int n_items = n_full + n_part + n_dec;
     for (int it = 0;; ++it) {
         if (tid == 0) s_item[it & 1] = atomicAdd(a.queue, 1);
         __syncthreads();
         const int item = __builtin_amdgcn_readfirstlane(s_item[it & 1]);
         if (item >= n_items) break;
-        int u, split;
-        if (item < n_full) {
-            u = lastAtMost(fpre, U, item);
-            split = item - fpre[u];
-        } else {
-            u = punit[item - n_full];
-            split = nspl[u] - 1;
+        // Order: the full prefill splits, the single-query sequences' kv heads
+        // (longest first), then the partial last splits.
+        const bool dec_item = WITH_DECODE && item >= n_full && item < n_full + n_dec;
+        if (!dec_item) {
+            int u, split;
+            if (item < n_full) {
+                u = lastAtMost(fpre, U, item);
+                split = item - fpre[u];
+            } else {
+                u = punit[item - n_full - n_dec];
+                split = nspl[u] - 1;
+            }
+            u = __builtin_amdgcn_readfirstlane(u);
+            split = __builtin_amdgcn_readfirstlane(split);
+            const int b = __builtin_amdgcn_readfirstlane(lastAtMost(ubase, B, u));
+            const int local = u - ubase[b];
+            const int block = local / a.nkvh, h = local - block * a.nkvh;
+            TileGeom t;
+            t.b = b;
+            t.q0 = __builtin_amdgcn_readfirstlane(cu[b]);
+            t.Lq = __builtin_amdgcn_readfirstlane(cu[b + 1]) - t.q0;
+            t.ctx = __builtin_amdgcn_readfirstlane(ctx[b]);
+            const int qi_max = min(t.Lq - 1, ((block + 1) * kWaves * kTiles * 16 - 1) / a.G);
+            t.npages = (t.ctx - t.Lq + qi_max + 1 + 15) >> 4;
+            t.nsplit = __builtin_amdgcn_readfirstlane(nspl[u]);
+            const int group_base = __builtin_amdgcn_readfirstlane(gbase[b]);
+            const int groups_b = __builtin_amdgcn_readfirstlane(gbase[b + 1]) - group_base;
+            prefillItem<OUT_F32>(a, kvs, b, block, group_base, h, split, groups_b, t);
+        } else if constexpr (WITH_DECODE) {
+            const int d = item - n_full;
+            const int b = __builtin_amdgcn_readfirstlane(dseq[d / a.nkvh]);
+            const int h = d - (d / a.nkvh) * a.nkvh;
+            decodeItem<OUT_F32>(a, kvs, b, h, __builtin_amdgcn_readfirstlane(cu[b]),
+                                __builtin_amdgcn_readfirstlane(ctx[b]));
         }
-        u = __builtin_amdgcn_readfirstlane(u);
-        split = __builtin_amdgcn_readfirstlane(split);
-        const int b = __builtin_amdgcn_readfirstlane(lastAtMost(ubase, B, u));
-        const int local = u - ubase[b];
-        const int block = local / a.nkvh, h = local - block * a.nkvh;
-        TileGeom t;
-        t.b = b;
-        t.q0 = __builtin_amdgcn_readfirstlane(cu[b]);
-        t.Lq = __builtin_amdgcn_readfirstlane(cu[b + 1]) - t.q0;
-        t.ctx = __builtin_amdgcn_readfirstlane(ctx[b]);
-        const int qi_max = min(t.Lq - 1, ((block + 1) * kWaves * kTiles * 16 - 1) / a.G);
-        t.npages = (t.ctx - t.Lq + qi_max + 1 + 15) >> 4;
-        t.nsplit = __builtin_amdgcn_readfirstlane(nspl[u]);
-        const int group_base = __builtin_amdgcn_readfirstlane(gbase[b]);
-        const int groups_b = __builtin_amdgcn_readfirstlane(gbase[b + 1]) - group_base;
-        prefillItem<OUT_F32>(a, kvs, b, block, group_base, h, split, groups_b, t);
     }
     if (tid == 0 && atomicAdd(a.queue + 1, 1) == int(gridDim.x) - 1) {
         atomicExch(a.queue, 0);
@@ -617,6 +764,18 @@ PagedAttentionPlan planPrefill(int B, int T, int nkvh, int group, int max_pages)
     return p;
 }
 
+bool prefillQueueUsable(int B, const PagedAttentionPlan &plan, const int *queue) {
+    return queue && envInt("LLAISYS_PREFILL_QUEUE", 1) != 0 && B <= kQueueMaxSeqs &&
+           plan.block_units <= kQueueMaxUnits &&
+           queueTableInts(B, plan.block_units) * sizeof(int) <= kQueueTableBytes;
+}
+
+bool prefillTakesDecode(int B, int T, const PagedAttentionPlan &plan, const int *queue) {
+    // A batch of single queries only (T == B) keeps the stream-K decode
+    // kernel, which balances sequences of very different lengths.
+    return T != B && prefillQueueUsable(B, plan, queue) && envInt("LLAISYS_PREFILL_TAKES_DECODE", 1) != 0;
+}
+
 void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                   const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                   int nkvh, int max_pages, int num_blocks, float scale, const PagedAttentionPlan &plan,
@@ -633,6 +792,7 @@ void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_
     a.records = records;
     a.err = err;
     a.queue = queue;
+    a.with_decode = 0;
     a.B = B;
     a.T = T;
     a.nh = nh;
@@ -652,18 +812,22 @@ void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_
     // stages (and a counter buffer is given); otherwise one workgroup per
     // grid slot.
     const size_t table_bytes = queueTableInts(B, plan.block_units) * sizeof(int);
-    const bool queued = queue && envInt("LLAISYS_PREFILL_QUEUE", 1) != 0 && B <= kQueueMaxSeqs &&
-                        plan.block_units <= kQueueMaxUnits && table_bytes <= kQueueTableBytes;
+    const bool queued = prefillQueueUsable(B, plan, queue);
+    a.with_decode = queued && prefillTakesDecode(B, T, plan, queue);
     const dim3 qgrid(unsigned(std::min<long long>(cuCount(), (long long)plan.block_units * plan.max_splits)));
     if (out_f32) {
-        if (queued)
-            hipLaunchKernelGGL((prefillQueueKernel<true>), qgrid, block, unsigned(table_bytes), s, a);
+        if (queued && a.with_decode)
+            hipLaunchKernelGGL((prefillQueueKernel<true, true>), qgrid, block, unsigned(table_bytes), s, a);
+        else if (queued)
+            hipLaunchKernelGGL((prefillQueueKernel<true, false>), qgrid, block, unsigned(table_bytes), s, a);
         else
             hipLaunchKernelGGL((prefillKernel<true>), grid, block, 0, s, a);
         if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<true>), dim3(plan.units * kTiles), cblock, 0, s, a);
     } else {
-        if (queued)
-            hipLaunchKernelGGL((prefillQueueKernel<false>), qgrid, block, unsigned(table_bytes), s, a);
+        if (queued && a.with_decode)
+            hipLaunchKernelGGL((prefillQueueKernel<false, true>), qgrid, block, unsigned(table_bytes), s, a);
+        else if (queued)
+            hipLaunchKernelGGL((prefillQueueKernel<false, false>), qgrid, block, unsigned(table_bytes), s, a);
         else
             hipLaunchKernelGGL((prefillKernel<false>), grid, block, 0, s, a);
         if (plan.max_splits > 1) hipLaunchKernelGGL((prefillCombineKernel<false>), dim3(plan.units * kTiles), cblock, 0, s, a);

@@ -340,12 +340,18 @@ void pagedAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k_po
     auto dplan = K::planDecode(int(B), int(nkvh), G, max_pages);
     auto pplan = K::planPrefill(int(B), int(T), int(nkvh), G, max_pages);
     float *records = static_cast<float *>(rt.scratch(std::max(dplan.record_bytes, pplan.partial_bytes)));
-    int *slot_hdr = dplan.slot_headers ? rt.decodeSlotHeaders(dplan.slot_headers) : nullptr;
-    void *slot_rec = dplan.slot_headers ? rt.decodeSlotRecords(dplan.slot_record_bytes) : nullptr;
-    K::pagedDecode(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
-                   scale, dplan, records, rt.errorWord(), slot_hdr, slot_rec, rt.stream());
+    int *queue = rt.queueCounters();
+    // The persistent prefill kernel takes the single-query sequences too
+    // when it runs (their HBM-bound work then overlaps the prefill's MFMA
+    // work); otherwise the decode kernel does.
+    if (!K::prefillTakesDecode(int(B), int(T), pplan, queue)) {
+        int *slot_hdr = dplan.slot_headers ? rt.decodeSlotHeaders(dplan.slot_headers) : nullptr;
+        void *slot_rec = dplan.slot_headers ? rt.decodeSlotRecords(dplan.slot_record_bytes) : nullptr;
+        K::pagedDecode(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
+                       scale, dplan, records, rt.errorWord(), slot_hdr, slot_rec, rt.stream());
+    }
     K::pagedPrefill(out->data(), f32, qp, kp, vp, tab, ctx, cu, int(B), int(T), int(nh), int(nkvh), max_pages, nb,
-                    scale, pplan, records, rt.errorWord(), rt.queueCounters(), rt.stream());
+                    scale, pplan, records, rt.errorWord(), queue, rt.stream());
 }
 
 // No counterpart in the reference: the decode above for callers that cannot

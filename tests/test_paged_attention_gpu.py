@@ -147,6 +147,41 @@ def test_prefill_work_queue_matches_one_workgroup_per_split(pps, monkeypatch):
     check(grid[0], grid[1], ref)
 
 
+def test_prefill_kernel_takes_decode_sequences(monkeypatch):
+    # The persistent prefill kernel also runs a mixed batch's single-query
+    # sequences (one item per kv head, all 8 waves, LDS merge) instead of the
+    # stream-K decode kernel: same results to fp32 rounding, repeated calls
+    # bit-identical, and a single-query sequence with an invalid length still
+    # raises error bit 2 and leaves its row alone.
+    ctx = np.array([700, 33, 1300, 1, 2049, 18, 4000, 250], np.int32)
+    lq = np.array([300, 1, 257, 1, 2, 1, 1, 1], np.int32)
+    case = make_case(35, ctx)
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = queries(36, int(cu_q[-1]), 12)
+    monkeypatch.setenv("LLAISYS_PREFILL_TAKES_DECODE", "0")
+    base = [run_varlen(case, q, cu_q, dt) for dt in (torch.float32, torch.bfloat16)]
+    monkeypatch.setenv("LLAISYS_PREFILL_TAKES_DECODE", "1")
+    got = [run_varlen(case, q, cu_q, dt) for dt in (torch.float32, torch.bfloat16)]
+    assert np.max(np.abs(got[0] - base[0])) <= 1e-5 * np.max(np.abs(base[0]))
+    assert np.max(np.abs(got[1] - base[1])) <= BF16_ABS
+    assert np.array_equal(run_varlen(case, q, cu_q, torch.float32), got[0])
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE, cu_q=cu_q)
+    check(got[0], got[1], ref)
+    # sequence 5 (one query) with length 0: flagged, its output row untouched
+    bad = ctx.copy()
+    bad[5] = 0
+    kp, vp = case.device_pools()
+    table, _ = case.device_meta()
+    out = to_llaisys(torch.full((int(cu_q[-1]), 12, 128), 7.0, dtype=torch.float32, device="cuda"))
+    L.Ops.paged_attention_varlen(out, to_llaisys(from_bits(q)), kp, vp, table, to_llaisys(torch.from_numpy(cu_q)),
+                                 to_llaisys(torch.from_numpy(bad)), SCALE)
+    assert L.device_error_flags() & 2
+    o = to_torch(out).cpu().numpy()
+    assert np.all(o[cu_q[5]] == 7.0)
+    rows = np.r_[cu_q[0]:cu_q[5], cu_q[6]:cu_q[-1]]
+    assert np.array_equal(o[rows], got[0][rows])
+
+
 def test_prefill_bad_geometry_flags_error():
     # A multi-query sequence with more new tokens than context (Lq > ctx) is
     # skipped with error bit 2; the other sequences' rows come out as when
