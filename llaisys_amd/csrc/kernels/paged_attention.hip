@@ -525,6 +525,7 @@ __device__ __forceinline__ int lastAtMost(const int *v, int n, int x) {
 // whole tail by an estimated time instead measured no better with decode
 // items and 4 us worse for prefill-only batches.)
 constexpr int kQueueMaxSeqs = 1024;
+constexpr int kQueueSortSeqs = 256; // decode items ranked by length up to this batch size
 constexpr int kQueueMaxUnits = 4000; // the unit scans (U + 1 entries) fit blockExclusiveScan
 
 __host__ __device__ constexpr size_t queueTableInts(int B, int units) {
@@ -577,7 +578,9 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     blockExclusiveScan(gbase, B + 1, scan_tmp);
     // Decode sequences longest first: dseq[rank] = b, the rank of b being
     // the number of valid sequences with a longer context, or as long and
-    // listed earlier (deterministic, so every workgroup builds the same order).
+    // listed earlier (deterministic, so every workgroup builds the same order;
+    // O(B^2), so the host gives this kernel the decode items only for batches
+    // of at most kQueueSortSeqs sequences).
     for (int b = tid; WITH_DECODE && b < B; b += nthreads) {
         const int kb = dkey[b];
         if (kb < 0) continue;
@@ -772,8 +775,11 @@ bool prefillQueueUsable(int B, const PagedAttentionPlan &plan, const int *queue)
 
 bool prefillTakesDecode(int B, int T, const PagedAttentionPlan &plan, const int *queue) {
     // A batch of single queries only (T == B) keeps the stream-K decode
-    // kernel, which balances sequences of very different lengths.
-    return T != B && prefillQueueUsable(B, plan, queue) && envInt("LLAISYS_PREFILL_TAKES_DECODE", 1) != 0;
+    // kernel, which balances sequences of very different lengths; so does a
+    // batch of more than kQueueSortSeqs sequences (the item order would cost
+    // more than it saves).
+    return T != B && B <= kQueueSortSeqs && prefillQueueUsable(B, plan, queue) &&
+           envInt("LLAISYS_PREFILL_TAKES_DECODE", 1) != 0;
 }
 
 void pagedPrefill(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
