@@ -20,8 +20,13 @@
 // kernel launched next merges them (the kernel boundary orders the records;
 // no fences, no waiting between waves).
 //
-// Workgroup ids are split-major over blocks padded to a multiple of 8, so all
-// splits of a block run on one XCD and share its L2 for the block's K/V pages.
+// Two launch forms run the same (block, split) code. By default a persistent
+// kernel (prefillQueueKernel, one workgroup per CU) takes the items from a
+// device counter, longest first, and for mixed batches of up to 256
+// sequences also the single-query sequences (decodeItem), so no decode
+// kernel runs beside it. Batches whose item tables do not fit its LDS use one
+// workgroup per grid slot (prefillKernel), slot ids split-major over blocks
+// padded to a multiple of 8.
 #include "mfma_common.hpp"
 
 #include "../device/hip_check.hpp"
