@@ -182,6 +182,21 @@ def test_prefill_kernel_takes_decode_sequences(monkeypatch):
     assert np.array_equal(o[rows], got[0][rows])
 
 
+@pytest.mark.parametrize("nseq", [300, 1100])
+def test_varlen_large_mixed_batches(nseq):
+    # Past 256 sequences the single queries go back to the stream-K decode
+    # kernel beside the persistent prefill kernel; past 1024 the prefill runs
+    # one workgroup per grid slot (its item tables no longer fit in LDS).
+    ctx = oracle.randint(37, nseq, 20, 120).astype(np.int32)
+    lq = np.ones(nseq, np.int32)
+    lq[::97] = np.minimum(ctx[::97], 17)  # a few multi-query sequences
+    case = make_case(38, ctx)
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = queries(39, int(cu_q[-1]), 12)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE, cu_q=cu_q, nthreads=16)
+    check(run_varlen(case, q, cu_q, torch.float32), run_varlen(case, q, cu_q, torch.bfloat16), ref)
+
+
 def test_prefill_bad_geometry_flags_error():
     # A multi-query sequence with more new tokens than context (Lq > ctx) is
     # skipped with error bit 2; the other sequences' rows come out as when
