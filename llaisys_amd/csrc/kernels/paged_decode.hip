@@ -552,13 +552,12 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
     // its bias; the new token's k dims (lane, lane + 64), v dims (2 lane,
     // 2 lane + 1) and their biases; the row's x for its 1/rms (the
     // projection row stands in when no norm is folded: read, not used).
-    // Issued first, before the length is known.
     const uint16_t *prow = ROPE ? r.qkv + size_t(b) * (a.nh + 2 * a.nkvh) * kHeadDim : nullptr;
     u32x4 qw[4], qb[4];
     uint32_t kw0 = 0, kw1 = 0, kb0 = 0, kb1 = 0, vw = 0, vb = 0;
     RowChunks xr;
     const int xd = r.x ? r.hs : 8;
-    if constexpr (ROPE) {
+    auto loadEpilogueInputs = [&]() {
         const int qcol = (h * G + min(n, G - 1)) * kHeadDim + grp * 8;
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) {
@@ -573,7 +572,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         vw = *reinterpret_cast<const uint32_t *>(prow + vcol + 2 * lane);
         vb = *reinterpret_cast<const uint32_t *>(r.bias + vcol + 2 * lane);
         xr.load(r.x ? r.x + size_t(b) * r.hs : prow, xd);
-    }
+    };
     int c = a.ctx[b];
     if (c < 1 || c > a.max_pages * 16) { // invalid length: zero output, error flag
         if (threadIdx.x == 0) atomicOr(a.err, kErrTooLong);
@@ -621,11 +620,12 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
     const int tok = (c - 1) & 15;
     bool issued = false; // the first window's first stages already in flight
     if constexpr (ROPE) {
-        // The epilogue's inputs are in flight since the kernel's start; the
-        // block-table window, the new token's block id and the first pages
-        // follow with no branch in between (loads clamped to valid addresses,
-        // results selected afterwards), so the epilogue's waits count only
-        // its own loads, not the pages behind them.
+        // Loads return in issue order, so the block-table window and the new
+        // token's block id go out first: the wait for them before the first
+        // pages' addresses then covers nothing else. The epilogue's inputs
+        // follow, then the first pages, with no branch in between (loads
+        // clamped to valid addresses, results selected afterwards), so the
+        // epilogue's waits count only the loads before the pages.
         __shared__ float2 trig[kUnitWaves][64];
         const int pos = c - 1;
         loadWindow();
@@ -636,6 +636,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         int slot_page = max(pos, 0) >> 4;
         asm volatile("" : "+v"(slot_page));
         const int blk = row[slot_page];
+        loadEpilogueInputs();
 #pragma unroll
         for (int st = 0; st < NSTAGE; ++st) issue(st, st);
         issued = true;
