@@ -612,13 +612,18 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
     if (!ROPE && p1 > p0) loadWindow();
 
     u32x4 qop[4];
-    // Fused epilogue (ROPE): wave 0 forms the new token's k and v and leaves
-    // them in LDS (kflat, vflat: bf16 by dim) for the last wave, which holds
-    // the unit's last pair.
+    // Fused epilogue (ROPE): the wave that holds the unit's last pair forms
+    // the new token's k and v after its loop (kflat, vflat: bf16 by dim, in
+    // LDS), patches them into that pair and stores them to the pool. Stores
+    // count in the same in-order counter as loads, so a store issued before
+    // the loop would hold up the waits on every page issued after it.
     __shared__ __align__(16) uint16_t kflat[ROPE ? kHeadDim : 8], vflat[ROPE ? kHeadDim : 8];
     const bool last_wave = ROPE && p1 > p0 && p1 == npr;
     const int tok = (c - 1) & 15;
     bool issued = false; // the first window's first stages already in flight
+    float rs = 1.f;      // the row's 1/rms (ROPE)
+    int blk = 0;         // the new token's block id (ROPE)
+    __shared__ float2 trig[ROPE ? kUnitWaves : 1][64];
     if constexpr (ROPE) {
         // Loads return in issue order, so the block-table window and the new
         // token's block id go out first: the wait for them before the first
@@ -626,7 +631,6 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         // follow, then the first pages, with no branch in between (loads
         // clamped to valid addresses, results selected afterwards), so the
         // epilogue's waits count only the loads before the pages.
-        __shared__ float2 trig[kUnitWaves][64];
         const int pos = c - 1;
         loadWindow();
         const bool qlive = c > 0 && n < G;
@@ -635,7 +639,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         // it would make the wave wait for every load issued before it).
         int slot_page = max(pos, 0) >> 4;
         asm volatile("" : "+v"(slot_page));
-        const int blk = row[slot_page];
+        blk = row[slot_page];
         loadEpilogueInputs();
 #pragma unroll
         for (int st = 0; st < NSTAGE; ++st) issue(st, st);
@@ -650,7 +654,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
             trig[wave][lane] = make_float2(sn, cs);
         }
         const float ss = xr.sumSquares(r.x ? r.x + size_t(b) * r.hs : prow, xd);
-        const float rs = r.x ? rsqrtf(ss / float(r.hs) + r.eps) : 1.f;
+        rs = r.x ? rsqrtf(ss / float(r.hs) + r.eps) : 1.f;
         __builtin_amdgcn_wave_barrier();
         // Query: rotate (j, j + 64) for the lane's 16 j; word w of chunk t4
         // holds dims grp * 8 + 32 t4 + 2 w, + 1, chunk t4 + 2 their partners.
@@ -677,36 +681,6 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
             }
 #pragma unroll
         for (int t4 = 0; t4 < 4; ++t4) qop[t4] = qlive ? qop[t4] : u32x4{0, 0, 0, 0};
-        if (wave == 0 && c > 0) {
-            // k: lane j rotates (j, j + 64) with the angle lane
-            // (j / 8 % 4) * 16 + (j / 32) * 8 + j % 8 worked out; v: 2 dims.
-            const float2 sc = trig[0][((lane >> 3) & 3) * 16 + (lane >> 5) * 8 + (lane & 7)];
-            const float x0 = rs * __uint_as_float(kw0 << 16) + __uint_as_float(kb0 << 16);
-            const float x1 = rs * __uint_as_float(kw1 << 16) + __uint_as_float(kb1 << 16);
-            const uint16_t k0 = __builtin_bit_cast(uint16_t, __float2bfloat16(x0 * sc.y - x1 * sc.x));
-            const uint16_t k1 = __builtin_bit_cast(uint16_t, __float2bfloat16(x1 * sc.y + x0 * sc.x));
-            const uint16_t v0 = __builtin_bit_cast(
-                uint16_t, __float2bfloat16(rs * __uint_as_float(vw << 16) + __uint_as_float(vb << 16)));
-            const uint16_t v1 = __builtin_bit_cast(
-                uint16_t, __float2bfloat16(rs * __uint_as_float(vw & 0xffff0000u) + __uint_as_float(vb & 0xffff0000u)));
-            kflat[lane] = k0;
-            kflat[lane + 64] = k1;
-            vflat[2 * lane] = v0;
-            vflat[2 * lane + 1] = v1;
-            // Stores into the page slot for later steps: lanes 0-15 the k
-            // chunks [d / 8][tok] (16 B each), every lane its 2 v dims.
-            if (unsigned(blk) >= unsigned(a.num_blocks)) {
-                if (lane == 0) atomicOr(a.err, kErrBadBlock);
-            } else {
-                const size_t page = (size_t(blk) * a.nkvh + h) * kPageElems;
-                __builtin_amdgcn_wave_barrier();
-                if (lane < 16)
-                    *reinterpret_cast<u32x4 *>(r.k_pool + page + kPageIndex(tok, 8 * lane)) =
-                        *reinterpret_cast<const u32x4 *>(&kflat[8 * lane]);
-                r.v_pool[page + vPageIndex(tok, 2 * lane)] = v0;
-                r.v_pool[page + vPageIndex(tok, 2 * lane + 1)] = v1;
-            }
-        }
     } else {
         const uint16_t *qrow = a.q + (size_t(b) * a.nh + h * G + min(n, G - 1)) * kHeadDim + grp * 8;
 #pragma unroll
@@ -739,14 +713,41 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         }
     }
     if constexpr (ROPE) {
-        // Wave 0's stash is visible after this barrier. Past the window's end
-        // every ring slot re-reads its last pair, so slot 0 holds the unit's
-        // last pair: patch in the new token, consume.
-        __syncthreads();
+        // Past the window's end every ring slot re-reads its last pair, so
+        // slot 0 holds the unit's last pair: form the new token's k and v,
+        // patch them in, consume, then store them into the page slot.
         if (last_wave) {
+            // k: lane j rotates (j, j + 64) with the angle lane
+            // (j / 8 % 4) * 16 + (j / 32) * 8 + j % 8 worked out; v: 2 dims.
+            const float2 sc = trig[wave][((lane >> 3) & 3) * 16 + (lane >> 5) * 8 + (lane & 7)];
+            const float x0 = rs * __uint_as_float(kw0 << 16) + __uint_as_float(kb0 << 16);
+            const float x1 = rs * __uint_as_float(kw1 << 16) + __uint_as_float(kb1 << 16);
+            const uint16_t k0 = __builtin_bit_cast(uint16_t, __float2bfloat16(x0 * sc.y - x1 * sc.x));
+            const uint16_t k1 = __builtin_bit_cast(uint16_t, __float2bfloat16(x1 * sc.y + x0 * sc.x));
+            const uint16_t v0 = __builtin_bit_cast(
+                uint16_t, __float2bfloat16(rs * __uint_as_float(vw << 16) + __uint_as_float(vb << 16)));
+            const uint16_t v1 = __builtin_bit_cast(
+                uint16_t, __float2bfloat16(rs * __uint_as_float(vw & 0xffff0000u) + __uint_as_float(vb & 0xffff0000u)));
+            kflat[lane] = k0;
+            kflat[lane + 64] = k1;
+            vflat[2 * lane] = v0;
+            vflat[2 * lane + 1] = v1;
+            __builtin_amdgcn_wave_barrier();
             const int j = npr - 1;
             patchNewToken(ring[0], kflat, vflat, tok, 2 * j == np - 1, lane);
             consumePair<OUT_F32>(acc, ring[0], qop, 32 * j, c - 1, c, 2 * j + 1 < np, grp, a.scale_log2);
+            // Stores into the page slot for later steps: lanes 0-15 the k
+            // chunks [d / 8][tok] (16 B each), every lane its 2 v dims.
+            if (unsigned(blk) >= unsigned(a.num_blocks)) {
+                if (lane == 0) atomicOr(a.err, kErrBadBlock);
+            } else {
+                const size_t page = (size_t(blk) * a.nkvh + h) * kPageElems;
+                if (lane < 16)
+                    *reinterpret_cast<u32x4 *>(r.k_pool + page + kPageIndex(tok, 8 * lane)) =
+                        *reinterpret_cast<const u32x4 *>(&kflat[8 * lane]);
+                r.v_pool[page + vPageIndex(tok, 2 * lane)] = v0;
+                r.v_pool[page + vPageIndex(tok, 2 * lane + 1)] = v1;
+            }
         }
     }
     if (bad_block && lane == 0) atomicOr(a.err, kErrBadBlock);
