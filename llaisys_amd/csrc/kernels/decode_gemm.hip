@@ -369,7 +369,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 // order.
 constexpr int kReduceBatch = 16;
 
-__global__ void splitKReduceKernel(uint16_t *y, const float *part, int M, int N, int S, int accumulate) {
+__global__ void splitKReduceKernel(uint16_t *y, const float *part, int M, int N, int S, int accumulate,
+                                   uint16_t *y_packed) {
     const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int n4 = N / 4;
     if (idx >= size_t(M) * n4) return;
@@ -395,7 +396,9 @@ __global__ void splitKReduceKernel(uint16_t *y, const float *part, int M, int N,
         const __bf16 b0 = (__bf16)a0, b1 = (__bf16)a1;
         return uint32_t(__builtin_bit_cast(uint16_t, b0)) | (uint32_t(__builtin_bit_cast(uint16_t, b1)) << 16);
     };
-    *reinterpret_cast<uint2 *>(y + size_t(m) * N + n) = make_uint2(pack(sum[0], sum[1]), pack(sum[2], sum[3]));
+    const uint2 out = make_uint2(pack(sum[0], sum[1]), pack(sum[2], sum[3]));
+    *reinterpret_cast<uint2 *>(y + size_t(m) * N + n) = out;
+    if (y_packed) *reinterpret_cast<uint2 *>(y_packed + packedRowIndex(m, n, N)) = out; // 4 elements, one 8 B piece
 }
 
 // About one workgroup per CU, at most kSplitMaxTiles k tiles per split (one
@@ -413,7 +416,114 @@ template <int MB> void launchSplitK(const SplitKArgs &a, hipStream_t st) {
     const size_t lds = size_t(16) * MB * 64 * sizeof(u32x4);
     hipLaunchKernelGGL((splitKGemmKernel<MB>), dim3((a.N / kSplitTileRows) * a.S), dim3(256), lds, st, a);
 }
+// Packed-X GEMM: workgroup (mt, nt) owns the 32 x 32 tile of Y at rows
+// 32 mt, columns 32 nt; wave w owns k tiles [12 w, 12 w + 12). Each wave
+// issues all 24 W tiles and 24 X tiles of its range (1 KiB each, 192
+// registers) and the old Y before its first MFMA: at M = 128 the time is
+// the workgroup's 192 KiB of operands reaching the CU, which a deeper
+// schedule cannot shorten. The four k partials meet in LDS; wave 0 adds
+// them in wave order (plus the old Y) and rounds once. An m block past the
+// last one re-reads the last (its rows are computed and dropped).
+constexpr int kPxTile = 2;   // 16-row blocks per tile side
+constexpr int kPxSteps = 12; // k tiles per wave (K = 4 x 12 x 32)
+
+template <bool ACC>
+__global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x4 *xp, const u32x4 *wp, int M,
+                                                         int N) {
+    __shared__ f32x4 red[3][kPxTile][kPxTile][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    constexpr int KT = 4 * kPxSteps;
+    const int ntiles = N / (16 * kPxTile);
+    const int mt = int(blockIdx.x) / ntiles, nt = int(blockIdx.x) % ntiles;
+    const int kb0 = wave * kPxSteps;
+    const int last_mb = (M - 1) >> 4;
+    u32x4 w[kPxSteps][kPxTile], xv[kPxSteps][kPxTile];
+#pragma unroll
+    for (int j = 0; j < kPxSteps; ++j) {
+#pragma unroll
+        for (int t = 0; t < kPxTile; ++t)
+            w[j][t] = __builtin_nontemporal_load(wp + (size_t(nt * kPxTile + t) * KT + kb0 + j) * 64 + lane);
+#pragma unroll
+        for (int i = 0; i < kPxTile; ++i) {
+            const int mb = min(mt * kPxTile + i, last_mb);
+            xv[j][i] = xp[(size_t(mb) * KT + kb0 + j) * 64 + lane];
+        }
+    }
+    // Lane holds C^T rows n0 + 0..3 of column m for each (t, i).
+    uint2 old_y[kPxTile][kPxTile];
+#pragma unroll
+    for (int t = 0; t < kPxTile; ++t)
+#pragma unroll
+        for (int i = 0; i < kPxTile; ++i) {
+            old_y[t][i] = make_uint2(0, 0);
+            const int m = min(16 * (mt * kPxTile + i) + (lane & 15), M - 1);
+            const int n0 = 16 * (nt * kPxTile + t) + 4 * (lane >> 4);
+            if (ACC && wave == 0) old_y[t][i] = *reinterpret_cast<const uint2 *>(y + size_t(m) * N + n0);
+        }
+    f32x4 acc[kPxTile][kPxTile];
+#pragma unroll
+    for (int t = 0; t < kPxTile; ++t)
+#pragma unroll
+        for (int i = 0; i < kPxTile; ++i) acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < kPxSteps; ++j)
+#pragma unroll
+        for (int t = 0; t < kPxTile; ++t)
+#pragma unroll
+            for (int i = 0; i < kPxTile; ++i) acc[t][i] = mfma(w[j][t], xv[j][i], acc[t][i]);
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < kPxTile; ++t)
+#pragma unroll
+            for (int i = 0; i < kPxTile; ++i) red[wave - 1][t][i][lane] = acc[t][i];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int t = 0; t < kPxTile; ++t)
+#pragma unroll
+        for (int i = 0; i < kPxTile; ++i) {
+            const uint2 o = old_y[t][i];
+            f32x4 v = ACC ? f32x4{__uint_as_float(o.x << 16), __uint_as_float(o.x & 0xffff0000u),
+                                  __uint_as_float(o.y << 16), __uint_as_float(o.y & 0xffff0000u)}
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+            v += acc[t][i];
+#pragma unroll
+            for (int r = 0; r < 3; ++r) v += red[r][t][i][lane];
+            const int m = 16 * (mt * kPxTile + i) + (lane & 15);
+            const int n0 = 16 * (nt * kPxTile + t) + 4 * (lane >> 4);
+            if (m < M) {
+                const __bf16 e0 = (__bf16)v[0], e1 = (__bf16)v[1], e2 = (__bf16)v[2], e3 = (__bf16)v[3];
+                const uint32_t w0 = uint32_t(__builtin_bit_cast(uint16_t, e0)) |
+                                    (uint32_t(__builtin_bit_cast(uint16_t, e1)) << 16);
+                const uint32_t w1 = uint32_t(__builtin_bit_cast(uint16_t, e2)) |
+                                    (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
+                *reinterpret_cast<uint2 *>(y + size_t(m) * N + n0) = make_uint2(w0, w1);
+            }
+        }
+}
 } // namespace
+
+bool packedXGemmSupported(int M, int N, int K) {
+    return M >= 1 && M <= kDecodeGemmMaxM && K == 4 * kPxSteps * 32 && N >= 32 && N % (16 * kPxTile) == 0;
+}
+
+void packedXGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed, int M, int N, int K,
+                 bool accumulate, void *stream) {
+    LLAISYS_CHECK(packedXGemmSupported(M, N, K),
+                  "packedXGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
+    const int mtiles = (M + 16 * kPxTile - 1) / (16 * kPxTile);
+    const dim3 grid(unsigned(mtiles * (N / (16 * kPxTile))));
+    auto st = static_cast<hipStream_t>(stream);
+    const auto *xp = reinterpret_cast<const u32x4 *>(x_packed);
+    const auto *wp = reinterpret_cast<const u32x4 *>(w_packed);
+    if (accumulate)
+        hipLaunchKernelGGL(packedXGemmKernel<true>, grid, dim3(256), 0, st, y, xp, wp, M, N);
+    else
+        hipLaunchKernelGGL(packedXGemmKernel<false>, grid, dim3(256), 0, st, y, xp, wp, M, N);
+    HIP_CHECK(hipGetLastError());
+}
 
 bool decodeGemmSupported(int M, int N, int K) {
     return M >= 1 && M <= kDecodeGemmMaxM && N >= 16 && N % 16 == 0 && K == kDecodeGemmK;
@@ -449,7 +559,7 @@ size_t splitKWorkspaceBytes(int M, int N, int K) {
 }
 
 void splitKGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
-                float *partials, void *stream) {
+                float *partials, void *stream, uint16_t *y_packed) {
     LLAISYS_CHECK(splitKGemmSupported(M, N, K), "splitKGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
     auto st = static_cast<hipStream_t>(stream);
     SplitKArgs a{x, reinterpret_cast<const u32x4 *>(packed), partials, M, N, K, K / 32, splitsFor(M, N, K)};
@@ -465,7 +575,7 @@ void splitKGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, i
     }
     const size_t threads = size_t(M) * (N / 4);
     hipLaunchKernelGGL(splitKReduceKernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, st, y, partials, M, N,
-                       a.S, accumulate ? 1 : 0);
+                       a.S, accumulate ? 1 : 0, y_packed);
     HIP_CHECK(hipGetLastError());
 }
 

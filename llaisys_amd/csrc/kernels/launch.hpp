@@ -68,12 +68,13 @@ void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t
 // does (x: residual rows whose RMSNorm is folded into the projection, or
 // null; position ctx_len[b] - 1), stores k/v into their page slot and attends
 // with q straight from LDS. Needs nh / nkvh <= 6 and head dim 128
-// (decodeUnitsRopeSupported).
+// (decodeUnitsRopeSupported). out_packed (bf16 only): write the [B, nh * 128]
+// output rows in operand order (packedRowIndex) there instead of to out.
 bool decodeUnitsRopeSupported(int nh, int nkvh, int d);
 void pagedDecodeUnitsRope(void *out, bool out_f32, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv,
                           const uint16_t *bias, const uint16_t *x, int hs, float eps, float theta,
                           const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                          int num_blocks, float scale, int *err, void *stream);
+                          int num_blocks, float scale, int *err, void *stream, uint16_t *out_packed = nullptr);
 
 // The decode above with its split records in a fixed per-GPU device array
 // (noAllocScratchBytes() bytes) instead of runtime workspace: no device
@@ -162,7 +163,25 @@ constexpr int kSplitKMaxK = 16384;
 bool splitKGemmSupported(int M, int N, int K);
 size_t splitKWorkspaceBytes(int M, int N, int K);
 void splitKGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
-                float *partials, void *stream);
+                float *partials, void *stream, uint16_t *y_packed = nullptr);
+// Rows in operand order: element (m, k) of an [M, K] matrix (K % 32 == 0)
+// kept the way packWeight keeps a weight, 16-row blocks of 1 KiB tiles, so
+// one 64-lane x 16 B load is an MFMA operand as loaded. Producers that write
+// a packed copy beside (or instead of) the row-major rows use this index;
+// a buffer holds ceil(M / 16) whole blocks (rows past M are never read back
+// into an output).
+__host__ __device__ inline size_t packedRowIndex(int m, int k, int K) {
+    return ((size_t(m >> 4) * size_t(K >> 5) + size_t(k >> 5)) * 64 + size_t(m & 15) + 16 * ((k >> 3) & 3)) * 8 +
+           size_t(k & 7);
+}
+inline size_t packedRowsElems(int M, int K) { return size_t((M + 15) / 16) * 16 * size_t(K); }
+// Y[M, N] (+)= X . W^T with X given packed (packedRowIndex) as well as W
+// (packWeight), for M <= kDecodeGemmMaxM, K == kDecodeGemmK, N % 32 == 0:
+// one workgroup per 32 x 32 tile of Y, its 4 waves splitting K, every operand
+// load issued before the first MFMA.
+bool packedXGemmSupported(int M, int N, int K);
+void packedXGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed, int M, int N, int K,
+                 bool accumulate, void *stream);
 
 // ---- Qwen2 step glue (qwen2_step.hip), bf16
 // qkv [T, (nh + 2 nkvh) d] + bias -> q [T, nh, d] rotated by position, and k
@@ -190,6 +209,11 @@ void foldNormColumns(uint16_t *out, const uint16_t *w, const uint16_t *g, size_t
 void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, int64_t *history, const int32_t *base,
                    const int64_t *first, const int64_t *next, int32_t *counter, int B, void *stream);
 void decodeRecordLast(int64_t *history, const int64_t *next, const int32_t *counter, int B, void *stream);
+// x[r] = weight[idx[r]] for r < T (bf16 rows of d, d % 32 == 0; an index
+// outside [0, vocab) sets bit 4 of err and leaves the row), also written in
+// operand order to x_packed (packedRowIndex over d columns).
+void embedRowsPacked(uint16_t *x, uint16_t *x_packed, const int64_t *idx, const uint16_t *weight, int T,
+                     int64_t vocab, int d, int *err, void *stream);
 // out [R, d] = rms_norm(x[rows ? rows[r] : r]) * w; d % 8 == 0.
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
                  void *stream);

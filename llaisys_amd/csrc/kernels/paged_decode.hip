@@ -531,6 +531,7 @@ struct RopeArgs {
     uint16_t *k_pool, *v_pool;
     int hs;
     float eps, theta;
+    uint16_t *o_packed; // non-null: the output rows go there in operand order
 };
 
 template <bool OUT_F32, int NSTAGE, bool ROPE>
@@ -775,6 +776,23 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         M = Mn;
     }
     const float inv = L > 0.f ? 1.f / L : 0.f; // no keys (invalid length): zeros
+    if (ROPE && !OUT_F32 && r.o_packed) {
+        // Dims 16 i + 4 grp .. + 3 of head h G + n: one 8 B piece of the
+        // packed row (4 consecutive columns never cross an 8-column chunk).
+        const int col0 = (h * G + n) * kHeadDim + 4 * grp;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4 v = acc.o[i] * inv;
+            const __bf16 e0 = (__bf16)v[0], e1 = (__bf16)v[1], e2 = (__bf16)v[2], e3 = (__bf16)v[3];
+            const uint32_t w0 =
+                uint32_t(__builtin_bit_cast(uint16_t, e0)) | (uint32_t(__builtin_bit_cast(uint16_t, e1)) << 16);
+            const uint32_t w1 =
+                uint32_t(__builtin_bit_cast(uint16_t, e2)) | (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
+            *reinterpret_cast<uint2 *>(r.o_packed + packedRowIndex(b, col0 + 16 * i, a.nh * kHeadDim)) =
+                make_uint2(w0, w1);
+        }
+        return;
+    }
     const size_t orow = (size_t(b) * a.nh + h * G + n) * kHeadDim;
 #pragma unroll
     for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, orow, i, grp, acc.o[i] * inv);
@@ -983,12 +1001,14 @@ bool decodeUnitsRopeSupported(int nh, int nkvh, int d) {
 void pagedDecodeUnitsRope(void *out, bool out_f32, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *qkv,
                           const uint16_t *bias, const uint16_t *x, int hs, float eps, float theta,
                           const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                          int num_blocks, float scale, int *err, void *stream) {
+                          int num_blocks, float scale, int *err, void *stream, uint16_t *out_packed) {
     LLAISYS_CHECK(decodeUnitsRopeSupported(nh, nkvh, kHeadDim),
                   "pagedDecodeUnitsRope: " << nh << " query heads over " << nkvh << " kv heads exceed "
                                            << kRopeMaxGroup << " per kv head");
     LLAISYS_CHECK(!x || (hs > 0 && hs % 8 == 0), "pagedDecodeUnitsRope: hidden size must be a positive multiple of 8");
-    const RopeArgs r{qkv, bias, x, k_pool, v_pool, hs, eps, theta};
+    LLAISYS_CHECK(!out_packed || (!out_f32 && (nh * kHeadDim) % 32 == 0),
+                  "pagedDecodeUnitsRope: a packed output is bf16 with nh * 128 % 32 == 0");
+    const RopeArgs r{qkv, bias, x, k_pool, v_pool, hs, eps, theta, out_packed};
     launchDecodeUnits(out, out_f32, nullptr, k_pool, v_pool, block_table, ctx_len, B, nh, nkvh, max_pages,
                       num_blocks, scale, err, &r, stream);
 }

@@ -243,6 +243,34 @@ void decodeAdvance(int32_t *ctx_before, int32_t *ctx_after, int64_t *tok, int64_
     HIP_CHECK(hipGetLastError());
 }
 
+namespace {
+// One block per row, 16 B (8 columns) per thread, stored twice: row-major and
+// packed (an 8-column chunk is one contiguous 16 B piece of both).
+__global__ void __launch_bounds__(kThreads) embedRowsPackedKernel(uint16_t *x, uint16_t *xp, const int64_t *idx,
+                                                                  const uint16_t *w, int64_t vocab, int d, int *err) {
+    const int r = blockIdx.x;
+    const int64_t i = idx[r];
+    if (i < 0 || i >= vocab) {
+        if (threadIdx.x == 0) atomicOr(err, 4);
+        return;
+    }
+    for (int c = 8 * threadIdx.x; c < d; c += 8 * kThreads) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(w + size_t(i) * d + c);
+        *reinterpret_cast<uint4 *>(x + size_t(r) * d + c) = v;
+        *reinterpret_cast<uint4 *>(xp + packedRowIndex(r, c, d)) = v;
+    }
+}
+} // namespace
+
+void embedRowsPacked(uint16_t *x, uint16_t *x_packed, const int64_t *idx, const uint16_t *weight, int T,
+                     int64_t vocab, int d, int *err, void *stream) {
+    LLAISYS_CHECK(d > 0 && d % 32 == 0, "embedRowsPacked: row length must be a positive multiple of 32, got " << d);
+    if (T <= 0) return;
+    hipLaunchKernelGGL(embedRowsPackedKernel, dim3(T), dim3(kThreads), 0, static_cast<hipStream_t>(stream), x,
+                       x_packed, idx, weight, vocab, d, err);
+    HIP_CHECK(hipGetLastError());
+}
+
 void decodeRecordLast(int64_t *history, const int64_t *next, const int32_t *counter, int B, void *stream) {
     hipLaunchKernelGGL(decodeRecordLastKernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), history,
                        next, counter, B);

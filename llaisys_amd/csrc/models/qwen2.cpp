@@ -70,6 +70,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     if (const char *e = std::getenv("LLAISYS_DECODE_UNITS")) unit_decode_allowed_ = e[0] != '0';
     unit_rope_ = K::decodeUnitsRopeSupported(int(cfg.nh), int(cfg.nkvh), int(cfg.dh));
     if (const char *e = std::getenv("LLAISYS_DECODE_UNIT_ROPE")) unit_rope_ = unit_rope_ && e[0] != '0';
+    if (const char *e = std::getenv("LLAISYS_PACKED_X")) packed_x_ = e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -190,6 +191,8 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
         qkv_ = dev({cap, q + 2 * kv}, dt, dev_);
         q_ = dev({cap, cfg_.nh, cfg_.dh}, dt, dev_);
         attn_ = dev({cap, cfg_.nh, cfg_.dh}, dt, dev_);
+        xp_ = dev({K::packedRowsElems(int(cap), int(cfg_.hs))}, dt, dev_);
+        ap_ = dev({K::packedRowsElems(int(cap), int(q))}, dt, dev_);
         gu_ = dev({cap, 2 * cfg_.di}, dt, dev_);
         act_ = dev({cap, cfg_.di}, dt, dev_);
         cap_T_ = cap;
@@ -491,7 +494,19 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     const int M = int(T);
     const float scale = 1.f / std::sqrt(float(cfg_.dh));
 
-    K::embedding(x_->data(), i64(tok_), in_embed_->data(), et, T, int64_t(cfg_.voc), hs, rt.errorWord(), s);
+    // Packed-operand decode path: qkv and o read x and the attention output
+    // in MFMA operand order, written beside their rows by the embedding, the
+    // down projection's split-K reduce and the attention itself.
+    const auto &L0 = layers_[0];
+    const bool px = packed_x_ && decode_only && unit_decode_ && unit_rope_ && fold_norm_ && T <= kFoldMaxRows &&
+                    cfg_.dtype == LLAISYS_DTYPE_BF16 && L0.qkv_wfp && L0.o_wp && L0.down_wp &&
+                    K::packedXGemmSupported(M, q + 2 * kv, hs) && K::packedXGemmSupported(M, hs, q) &&
+                    K::splitKGemmSupported(M, hs, di);
+    if (px)
+        K::embedRowsPacked(u16(x_), u16(xp_), i64(tok_), u16(in_embed_), M, int64_t(cfg_.voc), hs, rt.errorWord(),
+                           s);
+    else
+        K::embedding(x_->data(), i64(tok_), in_embed_->data(), et, T, int64_t(cfg_.voc), hs, rt.errorWord(), s);
     const tensor_t q3 = rows(q_, T), a3 = rows(attn_, T);
     for (size_t l = 0; l < cfg_.nlayer; ++l) {
         const auto &L = layers_[l];
@@ -503,15 +518,18 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
         const bool fold = fold_norm_ && T <= kFoldMaxRows;
         const uint16_t *xr = fold ? u16(x_) : nullptr;
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
-        project(qkv_, fold ? x_ : h_, fold ? L.qkv_wf : L.qkv_w, fold ? L.qkv_wfp : nullptr, M, q + 2 * kv, hs, false,
-                s);
+        if (px)
+            K::packedXGemm(u16(qkv_), u16(xp_), u16(L.qkv_wfp), M, q + 2 * kv, hs, false, s);
+        else
+            project(qkv_, fold ? x_ : h_, fold ? L.qkv_wf : L.qkv_w, fold ? L.qkv_wfp : nullptr, M, q + 2 * kv, hs,
+                    false, s);
         if (decode_only && unit_decode_ && unit_rope_) {
             // QKV epilogue (bias, 1/rms, RoPE, k/v append) inside the attention
             // launch: one kernel fewer per layer.
             K::pagedDecodeUnitsRope(a3->data(), false, u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), xr,
                                     hs, cfg_.epsilon, cfg_.theta, i32(table_), i32(ctx_after_), int(B),
                                     int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]), int(num_blocks_), scale,
-                                    rt.errorWord(), s);
+                                    rt.errorWord(), s, px ? u16(ap_) : nullptr);
         } else {
             K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
                              i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh),
@@ -525,12 +543,15 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
                 ops::pagedAttention(a3, q3, k_pool_[l], v_pool_[l], table_, ctx_after_, decode_only ? nullptr : cu_,
                                     scale);
         }
-        project(x_, attn_, L.o_w, L.o_wp, M, hs, q, true, s);
+        if (px)
+            K::packedXGemm(u16(x_), u16(ap_), u16(L.o_wp), M, hs, q, true, s);
+        else
+            project(x_, attn_, L.o_w, L.o_wp, M, hs, q, true, s);
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
         project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, fold ? L.gate_up_wfp : nullptr, M, 2 * di, hs,
                 false, s);
         K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s);
-        project(x_, act_, L.down_w, L.down_wp, M, hs, di, true, s);
+        project(x_, act_, L.down_w, L.down_wp, M, hs, di, true, s, px ? u16(xp_) : nullptr);
     }
     K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);
     project(logits_, hl_, out_embed_, out_embed_p_, int(B), int(cfg_.voc), hs, false, s);
@@ -548,8 +569,8 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
 static int decodeGemmMaxM(int N) { return N >= 65536 ? 128 : N >= 8192 ? 96 : 64; }
 
 void Qwen2Model::project(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &packed, int M,
-                         int N, int K, bool accumulate, void *s) const {
-    if (packed && M <= decodeGemmMaxM(N) && K::decodeGemmSupported(M, N, K)) {
+                         int N, int K, bool accumulate, void *s, uint16_t *y_packed) const {
+    if (!y_packed && packed && M <= decodeGemmMaxM(N) && K::decodeGemmSupported(M, N, K)) {
         K::decodeGemm(u16(y), u16(x), u16(packed), M, N, K, accumulate, s);
         return;
     }
@@ -558,9 +579,10 @@ void Qwen2Model::project(const tensor_t &y, const tensor_t &x, const tensor_t &w
     // vs 22.5 us autotuned at M = 128).
     if (packed && K::splitKGemmSupported(M, N, K)) {
         auto *part = static_cast<float *>(core::context().runtime().scratch(K::splitKWorkspaceBytes(M, N, K)));
-        K::splitKGemm(u16(y), u16(x), u16(packed), M, N, K, accumulate, part, s);
+        K::splitKGemm(u16(y), u16(x), u16(packed), M, N, K, accumulate, part, s, y_packed);
         return;
     }
+    LLAISYS_CHECK(!y_packed, "qwen2: a packed copy of the output needs the split-K projection");
     gemm(y, x, w, nullptr, M, N, K, accumulate, s);
 }
 

@@ -93,9 +93,10 @@ private:
     void ensureFolded();
     // Y[M, N] (+)= X W^T: the hand-written decode GEMM over `packed` when it
     // exists and M is at most the size where it beats the library for this N,
-    // else the library GEMM over the row-major `w`.
+    // else the library GEMM over the row-major `w`. y_packed: also write Y in
+    // operand order (only the split-K path can; the caller checks it is taken).
     void project(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &packed, int M, int N, int K,
-                 bool accumulate, void *s) const;
+                 bool accumulate, void *s, uint16_t *y_packed = nullptr) const;
     void decodeGraph(size_t B, size_t width);
     std::vector<int32_t> reserveAll(const int64_t *ids, size_t B, const size_t *n, std::vector<int32_t> &before);
 
@@ -117,6 +118,9 @@ private:
     // step workspace (grow-only)
     size_t cap_T_ = 0, cap_B_ = 0, cap_i32_ = 0, cap_i64_ = 0;
     tensor_t x_, h_, qkv_, q_, attn_, gu_, act_, hl_, logits_, next_;
+    // x and the attention output in MFMA operand order (packedRowIndex), for
+    // the packed-operand qkv and o projections of decode steps.
+    tensor_t xp_, ap_;
     tensor_t dev_i32_, dev_i64_;     // per-step indices, uploaded in one copy each
     core::storage_t host32_, host64_; // pinned staging of the same
     tensor_t table_, ctx_before_, ctx_after_, cu_, cow_, tok_, last_; // views of dev_i32_/dev_i64_
@@ -143,6 +147,11 @@ private:
     // (pagedDecodeUnitsRope) when the head grouping allows;
     // LLAISYS_DECODE_UNIT_ROPE=0 keeps the separate qkvRopeAppend launch.
     bool unit_rope_ = true;
+    // Decode steps on that path (M <= 128, K = 1536) run the qkv and o
+    // projections with both operands packed: the embedding, the split-K
+    // reduce and the attention write packed copies of their rows.
+    // LLAISYS_PACKED_X=0 keeps the library GEMMs there.
+    bool packed_x_ = true;
     void chooseDecodeAttention(size_t B, int32_t min_ctx, int32_t max_ctx);
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
     std::map<size_t, DecodeGraph> graphs_;       // one step (step())

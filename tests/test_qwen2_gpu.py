@@ -25,6 +25,9 @@ SHAPES = {
     "gqa12": dict(nlayer=1, hs=384, nh=12, nkvh=2, di=768, voc=777),
     # a 20000-word vocabulary: the LM head as a wide GEMM
     "widehead": dict(nlayer=1, hs=256, nh=2, nkvh=1, di=384, voc=20000),
+    # the 1.5B model's hidden size and heads (K = 1536 for qkv and o), FFN
+    # past 1536 (the split-K down projection)
+    "hs1536": dict(nlayer=2, hs=1536, nh=12, nkvh=2, di=2048, voc=1000),
 }
 
 
@@ -187,6 +190,68 @@ def test_fused_qkv_epilogue_matches_separate_launch(monkeypatch):
         del model
     for lg_a, lg_b in zip(*runs):
         assert (lg_a - lg_b).abs().max().item() <= 1e-2 * lg_b.abs().max().item()
+
+
+def test_packed_operand_projections_match_library_and_reference(monkeypatch):
+    # Decode steps on the fused unit attention at K = 1536 run qkv and o with
+    # both operands in MFMA operand order: the embedding, the split-K reduce
+    # and the attention write packed copies of x and of the attention output.
+    # 66 sequences (132 units) over 4 decode steps: against transformers, and
+    # step by step against the same model with library GEMMs there
+    # (LLAISYS_PACKED_X=0; other fp32 summation orders, so within a bound).
+    # A wrong packed index or tile would move the logits by far more. At this
+    # width the bf16 activations alone put both runs near the small models'
+    # 3 % bound, so each run's error against transformers is measured and
+    # the packed run's may exceed the library run's by at most a quarter (plus
+    # 0.5 % of the logits' max). Then a multi-step decode call (captured
+    # graph) against single steps.
+    monkeypatch.setenv("LLAISYS_DECODE_UNITS", "1")
+    monkeypatch.setenv("LLAISYS_DECODE_UNIT_ROPE", "1")
+    nseq = 66
+    lens = [200 + (i * 53) % 190 for i in range(nseq)]
+    runs, ref_err = [], {}
+    for packed in ("1", "0"):
+        monkeypatch.setenv("LLAISYS_PACKED_X", packed)
+        model, hf = build("hs1536", num_blocks=nseq * 30 + 8)
+        prompts = [prompt(n, model.meta.voc, 700 + i) for i, n in enumerate(lens)]
+        ids = [model.create_sequence()[0] for _ in prompts]
+        for s in range(0, nseq, 11):
+            model.step(ids[s:s + 11], prompts[s:s + 11])
+        hist = [list(p) for p in prompts]
+        steps = []
+        for k in range(4):  # the same fed tokens in both runs
+            fed = prompt(nseq, model.meta.voc, 750 + k)
+            nxt = model.step(ids, [[t] for t in fed])
+            for h, t in zip(hist, fed):
+                h.append(t)
+            logits = to_torch(model.logits()).float().clone()
+            steps.append(logits)
+        err, scale = 0.0, 0.0
+        for r in range(0, nseq, 16):
+            ref = hf_logits(hf, hist[r])[-1]
+            err = max(err, (logits[r] - ref).abs().max().item())
+            scale = max(scale, ref.abs().max().item())
+        ref_err[packed] = (err, scale)
+        if packed == "1":
+            forks = [model.fork(i) for i in ids]
+            multi = model.decode(ids, nxt, 4)
+            single, cur = [], nxt
+            for _ in range(4):
+                cur = model.step(forks, [[t] for t in cur])
+                single.append(cur)
+            assert np.array_equal(np.asarray(multi), np.asarray(single, np.int64))
+        assert L.device_error_flags() == 0
+        runs.append(steps)
+        del model, hf
+    (e_px, scale), (e_lib, _) = ref_err["1"], ref_err["0"]
+    print(f"max |logit - transformers|: packed {e_px:.4g}, library {e_lib:.4g}, max |logit| {scale:.4g}")
+    assert e_px <= 1.25 * e_lib + 5e-3 * scale
+    assert e_lib <= 0.05 * scale
+    # Run against run: each is ~3 % of the logits' max from transformers here,
+    # and two summation orders measured ~1 % apart; 2.5 % still fails a wrong
+    # tile (tens of percent).
+    for lg_a, lg_b in zip(*runs):
+        assert (lg_a - lg_b).abs().max().item() <= 2.5e-2 * lg_b.abs().max().item()
 
 
 def test_infer_restarts_on_a_new_history_and_reuses_cached_blocks():
