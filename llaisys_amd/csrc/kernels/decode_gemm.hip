@@ -167,7 +167,7 @@ decodeGemmKernel(GemmArgs a) {
 // One thread per 16 B of the packed layout: tile (nb, kb), lane l holds
 // W[16 nb + l % 16][32 kb + 8 (l / 16) .. + 7], times g[k] when g is given
 // (an RMSNorm weight folded into the columns, rounded once to bf16).
-__global__ void packKernel(u32x4 *wp, const uint16_t *w, const uint16_t *g, int N, int K) {
+__global__ void packKernel(u32x4 *wp, const uint16_t *w, const uint16_t *g, int N, int K, int interleave_di) {
     const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int KT = K / 32;
     const size_t total = size_t(N / 16) * KT * 64;
@@ -176,7 +176,10 @@ __global__ void packKernel(u32x4 *wp, const uint16_t *w, const uint16_t *g, int 
     const size_t tile = idx >> 6;
     const int kb = int(tile % KT);
     const int nb = int(tile / KT);
-    const int row = 16 * nb + (lane & 15);
+    // interleave_di > 0: block nb takes gate rows 8 nb .. + 7 and the up
+    // rows interleave_di + 8 nb .. + 7 of a [gate; up] weight.
+    const int r16 = lane & 15;
+    const int row = interleave_di ? (r16 < 8 ? 8 * nb + r16 : interleave_di + 8 * nb + r16 - 8) : 16 * nb + r16;
     const int k = 32 * kb + 8 * (lane >> 4);
     u32x4 v = *reinterpret_cast<const u32x4 *>(w + size_t(row) * K + k);
     if (g) {
@@ -429,7 +432,7 @@ constexpr int kPxSteps = 12; // k tiles per wave (K = 4 x 12 x 32)
 
 template <bool ACC>
 __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x4 *xp, const u32x4 *wp, int M,
-                                                         int N) {
+                                                         int N, uint16_t *y_packed) {
     __shared__ f32x4 red[3][kPxTile][kPxTile][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -500,17 +503,152 @@ __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x
                 const uint32_t w1 = uint32_t(__builtin_bit_cast(uint16_t, e2)) |
                                     (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
                 *reinterpret_cast<uint2 *>(y + size_t(m) * N + n0) = make_uint2(w0, w1);
+                if (y_packed) *reinterpret_cast<uint2 *>(y_packed + packedRowIndex(m, n0, N)) = make_uint2(w0, w1);
             }
         }
 }
+
+// Gate-up projection + row 1/rms + SwiGLU over packed x and a
+// packWeightGateUp weight. Workgroup g owns NB 16-row blocks (8 act columns
+// each) and all M rows; its 4 waves split K (12 k tiles each) and stream W
+// and X tiles of one k step together through a kGuRing-deep register ring
+// (loads return in issue order, so X issued behind all of W would wait for
+// all of W). Every wave also sums the squares of the x values it loads, per
+// row; the rows' sums meet in LDS with the partial tiles, and the wave that
+// owns m blocks 2w, 2w + 1 adds the four k partials in wave order, scales by
+// r, pairs each gate value with its up value (lane l and l ^ 32 hold the
+// same columns) and stores act.
+constexpr int kGuRing = 4;
+constexpr int kGuRows = 8; // 16-row m blocks (M <= 128)
+
+template <int NB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int di, float eps) {
+    constexpr int KT = 4 * kPxSteps, MB = kGuRows, R = kGuRing;
+    __shared__ f32x4 red[3][NB][MB][64];
+    __shared__ float ssl[4][16 * MB];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int blk0 = int(blockIdx.x) * NB;
+    const int kb0 = wave * kPxSteps;
+    const int last_mb = (M - 1) >> 4;
+    const u32x4 *wl = wp + (size_t(blk0) * KT + kb0) * 64 + lane;
+    const u32x4 *xl = xp + size_t(kb0) * 64 + lane;
+    u32x4 rw[R][NB], rx[R][MB];
+    auto issue = [&](int st, int j) {
+#pragma unroll
+        for (int t = 0; t < NB; ++t) rw[st][t] = __builtin_nontemporal_load(wl + (size_t(t) * KT + j) * 64);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) rx[st][i] = xl[(size_t(min(i, last_mb)) * KT + j) * 64];
+    };
+#pragma unroll
+    for (int j = 0; j < R; ++j) issue(j, j);
+    f32x4 acc[NB][MB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int i = 0; i < MB; ++i) acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ss[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) ss[i] = 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kPxSteps; ++j) {
+        const int st = j % R;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int t = 0; t < NB; ++t) acc[t][i] = mfma(rw[st][t], rx[st][i], acc[t][i]);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = __uint_as_float(rx[st][i][e] << 16), hi = __uint_as_float(rx[st][i][e] & 0xffff0000u);
+                ss[i] += lo * lo + hi * hi;
+            }
+        if (j + R < kPxSteps) issue(st, j + R);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Row m = 16 i + lane % 16: the lane's 8 k per step, then its 4 k groups.
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        ss[i] += __shfl_xor(ss[i], 16);
+        ss[i] += __shfl_xor(ss[i], 32);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) ssl[wave][16 * i + lane] = ss[i];
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int owner = i / 2;
+        if (owner == wave) continue;
+        const int slot = wave < owner ? wave : wave - 1;
+#pragma unroll
+        for (int t = 0; t < NB; ++t) red[slot][t][i][lane] = acc[t][i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        if (i / 2 != wave) continue;
+        const int m = 16 * i + (lane & 15);
+        const float r = rsqrtf((ssl[0][m] + ssl[1][m] + ssl[2][m] + ssl[3][m]) / float(KT * 32) + eps);
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v += q == wave ? acc[t][i] : red[q < wave ? q : q - 1][t][i][lane];
+            // Lane groups 0, 1 hold gate rows 4 g .. 4 g + 3 of the block, 2, 3
+            // the up rows of the same columns; lane < 32 finishes elements
+            // 0, 1, lane >= 32 elements 2, 3.
+            const bool lo = lane < 32;
+            const float p0 = __shfl_xor(lo ? v[2] : v[0], 32), p1 = __shfl_xor(lo ? v[3] : v[1], 32);
+            const float g0 = r * (lo ? v[0] : p0), g1 = r * (lo ? v[1] : p1);
+            const float u0 = r * (lo ? p0 : v[2]), u1 = r * (lo ? p1 : v[3]);
+            const __bf16 b0 = (__bf16)(u0 * g0 / (1.f + expf(-g0)));
+            const __bf16 b1 = (__bf16)(u1 * g1 / (1.f + expf(-g1)));
+            const int col = 8 * (blk0 + t) + 4 * ((lane >> 4) & 1) + (lo ? 0 : 2);
+            if (m < M)
+                *reinterpret_cast<uint32_t *>(act + size_t(m) * di + col) =
+                    uint32_t(__builtin_bit_cast(uint16_t, b0)) | (uint32_t(__builtin_bit_cast(uint16_t, b1)) << 16);
+        }
+    }
+}
+
+int gateUpBlocksPerGroup(int di) {
+    const int blocks = 2 * di / 16;
+    return blocks % 5 == 0 ? 5 : blocks % 4 == 0 ? 4 : 0;
+}
 } // namespace
+
+bool gateUpSwigluSupported(int M, int di, int K) {
+    return M >= 1 && M <= 16 * kGuRows && K == 4 * kPxSteps * 32 && di > 0 && di % 8 == 0 &&
+           gateUpBlocksPerGroup(di) > 0;
+}
+
+void gateUpSwiglu(uint16_t *act, const uint16_t *x_packed, const uint16_t *w_packed, int M, int di, int K, float eps,
+                  void *stream) {
+    LLAISYS_CHECK(gateUpSwigluSupported(M, di, K), "gateUpSwiglu: unsupported shape M=" << M << " di=" << di
+                                                                                        << " K=" << K);
+    const int nb = gateUpBlocksPerGroup(di);
+    const dim3 grid(unsigned(2 * di / 16 / nb));
+    auto st = static_cast<hipStream_t>(stream);
+    const auto *xp = reinterpret_cast<const u32x4 *>(x_packed);
+    const auto *wp = reinterpret_cast<const u32x4 *>(w_packed);
+    if (nb == 5)
+        hipLaunchKernelGGL(gateUpSwigluKernel<5>, grid, dim3(256), 0, st, act, xp, wp, M, di, eps);
+    else
+        hipLaunchKernelGGL(gateUpSwigluKernel<4>, grid, dim3(256), 0, st, act, xp, wp, M, di, eps);
+    HIP_CHECK(hipGetLastError());
+}
+
 
 bool packedXGemmSupported(int M, int N, int K) {
     return M >= 1 && M <= kDecodeGemmMaxM && K == 4 * kPxSteps * 32 && N >= 32 && N % (16 * kPxTile) == 0;
 }
 
 void packedXGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed, int M, int N, int K,
-                 bool accumulate, void *stream) {
+                 bool accumulate, void *stream, uint16_t *y_packed) {
     LLAISYS_CHECK(packedXGemmSupported(M, N, K),
                   "packedXGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
     const int mtiles = (M + 16 * kPxTile - 1) / (16 * kPxTile);
@@ -519,9 +657,9 @@ void packedXGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed
     const auto *xp = reinterpret_cast<const u32x4 *>(x_packed);
     const auto *wp = reinterpret_cast<const u32x4 *>(w_packed);
     if (accumulate)
-        hipLaunchKernelGGL(packedXGemmKernel<true>, grid, dim3(256), 0, st, y, xp, wp, M, N);
+        hipLaunchKernelGGL(packedXGemmKernel<true>, grid, dim3(256), 0, st, y, xp, wp, M, N, y_packed);
     else
-        hipLaunchKernelGGL(packedXGemmKernel<false>, grid, dim3(256), 0, st, y, xp, wp, M, N);
+        hipLaunchKernelGGL(packedXGemmKernel<false>, grid, dim3(256), 0, st, y, xp, wp, M, N, y_packed);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -536,7 +674,17 @@ void packWeight(uint16_t *packed, const uint16_t *w, const uint16_t *fold_g, int
     const size_t total = size_t(N / 16) * (K / 32) * 64;
     if (!total) return;
     hipLaunchKernelGGL(packKernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                       reinterpret_cast<u32x4 *>(packed), w, fold_g, N, K);
+                       reinterpret_cast<u32x4 *>(packed), w, fold_g, N, K, 0);
+    HIP_CHECK(hipGetLastError());
+}
+
+void packWeightGateUp(uint16_t *packed, const uint16_t *w, int di, int K, void *stream) {
+    LLAISYS_CHECK(di % 8 == 0 && K % 32 == 0,
+                  "packWeightGateUp: di % 8 and K % 32 must be 0 (di=" << di << ", K=" << K << ")");
+    const size_t total = size_t(2 * di / 16) * (K / 32) * 64;
+    if (!total) return;
+    hipLaunchKernelGGL(packKernel, dim3(unsigned((total + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<u32x4 *>(packed), w, nullptr, 2 * di, K, di);
     HIP_CHECK(hipGetLastError());
 }
 

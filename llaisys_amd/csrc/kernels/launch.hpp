@@ -152,6 +152,11 @@ constexpr int kDecodeGemmK = 1536;
 bool decodeGemmSupported(int M, int N, int K);
 size_t packedWeightElems(int N, int K);
 void packWeight(uint16_t *packed, const uint16_t *w, const uint16_t *fold_g, int N, int K, void *stream);
+// packWeight of a fused [gate; up] weight (2 di rows) with the halves
+// interleaved: 16-row block b holds gate rows 8b .. 8b + 7, then up rows
+// 8b .. 8b + 7 (di % 8 == 0). A product over it has gate columns 8b + e at
+// 16b + e and up columns at 16b + 8 + e (swigluRows' interleaved layout).
+void packWeightGateUp(uint16_t *packed, const uint16_t *w, int di, int K, void *stream);
 void decodeGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
                 void *stream);
 // The same product for long K (kDecodeGemmK < K <= kSplitKMaxK, K % 32 == 0,
@@ -181,7 +186,15 @@ inline size_t packedRowsElems(int M, int K) { return size_t((M + 15) / 16) * 16 
 // load issued before the first MFMA.
 bool packedXGemmSupported(int M, int N, int K);
 void packedXGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed, int M, int N, int K,
-                 bool accumulate, void *stream);
+                 bool accumulate, void *stream, uint16_t *y_packed = nullptr);
+// act[M, di] = up * silu(gate) of r * (x [gate; up]^T), r = 1/sqrt(mean(x^2)
+// + eps) per row, for x given packed ([M, K], K == kDecodeGemmK, M <=
+// kDecodeGemmMaxM) and the gate/up weight packed by packWeightGateUp (its
+// RMSNorm weight folded in): the gate-up projection, the row's 1/rms and the
+// SwiGLU in one kernel, from fp32 sums (no bf16 gate/up rows in between).
+bool gateUpSwigluSupported(int M, int di, int K);
+void gateUpSwiglu(uint16_t *act, const uint16_t *x_packed, const uint16_t *w_packed, int M, int di, int K, float eps,
+                  void *stream);
 
 // ---- Qwen2 step glue (qwen2_step.hip), bf16
 // qkv [T, (nh + 2 nkvh) d] + bias -> q [T, nh, d] rotated by position, and k
@@ -197,8 +210,10 @@ void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16
                    void *stream);
 // act [T, di] = up * silu(gate) with gate_up rows [gate (di) | up (di)]; di % 8 == 0.
 // x (may be null): as for qkvRopeAppend, gate and up scaled by the row's 1/rms.
+// interleaved: rows in packWeightGateUp's column order instead (gate columns
+// 8b + e at 16b + e, up columns at 16b + 8 + e).
 void swigluRows(uint16_t *act, const uint16_t *gate_up, const uint16_t *x, size_t T, int di, int hs, float eps,
-                void *stream);
+                void *stream, bool interleaved = false);
 // out[r, c] = w[r, c] * g[c] (bf16, one rounding): an RMSNorm weight folded
 // into the columns of the projection that consumes the normalised rows.
 void foldNormColumns(uint16_t *out, const uint16_t *w, const uint16_t *g, size_t rows, int cols, void *stream);

@@ -66,15 +66,17 @@ __global__ void foldNormColumnsKernel(uint4 *out, const uint4 *w, const uint4 *g
 // weight was folded into the gate/up projection; gate and up are then scaled
 // by the row's 1/rms (each wave works it out itself: no barrier).
 __global__ void __launch_bounds__(kThreads) swigluRowsKernel(bf16 *act, const bf16 *gu, const bf16 *x, int di, int hs,
-                                                             float eps) {
+                                                             float eps, int interleaved) {
     const int nv = di / 8;
     const size_t r = blockIdx.y;
     const int c = blockIdx.x * kThreads + threadIdx.x;
     // Every load first (gate, up and the row's x, clamped rather than
     // branched), so the latencies overlap.
     const int cc = min(c, nv - 1);
-    const uint4 g = reinterpret_cast<const uint4 *>(gu + r * 2 * di)[cc];
-    const uint4 u = reinterpret_cast<const uint4 *>(gu + r * 2 * di + di)[cc];
+    // 8 columns: gate chunk cc and up chunk cc, side by side when interleaved.
+    const uint4 *row = reinterpret_cast<const uint4 *>(gu + r * 2 * di);
+    const uint4 g = interleaved ? row[2 * cc] : row[cc];
+    const uint4 u = interleaved ? row[2 * cc + 1] : row[cc + di / 8];
     RowChunks xr; // (without x the gate row stands in: read, not used)
     xr.load(reinterpret_cast<const uint16_t *>(x ? x + r * hs : gu + r * 2 * di), x ? hs : 8);
     const float rs = x ? rowInvRms(xr, x + r * hs, hs, eps) : 1.f;
@@ -293,7 +295,7 @@ void qkvRopeAppend(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16
 }
 
 void swigluRows(uint16_t *act, const uint16_t *gate_up, const uint16_t *x, size_t T, int di, int hs, float eps,
-                void *stream) {
+                void *stream, bool interleaved) {
     LLAISYS_CHECK(di % 8 == 0, "swigluRows: di must be a multiple of 8, got " << di);
     LLAISYS_CHECK(!x || (hs > 0 && hs % 8 == 0), "swigluRows: hidden size must be a positive multiple of 8");
     constexpr size_t kMaxRows = 65535; // grid y limit: longer batches take several launches
@@ -302,7 +304,7 @@ void swigluRows(uint16_t *act, const uint16_t *gate_up, const uint16_t *x, size_
         const dim3 grid(unsigned((di / 8 + kThreads - 1) / kThreads), unsigned(rows));
         hipLaunchKernelGGL(swigluRowsKernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                            reinterpret_cast<bf16 *>(act + r0 * di), reinterpret_cast<const bf16 *>(gate_up + r0 * 2 * di),
-                           x ? reinterpret_cast<const bf16 *>(x + r0 * hs) : nullptr, di, hs, eps);
+                           x ? reinterpret_cast<const bf16 *>(x + r0 * hs) : nullptr, di, hs, eps, interleaved ? 1 : 0);
         HIP_CHECK(hipGetLastError());
     }
 }

@@ -36,6 +36,7 @@ bool scatterBlocks() {
 
 // Steps with at most this many token rows use the folded-norm projections.
 constexpr size_t kFoldMaxRows = 512;
+bool takesDecodeGemm(const tensor_t &packed, int M, int N, int K);
 
 tensor_t dev(std::vector<size_t> shape, llaisysDataType_t dt, int id) {
     return Tensor::create(shape, dt, LLAISYS_DEVICE_AMD, id);
@@ -476,9 +477,9 @@ void Qwen2Model::ensureFolded() {
         if (v[2] != L.folded_from[2] || v[3] != L.folded_from[3]) {
             K::foldNormColumns(u16(L.gate_up_wf), u16(L.gate_up_w), u16(L.mlp_norm), L.gate_up_w->shape()[0],
                                int(cfg_.hs), s);
-            if (L.gate_up_wfp)
-                K::packWeight(u16(L.gate_up_wfp), u16(L.gate_up_wf), nullptr, int(L.gate_up_w->shape()[0]),
-                              int(cfg_.hs), s);
+            // Gate and up rows interleaved per 16-row block, so that each
+            // block of the product finishes its own SwiGLU columns.
+            if (L.gate_up_wfp) K::packWeightGateUp(u16(L.gate_up_wfp), u16(L.gate_up_wf), int(cfg_.di), int(cfg_.hs), s);
             L.folded_from[2] = v[2];
             L.folded_from[3] = v[3];
         }
@@ -502,6 +503,9 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
                     cfg_.dtype == LLAISYS_DTYPE_BF16 && L0.qkv_wfp && L0.o_wp && L0.down_wp &&
                     K::packedXGemmSupported(M, q + 2 * kv, hs) && K::packedXGemmSupported(M, hs, q) &&
                     K::splitKGemmSupported(M, hs, di);
+    // On that path the gate-up projection, the row's 1/rms and the SwiGLU
+    // run as one kernel over the packed x the o projection leaves.
+    const bool fused_mlp = px && L0.gate_up_wfp && K::gateUpSwigluSupported(M, di, hs);
     if (px)
         K::embedRowsPacked(u16(x_), u16(xp_), i64(tok_), u16(in_embed_), M, int64_t(cfg_.voc), hs, rt.errorWord(),
                            s);
@@ -544,13 +548,19 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
                                     scale);
         }
         if (px)
-            K::packedXGemm(u16(x_), u16(ap_), u16(L.o_wp), M, hs, q, true, s);
+            K::packedXGemm(u16(x_), u16(ap_), u16(L.o_wp), M, hs, q, true, s, fused_mlp ? u16(xp_) : nullptr);
         else
             project(x_, attn_, L.o_w, L.o_wp, M, hs, q, true, s);
-        if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
-        project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, fold ? L.gate_up_wfp : nullptr, M, 2 * di, hs,
-                false, s);
-        K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s);
+        if (fused_mlp) {
+            K::gateUpSwiglu(u16(act_), u16(xp_), u16(L.gate_up_wfp), M, di, hs, cfg_.epsilon, s);
+        } else {
+            if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
+            const tensor_t gup = fold ? L.gate_up_wfp : tensor_t();
+            project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, gup, M, 2 * di, hs, false, s);
+            // The decode GEMM over the interleaved packed copy leaves gate
+            // and up columns interleaved as well.
+            K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s, takesDecodeGemm(gup, M, 2 * di, hs));
+        }
         project(x_, act_, L.down_w, L.down_wp, M, hs, di, true, s, px ? u16(xp_) : nullptr);
     }
     K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);
@@ -566,11 +576,18 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
 // Measured in the graph-replayed config-5 step (M = 128), the library's
 // autotuned kernels still win for qkv, o and gate-up: 3.55 ms per step with
 // these limits, 3.75 ms with qkv and o at 128, 3.86 ms with all at 128.
-static int decodeGemmMaxM(int N) { return N >= 65536 ? 128 : N >= 8192 ? 96 : 64; }
+namespace {
+int decodeGemmMaxM(int N) { return N >= 65536 ? 128 : N >= 8192 ? 96 : 64; }
+
+// Whether project() runs the decode GEMM over `packed` for this shape.
+bool takesDecodeGemm(const tensor_t &packed, int M, int N, int K) {
+    return packed && M <= decodeGemmMaxM(N) && K::decodeGemmSupported(M, N, K);
+}
+} // namespace
 
 void Qwen2Model::project(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &packed, int M,
                          int N, int K, bool accumulate, void *s, uint16_t *y_packed) const {
-    if (!y_packed && packed && M <= decodeGemmMaxM(N) && K::decodeGemmSupported(M, N, K)) {
+    if (!y_packed && takesDecodeGemm(packed, M, N, K)) {
         K::decodeGemm(u16(y), u16(x), u16(packed), M, N, K, accumulate, s);
         return;
     }
