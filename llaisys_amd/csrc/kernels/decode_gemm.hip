@@ -518,7 +518,7 @@ __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x
 // owns m blocks 2w, 2w + 1 adds the four k partials in wave order, scales by
 // r, pairs each gate value with its up value (lane l and l ^ 32 hold the
 // same columns) and stores act.
-constexpr int kGuRing = 4;
+constexpr int kGuRing = 3; // (4: 20.6 us, 6: spills; 3: 20.4 us in the config-5 step)
 constexpr int kGuRows = 8; // 16-row m blocks (M <= 128)
 
 template <int NB>
