@@ -24,6 +24,7 @@
 //    bias enters the same way, preset as the rows of Y).
 // Double-buffered partials make that the only barrier per block.
 #include "launch.hpp"
+#include "step_common.hpp"
 
 #include "../device/hip_check.hpp"
 
@@ -508,6 +509,157 @@ __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x
         }
 }
 
+// QKV projection + qkvRopeAppend's epilogue. Workgroup (mt, g) owns rows
+// 32 mt .. + 31 and, of head g / 4, the 16-column blocks t and t + 4 (t =
+// g % 4): dims d and d + 64 of the head sit in the same lane, so the
+// rotation needs no exchange. The operands and the k sweep are those of
+// packedXGemmKernel; each wave also sums the squares of the x values it
+// loads, per row, for the row's 1/rms; waves 0 and 1 each finish one 16-row
+// block.
+struct QkvRopeArgs {
+    uint16_t *q, *k_pool, *v_pool;
+    const uint16_t *bias;
+    const int32_t *table, *ctx;
+    int nh, nkvh, max_pages, num_blocks, hs;
+    float eps, theta;
+    int *err;
+};
+
+__device__ __forceinline__ uint32_t packBf16(float a, float b) {
+    const __bf16 x = (__bf16)a, y = (__bf16)b;
+    return uint32_t(__builtin_bit_cast(uint16_t, x)) | (uint32_t(__builtin_bit_cast(uint16_t, y)) << 16);
+}
+
+__global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const u32x4 *wp, int M, QkvRopeArgs e) {
+    __shared__ f32x4 red[3][2][kPxTile][64];
+    __shared__ float ssl[4][16 * kPxTile];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    constexpr int KT = 4 * kPxSteps;
+    const int groups = (e.nh + 2 * e.nkvh) * 4;
+    const int mt = int(blockIdx.x) / groups, g = int(blockIdx.x) % groups;
+    const int head = g >> 2, t4 = g & 3;
+    const int kb0 = wave * kPxSteps;
+    const int last_mb = (M - 1) >> 4;
+    // Wave i < kPxTile finishes m block i of the tile. Its row's position
+    // (the sequence's length) and the bias are loaded before the operands,
+    // so the angles are worked out while those are in flight; the block
+    // table entry, which needs the position, goes out behind them.
+    const bool finisher = wave < kPxTile;
+    const int m_own = 16 * (mt * kPxTile + min(wave, kPxTile - 1)) + (lane & 15);
+    const int pos = e.ctx[min(m_own, M - 1)];
+    const int d = 16 * t4 + 4 * (lane >> 4); // dims d .. d + 3 and d + 64 .. d + 67
+    const int c0 = head * kHeadDim + d;
+    const uint2 bw0 = *reinterpret_cast<const uint2 *>(e.bias + c0);
+    const uint2 bw1 = *reinterpret_cast<const uint2 *>(e.bias + c0 + 64);
+    u32x4 w[kPxSteps][2], xv[kPxSteps][kPxTile];
+#pragma unroll
+    for (int j = 0; j < kPxSteps; ++j) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            w[j][u] = __builtin_nontemporal_load(wp + (size_t(8 * head + t4 + 4 * u) * KT + kb0 + j) * 64 + lane);
+#pragma unroll
+        for (int i = 0; i < kPxTile; ++i) {
+            const int mb = min(mt * kPxTile + i, last_mb);
+            xv[j][i] = xp[(size_t(mb) * KT + kb0 + j) * 64 + lane];
+        }
+    }
+    const bool rope = head < e.nh + e.nkvh;
+    float sn[4], cs[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        sn[c] = 0.f;
+        cs[c] = 1.f;
+        if (finisher && rope) sincosf(ropePhi(pos, d + c, kHeadDim, e.theta), &sn[c], &cs[c]);
+    }
+    const int page = pos >> 4, slot = pos & 15;
+    const bool in_table = pos >= 0 && page < e.max_pages;
+    const int blk = e.table[size_t(min(m_own, M - 1)) * e.max_pages + (in_table ? page : 0)];
+    f32x4 acc[2][kPxTile];
+    float ss[kPxTile];
+#pragma unroll
+    for (int i = 0; i < kPxTile; ++i) {
+        ss[i] = 0.f;
+        acc[0][i] = acc[1][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < kPxSteps; ++j)
+#pragma unroll
+        for (int i = 0; i < kPxTile; ++i) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) acc[u][i] = mfma(w[j][u], xv[j][i], acc[u][i]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float lo = __uint_as_float(xv[j][i][c] << 16), hi = __uint_as_float(xv[j][i][c] & 0xffff0000u);
+                ss[i] += lo * lo + hi * hi;
+            }
+        }
+#pragma unroll
+    for (int i = 0; i < kPxTile; ++i) {
+        ss[i] += __shfl_xor(ss[i], 16);
+        ss[i] += __shfl_xor(ss[i], 32);
+    }
+    if (lane < 16) {
+#pragma unroll
+        for (int i = 0; i < kPxTile; ++i) ssl[wave][16 * i + lane] = ss[i];
+    }
+    // Partial tiles of m block i go to LDS from every wave but i.
+#pragma unroll
+    for (int i = 0; i < kPxTile; ++i) {
+        if (i == wave) continue;
+        const int sl = wave < i ? wave : wave - 1;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) red[sl][u][i][lane] = acc[u][i];
+    }
+    __syncthreads();
+    if (!finisher || m_own >= M) return;
+    const int i = wave;
+    const int rr = 16 * i + (lane & 15);
+    const float r = rsqrtf((ssl[0][rr] + ssl[1][rr] + ssl[2][rr] + ssl[3][rr]) / float(e.hs) + e.eps);
+    f32x4 v0 = acc[0][i], v1 = acc[1][i];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        v0 += red[q][0][i][lane];
+        v1 += red[q][1][i][lane];
+    }
+    const float b0[4] = {__uint_as_float(bw0.x << 16), __uint_as_float(bw0.x & 0xffff0000u),
+                         __uint_as_float(bw0.y << 16), __uint_as_float(bw0.y & 0xffff0000u)};
+    const float b1[4] = {__uint_as_float(bw1.x << 16), __uint_as_float(bw1.x & 0xffff0000u),
+                         __uint_as_float(bw1.y << 16), __uint_as_float(bw1.y & 0xffff0000u)};
+    float y0[4], y1[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const float a = r * v0[c] + b0[c], bb = r * v1[c] + b1[c];
+        y0[c] = rope ? a * cs[c] - bb * sn[c] : a;
+        y1[c] = rope ? bb * cs[c] + a * sn[c] : bb;
+    }
+    if (head < e.nh) {
+        uint16_t *dst = e.q + (size_t(m_own) * e.nh + head) * kHeadDim + d;
+        *reinterpret_cast<uint2 *>(dst) = make_uint2(packBf16(y0[0], y0[1]), packBf16(y0[2], y0[3]));
+        *reinterpret_cast<uint2 *>(dst + 64) = make_uint2(packBf16(y1[0], y1[1]), packBf16(y1[2], y1[3]));
+        return;
+    }
+    // k or v head: the new token's page slot
+    if (!in_table || blk < 0 || blk >= e.num_blocks) {
+        if (head == e.nh && t4 == 0 && (lane >> 4) == 0) atomicOr(e.err, in_table ? 1 : 2);
+        return;
+    }
+    if (rope) {
+        uint16_t *pg = e.k_pool + (size_t(blk) * e.nkvh + (head - e.nh)) * kPageElems;
+        *reinterpret_cast<uint2 *>(pg + kPageIndex(slot, d)) = make_uint2(packBf16(y0[0], y0[1]), packBf16(y0[2], y0[3]));
+        *reinterpret_cast<uint2 *>(pg + kPageIndex(slot, d + 64)) =
+            make_uint2(packBf16(y1[0], y1[1]), packBf16(y1[2], y1[3]));
+    } else {
+        uint16_t *pg = e.v_pool + (size_t(blk) * e.nkvh + (head - e.nh - e.nkvh)) * kPageElems;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const __bf16 h0 = (__bf16)y0[c], h1 = (__bf16)y1[c];
+            pg[vPageIndex(slot, d + c)] = __builtin_bit_cast(uint16_t, h0);
+            pg[vPageIndex(slot, d + c + 64)] = __builtin_bit_cast(uint16_t, h1);
+        }
+    }
+}
+
 // Gate-up projection + row 1/rms + SwiGLU over packed x and a
 // packWeightGateUp weight. Workgroup g owns NB 16-row blocks (8 act columns
 // each) and all M rows; its 4 waves split K (12 k tiles each) and stream W
@@ -620,6 +772,23 @@ int gateUpBlocksPerGroup(int di) {
     return blocks % 5 == 0 ? 5 : blocks % 4 == 0 ? 4 : 0;
 }
 } // namespace
+
+bool qkvRopeGemmSupported(int M, int nh, int nkvh, int K) {
+    return nh > 0 && nkvh > 0 && packedXGemmSupported(M, (nh + 2 * nkvh) * kHeadDim, K);
+}
+
+void qkvRopeGemm(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *x_packed, const uint16_t *w_packed,
+                 const uint16_t *bias, const int32_t *table, const int32_t *ctx, int M, int nh, int nkvh, int K,
+                 int max_pages, int num_blocks, float eps, float theta, int *err, void *stream) {
+    LLAISYS_CHECK(qkvRopeGemmSupported(M, nh, nkvh, K),
+                  "qkvRopeGemm: unsupported shape M=" << M << " nh=" << nh << " nkvh=" << nkvh << " K=" << K);
+    const QkvRopeArgs e{q, k_pool, v_pool, bias, table, ctx, nh, nkvh, max_pages, num_blocks, K, eps, theta, err};
+    const int mtiles = (M + 16 * kPxTile - 1) / (16 * kPxTile);
+    const dim3 grid(unsigned(mtiles * (nh + 2 * nkvh) * 4));
+    hipLaunchKernelGGL(qkvRopeGemmKernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<const u32x4 *>(x_packed), reinterpret_cast<const u32x4 *>(w_packed), M, e);
+    HIP_CHECK(hipGetLastError());
+}
 
 bool gateUpSwigluSupported(int M, int di, int K) {
     return M >= 1 && M <= 16 * kGuRows && K == 4 * kPxSteps * 32 && di > 0 && di % 8 == 0 &&

@@ -57,10 +57,12 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
 // The same attention (cu_q null: query row b is sequence b) with one
 // workgroup of 4 waves per (sequence, kv head), merging in LDS: no records,
 // one launch. For batches whose contexts are of similar length (the waves
-// of a long sequence's workgroup would otherwise finish last).
+// of a long sequence's workgroup would otherwise finish last). out_packed
+// (bf16 only): the output rows in operand order (packedRowIndex) there
+// instead of in out.
 void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                       const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                      int num_blocks, float scale, int *err, void *stream);
+                      int num_blocks, float scale, int *err, void *stream, uint16_t *out_packed = nullptr);
 
 // pagedDecodeUnits with the decode step's QKV epilogue fused in (one token per
 // sequence): from qkv [B, (nh + 2 nkvh) * 128] (projection rows before bias)
@@ -192,6 +194,16 @@ void packedXGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed
 // kDecodeGemmMaxM) and the gate/up weight packed by packWeightGateUp (its
 // RMSNorm weight folded in): the gate-up projection, the row's 1/rms and the
 // SwiGLU in one kernel, from fp32 sums (no bf16 gate/up rows in between).
+// The QKV projection of a decode step (one token per row: row m is sequence
+// m at position ctx[m]) with qkvRopeAppend's epilogue in the GEMM: y = r *
+// (x W^T) + bias (r: the row's 1/rms, W with the RMSNorm weight folded in),
+// q and k heads rotated, q to q [M, nh, 128], k and v stored into their page
+// slot (block table [M, max_pages]; err bits as qkvRopeAppend). x packed,
+// W packed (packWeight), K == kDecodeGemmK, M <= kDecodeGemmMaxM.
+bool qkvRopeGemmSupported(int M, int nh, int nkvh, int K);
+void qkvRopeGemm(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t *x_packed, const uint16_t *w_packed,
+                 const uint16_t *bias, const int32_t *table, const int32_t *ctx, int M, int nh, int nkvh, int K,
+                 int max_pages, int num_blocks, float eps, float theta, int *err, void *stream);
 bool gateUpSwigluSupported(int M, int di, int K);
 void gateUpSwiglu(uint16_t *act, const uint16_t *x_packed, const uint16_t *w_packed, int M, int di, int K, float eps,
                   void *stream);

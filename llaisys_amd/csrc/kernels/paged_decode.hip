@@ -531,7 +531,7 @@ struct RopeArgs {
     uint16_t *k_pool, *v_pool;
     int hs;
     float eps, theta;
-    uint16_t *o_packed; // non-null: the output rows go there in operand order
+    uint16_t *o_packed; // non-null: the output rows go there in operand order (with or without ROPE)
 };
 
 template <bool OUT_F32, int NSTAGE, bool ROPE>
@@ -776,7 +776,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         M = Mn;
     }
     const float inv = L > 0.f ? 1.f / L : 0.f; // no keys (invalid length): zeros
-    if (ROPE && !OUT_F32 && r.o_packed) {
+    if (!OUT_F32 && r.o_packed) {
         // Dims 16 i + 4 grp .. + 3 of head h G + n: one 8 B piece of the
         // packed row (4 consecutive columns never cross an 8-column chunk).
         const int col0 = (h * G + n) * kHeadDim + 4 * grp;
@@ -948,7 +948,7 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
 namespace {
 void launchDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                        const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                       int num_blocks, float scale, int *err, const RopeArgs *rope, void *stream) {
+                       int num_blocks, float scale, int *err, const RopeArgs &r, bool rope, void *stream) {
     if (B == 0) return;
     DecodeArgs a{};
     a.q = q;
@@ -966,7 +966,6 @@ void launchDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_
     a.max_pages = max_pages;
     a.num_blocks = num_blocks;
     a.scale_log2 = scale * 1.4426950408889634f;
-    const RopeArgs r = rope ? *rope : RopeArgs{};
     // Two page pairs in flight per wave, two waves per SIMD: measured best
     // in the config-5 step (3.37 ms; three in flight at one wave per SIMD:
     // 3.47 ms; 8 waves per unit: 3.46 ms).
@@ -989,9 +988,13 @@ void launchDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_
 
 void pagedDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                       const int32_t *block_table, const int32_t *ctx_len, int B, int nh, int nkvh, int max_pages,
-                      int num_blocks, float scale, int *err, void *stream) {
+                      int num_blocks, float scale, int *err, void *stream, uint16_t *out_packed) {
+    LLAISYS_CHECK(!out_packed || (!out_f32 && (nh * kHeadDim) % 32 == 0),
+                  "pagedDecodeUnits: a packed output is bf16 with nh * 128 % 32 == 0");
+    RopeArgs r{};
+    r.o_packed = out_packed;
     launchDecodeUnits(out, out_f32, q, k_pool, v_pool, block_table, ctx_len, B, nh, nkvh, max_pages, num_blocks,
-                      scale, err, nullptr, stream);
+                      scale, err, r, false, stream);
 }
 
 bool decodeUnitsRopeSupported(int nh, int nkvh, int d) {
@@ -1010,7 +1013,7 @@ void pagedDecodeUnitsRope(void *out, bool out_f32, uint16_t *k_pool, uint16_t *v
                   "pagedDecodeUnitsRope: a packed output is bf16 with nh * 128 % 32 == 0");
     const RopeArgs r{qkv, bias, x, k_pool, v_pool, hs, eps, theta, out_packed};
     launchDecodeUnits(out, out_f32, nullptr, k_pool, v_pool, block_table, ctx_len, B, nh, nkvh, max_pages,
-                      num_blocks, scale, err, &r, stream);
+                      num_blocks, scale, err, r, true, stream);
 }
 
 } // namespace llaisys::kernels

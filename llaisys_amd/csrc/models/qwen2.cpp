@@ -72,6 +72,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     unit_rope_ = K::decodeUnitsRopeSupported(int(cfg.nh), int(cfg.nkvh), int(cfg.dh));
     if (const char *e = std::getenv("LLAISYS_DECODE_UNIT_ROPE")) unit_rope_ = unit_rope_ && e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_PACKED_X")) packed_x_ = e[0] != '0';
+    if (const char *e = std::getenv("LLAISYS_QKV_GEMM_EPILOGUE")) qkv_gemm_epilogue_ = e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -506,6 +507,8 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     // On that path the gate-up projection, the row's 1/rms and the SwiGLU
     // run as one kernel over the packed x the o projection leaves.
     const bool fused_mlp = px && L0.gate_up_wfp && K::gateUpSwigluSupported(M, di, hs);
+    // and the QKV epilogue runs in the QKV projection's epilogue.
+    const bool qkv_epi = px && qkv_gemm_epilogue_ && K::qkvRopeGemmSupported(M, int(cfg_.nh), int(cfg_.nkvh), hs);
     if (px)
         K::embedRowsPacked(u16(x_), u16(xp_), i64(tok_), u16(in_embed_), M, int64_t(cfg_.voc), hs, rt.errorWord(),
                            s);
@@ -522,19 +525,28 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
         const bool fold = fold_norm_ && T <= kFoldMaxRows;
         const uint16_t *xr = fold ? u16(x_) : nullptr;
         if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.attn_norm), T, hs, cfg_.epsilon, s);
-        if (px)
+        if (qkv_epi) {
+            // QKV epilogue (bias, 1/rms, RoPE, k/v append) in the projection's
+            // own epilogue, then the attention reading q.
+            K::qkvRopeGemm(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(xp_), u16(L.qkv_wfp), u16(L.qkv_b),
+                           i32(table_), i32(ctx_before_), M, int(cfg_.nh), int(cfg_.nkvh), hs,
+                           int(table_->shape()[1]), int(num_blocks_), cfg_.epsilon, cfg_.theta, rt.errorWord(), s);
+            K::pagedDecodeUnits(a3->data(), false, u16(q3), u16(k_pool_[l]), u16(v_pool_[l]), i32(table_),
+                                i32(ctx_after_), int(B), int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]),
+                                int(num_blocks_), scale, rt.errorWord(), s, u16(ap_));
+        } else if (px)
             K::packedXGemm(u16(qkv_), u16(xp_), u16(L.qkv_wfp), M, q + 2 * kv, hs, false, s);
         else
             project(qkv_, fold ? x_ : h_, fold ? L.qkv_wf : L.qkv_w, fold ? L.qkv_wfp : nullptr, M, q + 2 * kv, hs,
                     false, s);
-        if (decode_only && unit_decode_ && unit_rope_) {
+        if (!qkv_epi && decode_only && unit_decode_ && unit_rope_) {
             // QKV epilogue (bias, 1/rms, RoPE, k/v append) inside the attention
             // launch: one kernel fewer per layer.
             K::pagedDecodeUnitsRope(a3->data(), false, u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), xr,
                                     hs, cfg_.epsilon, cfg_.theta, i32(table_), i32(ctx_after_), int(B),
                                     int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]), int(num_blocks_), scale,
                                     rt.errorWord(), s, px ? u16(ap_) : nullptr);
-        } else {
+        } else if (!qkv_epi) {
             K::qkvRopeAppend(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(qkv_), u16(L.qkv_b), i32(table_),
                              i32(ctx_before_), decode_only ? nullptr : i32(cu_), M, int(B), int(cfg_.nh),
                              int(cfg_.nkvh), int(cfg_.dh), int(table_->shape()[1]), int(num_blocks_), cfg_.theta,

@@ -152,6 +152,10 @@ private:
     // reduce and the attention write packed copies of their rows.
     // LLAISYS_PACKED_X=0 keeps the library GEMMs there.
     bool packed_x_ = true;
+    // On that path the QKV epilogue (bias, 1/rms, RoPE, k/v append) runs in
+    // the QKV projection's epilogue, and the attention reads q
+    // (LLAISYS_QKV_GEMM_EPILOGUE=0: in the attention kernel instead).
+    bool qkv_gemm_epilogue_ = true;
     void chooseDecodeAttention(size_t B, int32_t min_ctx, int32_t max_ctx);
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
     std::map<size_t, DecodeGraph> graphs_;       // one step (step())

@@ -193,18 +193,20 @@ def test_fused_qkv_epilogue_matches_separate_launch(monkeypatch):
 
 
 def test_packed_operand_projections_match_library_and_reference(monkeypatch):
-    # Decode steps on the fused unit attention at K = 1536 run qkv and o with
-    # both operands in MFMA operand order: the embedding, the split-K reduce
-    # and the attention write packed copies of x and of the attention output.
-    # 66 sequences (132 units) over 4 decode steps: against transformers, and
-    # step by step against the same model with library GEMMs there
-    # (LLAISYS_PACKED_X=0; other fp32 summation orders, so within a bound).
-    # A wrong packed index or tile would move the logits by far more. At this
-    # width the bf16 activations alone put both runs near the small models'
-    # 3 % bound, so each run's error against transformers is measured and
-    # the packed run's may exceed the library run's by at most a quarter (plus
-    # 0.5 % of the logits' max). Then a multi-step decode call (captured
-    # graph) against single steps.
+    # Decode steps on the unit attention at K = 1536 run the projections over
+    # packed operands: the embedding, the split-K reduce, the attention and
+    # the o projection write copies of their rows in MFMA operand order; qkv
+    # carries the QKV epilogue (bias, 1/rms, RoPE, k/v append), gate-up the
+    # row's 1/rms and the SwiGLU. 66 sequences (132 units) over 4 decode
+    # steps, each step's logits against transformers for every 16th
+    # sequence, for this path and for the same model with library GEMMs
+    # (LLAISYS_PACKED_X=0). At this width the bf16 activations alone put both
+    # ~3 % of the logits' max from transformers, so the packed path's error
+    # may exceed the library path's by at most a quarter (plus 0.5 % of the
+    # max); a wrong packed index, tile or slot moves the logits by tens of
+    # percent. The two runs also agree to 5 % (each ~3 % off, in its own
+    # direction). Then a multi-step decode call (captured graph) against
+    # single steps.
     monkeypatch.setenv("LLAISYS_DECODE_UNITS", "1")
     monkeypatch.setenv("LLAISYS_DECODE_UNIT_ROPE", "1")
     nseq = 66
@@ -218,7 +220,7 @@ def test_packed_operand_projections_match_library_and_reference(monkeypatch):
         for s in range(0, nseq, 11):
             model.step(ids[s:s + 11], prompts[s:s + 11])
         hist = [list(p) for p in prompts]
-        steps = []
+        steps, err, scale = [], 0.0, 0.0
         for k in range(4):  # the same fed tokens in both runs
             fed = prompt(nseq, model.meta.voc, 750 + k)
             nxt = model.step(ids, [[t] for t in fed])
@@ -226,11 +228,10 @@ def test_packed_operand_projections_match_library_and_reference(monkeypatch):
                 h.append(t)
             logits = to_torch(model.logits()).float().clone()
             steps.append(logits)
-        err, scale = 0.0, 0.0
-        for r in range(0, nseq, 16):
-            ref = hf_logits(hf, hist[r])[-1]
-            err = max(err, (logits[r] - ref).abs().max().item())
-            scale = max(scale, ref.abs().max().item())
+            for r in range(0, nseq, 16):
+                ref = hf_logits(hf, hist[r])[-1]
+                err = max(err, (logits[r] - ref).abs().max().item())
+                scale = max(scale, ref.abs().max().item())
         ref_err[packed] = (err, scale)
         if packed == "1":
             forks = [model.fork(i) for i in ids]
@@ -244,14 +245,11 @@ def test_packed_operand_projections_match_library_and_reference(monkeypatch):
         runs.append(steps)
         del model, hf
     (e_px, scale), (e_lib, _) = ref_err["1"], ref_err["0"]
-    print(f"max |logit - transformers|: packed {e_px:.4g}, library {e_lib:.4g}, max |logit| {scale:.4g}")
+    print(f"max |logit - transformers| over 4 steps: packed {e_px:.4g}, library {e_lib:.4g}, max |logit| {scale:.4g}")
     assert e_px <= 1.25 * e_lib + 5e-3 * scale
     assert e_lib <= 0.05 * scale
-    # Run against run: each is ~3 % of the logits' max from transformers here,
-    # and two summation orders measured ~1 % apart; 2.5 % still fails a wrong
-    # tile (tens of percent).
     for lg_a, lg_b in zip(*runs):
-        assert (lg_a - lg_b).abs().max().item() <= 2.5e-2 * lg_b.abs().max().item()
+        assert (lg_a - lg_b).abs().max().item() <= 5e-2 * lg_b.abs().max().item()
 
 
 def test_infer_restarts_on_a_new_history_and_reuses_cached_blocks():
