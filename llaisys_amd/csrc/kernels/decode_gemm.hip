@@ -40,6 +40,13 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// ss + x.lo^2 + x.hi^2 for a word of two bf16 values (one v_dot2 instruction).
+__device__ __forceinline__ float addSquares(float ss, uint32_t w) {
+    const bf16x2 v = __builtin_bit_cast(bf16x2, w);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
+}
 
 
 struct GemmArgs {
@@ -589,10 +596,7 @@ __global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const 
 #pragma unroll
             for (int u = 0; u < 2; ++u) acc[u][i] = mfma(w[j][u], xv[j][i], acc[u][i]);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float lo = __uint_as_float(xv[j][i][c] << 16), hi = __uint_as_float(xv[j][i][c] & 0xffff0000u);
-                ss[i] += lo * lo + hi * hi;
-            }
+            for (int c = 0; c < 4; ++c) ss[i] = addSquares(ss[i], xv[j][i][c]);
         }
 #pragma unroll
     for (int i = 0; i < kPxTile; ++i) {
@@ -714,10 +718,7 @@ gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int d
 #pragma unroll
         for (int i = 0; i < MB; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float lo = __uint_as_float(rx[st][i][e] << 16), hi = __uint_as_float(rx[st][i][e] & 0xffff0000u);
-                ss[i] += lo * lo + hi * hi;
-            }
+            for (int e = 0; e < 4; ++e) ss[i] = addSquares(ss[i], rx[st][i][e]);
         if (j + R < kPxSteps) issue(st, j + R);
         __builtin_amdgcn_sched_barrier(0);
     }
