@@ -691,7 +691,12 @@ gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int d
     const u32x4 *wl = wp + (size_t(blk0) * KT + kb0) * 64 + lane;
     const u32x4 *xl = xp + size_t(kb0) * 64 + lane;
     u32x4 rw[R][NB], rx[R][MB];
-    auto issue = [&](int st, int j) {
+    // Every workgroup reads the same X tiles: each starts its k range at its
+    // own step (the sum is the same; the order of the k partials is fixed per
+    // workgroup), so those of one XCD do not ask for the same lines at once.
+    const int krot = int(blockIdx.x) % kPxSteps;
+    auto issue = [&](int st, int j0) {
+        const int j = j0 + krot < kPxSteps ? j0 + krot : j0 + krot - kPxSteps;
 #pragma unroll
         for (int t = 0; t < NB; ++t) rw[st][t] = __builtin_nontemporal_load(wl + (size_t(t) * KT + j) * 64);
 #pragma unroll
