@@ -521,8 +521,7 @@ __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x
 // g % 4): dims d and d + 64 of the head sit in the same lane, so the
 // rotation needs no exchange. The operands and the k sweep are those of
 // packedXGemmKernel; each wave also sums the squares of the x values it
-// loads, per row, for the row's 1/rms; waves 0 and 1 each finish one 16-row
-// block.
+// loads, per row, for the row's 1/rms; the four waves share the finish.
 struct QkvRopeArgs {
     uint16_t *q, *k_pool, *v_pool;
     const uint16_t *bias;
@@ -538,7 +537,7 @@ __device__ __forceinline__ uint32_t packBf16(float a, float b) {
 }
 
 __global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const u32x4 *wp, int M, QkvRopeArgs e) {
-    __shared__ f32x4 red[3][2][kPxTile][64];
+    __shared__ f32x4 red[4][2][kPxTile][64];
     __shared__ float ssl[4][16 * kPxTile];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -548,17 +547,19 @@ __global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const 
     const int head = g >> 2, t4 = g & 3;
     const int kb0 = wave * kPxSteps;
     const int last_mb = (M - 1) >> 4;
-    // Wave i < kPxTile finishes m block i of the tile. Its row's position
-    // (the sequence's length) and the bias are loaded before the operands,
-    // so the angles are worked out while those are in flight; the block
-    // table entry, which needs the position, goes out behind them.
-    const bool finisher = wave < kPxTile;
-    const int m_own = 16 * (mt * kPxTile + min(wave, kPxTile - 1)) + (lane & 15);
+    // Wave w finishes m block w % 2 of the tile, elements 2 (w / 2) and
+    // 2 (w / 2) + 1 of the lane's four: dims dd, dd + 1 and dd + 64, dd + 65.
+    // Its row's position (the sequence's length) and the bias are loaded
+    // before the operands, so the angles are worked out while those are in
+    // flight; the block-table entry, which needs the position, goes out
+    // behind them.
+    const int fi = wave & 1, ch = wave >> 1;
+    const int m_own = 16 * (mt * kPxTile + fi) + (lane & 15);
     const int pos = e.ctx[min(m_own, M - 1)];
-    const int d = 16 * t4 + 4 * (lane >> 4); // dims d .. d + 3 and d + 64 .. d + 67
-    const int c0 = head * kHeadDim + d;
-    const uint2 bw0 = *reinterpret_cast<const uint2 *>(e.bias + c0);
-    const uint2 bw1 = *reinterpret_cast<const uint2 *>(e.bias + c0 + 64);
+    const int dd = 16 * t4 + 4 * (lane >> 4) + 2 * ch;
+    const int c0 = head * kHeadDim + dd;
+    const uint32_t bw0 = *reinterpret_cast<const uint32_t *>(e.bias + c0);
+    const uint32_t bw1 = *reinterpret_cast<const uint32_t *>(e.bias + c0 + 64);
     u32x4 w[kPxSteps][2], xv[kPxSteps][kPxTile];
 #pragma unroll
     for (int j = 0; j < kPxSteps; ++j) {
@@ -572,12 +573,12 @@ __global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const 
         }
     }
     const bool rope = head < e.nh + e.nkvh;
-    float sn[4], cs[4];
+    float sn[2], cs[2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 2; ++c) {
         sn[c] = 0.f;
         cs[c] = 1.f;
-        if (finisher && rope) sincosf(ropePhi(pos, d + c, kHeadDim, e.theta), &sn[c], &cs[c]);
+        if (rope) sincosf(ropePhi(pos, dd + c, kHeadDim, e.theta), &sn[c], &cs[c]);
     }
     const int page = pos >> 4, slot = pos & 15;
     const bool in_table = pos >= 0 && page < e.max_pages;
@@ -607,59 +608,55 @@ __global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const 
 #pragma unroll
         for (int i = 0; i < kPxTile; ++i) ssl[wave][16 * i + lane] = ss[i];
     }
-    // Partial tiles of m block i go to LDS from every wave but i.
 #pragma unroll
-    for (int i = 0; i < kPxTile; ++i) {
-        if (i == wave) continue;
-        const int sl = wave < i ? wave : wave - 1;
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) red[sl][u][i][lane] = acc[u][i];
-    }
+        for (int i = 0; i < kPxTile; ++i) red[wave][u][i][lane] = acc[u][i];
     __syncthreads();
-    if (!finisher || m_own >= M) return;
-    const int i = wave;
-    const int rr = 16 * i + (lane & 15);
+    if (m_own >= M) return;
+    const int rr = 16 * fi + (lane & 15);
     const float r = rsqrtf((ssl[0][rr] + ssl[1][rr] + ssl[2][rr] + ssl[3][rr]) / float(e.hs) + e.eps);
-    f32x4 v0 = acc[0][i], v1 = acc[1][i];
+    float v0[2] = {0.f, 0.f}, v1[2] = {0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 3; ++q) {
-        v0 += red[q][0][i][lane];
-        v1 += red[q][1][i][lane];
+    for (int q = 0; q < 4; ++q) { // the k partials in wave order
+        const f32x4 p0 = red[q][0][fi][lane], p1 = red[q][1][fi][lane];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            v0[c] += p0[2 * ch + c];
+            v1[c] += p1[2 * ch + c];
+        }
     }
-    const float b0[4] = {__uint_as_float(bw0.x << 16), __uint_as_float(bw0.x & 0xffff0000u),
-                         __uint_as_float(bw0.y << 16), __uint_as_float(bw0.y & 0xffff0000u)};
-    const float b1[4] = {__uint_as_float(bw1.x << 16), __uint_as_float(bw1.x & 0xffff0000u),
-                         __uint_as_float(bw1.y << 16), __uint_as_float(bw1.y & 0xffff0000u)};
-    float y0[4], y1[4];
+    const float b0[2] = {__uint_as_float(bw0 << 16), __uint_as_float(bw0 & 0xffff0000u)};
+    const float b1[2] = {__uint_as_float(bw1 << 16), __uint_as_float(bw1 & 0xffff0000u)};
+    float y0[2], y1[2];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 2; ++c) {
         const float a = r * v0[c] + b0[c], bb = r * v1[c] + b1[c];
         y0[c] = rope ? a * cs[c] - bb * sn[c] : a;
         y1[c] = rope ? bb * cs[c] + a * sn[c] : bb;
     }
     if (head < e.nh) {
-        uint16_t *dst = e.q + (size_t(m_own) * e.nh + head) * kHeadDim + d;
-        *reinterpret_cast<uint2 *>(dst) = make_uint2(packBf16(y0[0], y0[1]), packBf16(y0[2], y0[3]));
-        *reinterpret_cast<uint2 *>(dst + 64) = make_uint2(packBf16(y1[0], y1[1]), packBf16(y1[2], y1[3]));
+        uint16_t *dst = e.q + (size_t(m_own) * e.nh + head) * kHeadDim + dd;
+        *reinterpret_cast<uint32_t *>(dst) = packBf16(y0[0], y0[1]);
+        *reinterpret_cast<uint32_t *>(dst + 64) = packBf16(y1[0], y1[1]);
         return;
     }
     // k or v head: the new token's page slot
     if (!in_table || blk < 0 || blk >= e.num_blocks) {
-        if (head == e.nh && t4 == 0 && (lane >> 4) == 0) atomicOr(e.err, in_table ? 1 : 2);
+        if (head == e.nh && t4 == 0 && ch == 0 && (lane >> 4) == 0) atomicOr(e.err, in_table ? 1 : 2);
         return;
     }
     if (rope) {
         uint16_t *pg = e.k_pool + (size_t(blk) * e.nkvh + (head - e.nh)) * kPageElems;
-        *reinterpret_cast<uint2 *>(pg + kPageIndex(slot, d)) = make_uint2(packBf16(y0[0], y0[1]), packBf16(y0[2], y0[3]));
-        *reinterpret_cast<uint2 *>(pg + kPageIndex(slot, d + 64)) =
-            make_uint2(packBf16(y1[0], y1[1]), packBf16(y1[2], y1[3]));
+        *reinterpret_cast<uint32_t *>(pg + kPageIndex(slot, dd)) = packBf16(y0[0], y0[1]);
+        *reinterpret_cast<uint32_t *>(pg + kPageIndex(slot, dd + 64)) = packBf16(y1[0], y1[1]);
     } else {
         uint16_t *pg = e.v_pool + (size_t(blk) * e.nkvh + (head - e.nh - e.nkvh)) * kPageElems;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < 2; ++c) {
             const __bf16 h0 = (__bf16)y0[c], h1 = (__bf16)y1[c];
-            pg[vPageIndex(slot, d + c)] = __builtin_bit_cast(uint16_t, h0);
-            pg[vPageIndex(slot, d + c + 64)] = __builtin_bit_cast(uint16_t, h1);
+            pg[vPageIndex(slot, dd + c)] = __builtin_bit_cast(uint16_t, h0);
+            pg[vPageIndex(slot, dd + c + 64)] = __builtin_bit_cast(uint16_t, h1);
         }
     }
 }
