@@ -432,16 +432,18 @@ template <int MB> void launchSplitK(const SplitKArgs &a, hipStream_t st) {
 // issues all 24 W tiles and 24 X tiles of its range (1 KiB each, 192
 // registers) and the old Y before its first MFMA: at M = 128 the time is
 // the workgroup's 192 KiB of operands reaching the CU, which a deeper
-// schedule cannot shorten. The four k partials meet in LDS; wave 0 adds
-// them in wave order (plus the old Y) and rounds once. An m block past the
-// last one re-reads the last (its rows are computed and dropped).
+// schedule cannot shorten. The four k partials meet in LDS; each wave adds
+// one 16 x 16 tile's in wave order (plus the old Y) and rounds once. An m
+// block past the last one re-reads the last (its rows are computed and
+// dropped).
 constexpr int kPxTile = 2;   // 16-row blocks per tile side
 constexpr int kPxSteps = 12; // k tiles per wave (K = 4 x 12 x 32)
 
 template <bool ACC>
 __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x4 *xp, const u32x4 *wp, int M,
                                                          int N, uint16_t *y_packed) {
-    __shared__ f32x4 red[3][kPxTile][kPxTile][64];
+    static_assert(kPxTile * kPxTile == 4, "one 16 x 16 tile per wave in the epilogue");
+    __shared__ f32x4 red[4][kPxTile][kPxTile][64];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     constexpr int KT = 4 * kPxSteps;
@@ -461,17 +463,13 @@ __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x
             xv[j][i] = xp[(size_t(mb) * KT + kb0 + j) * 64 + lane];
         }
     }
-    // Lane holds C^T rows n0 + 0..3 of column m for each (t, i).
-    uint2 old_y[kPxTile][kPxTile];
-#pragma unroll
-    for (int t = 0; t < kPxTile; ++t)
-#pragma unroll
-        for (int i = 0; i < kPxTile; ++i) {
-            old_y[t][i] = make_uint2(0, 0);
-            const int m = min(16 * (mt * kPxTile + i) + (lane & 15), M - 1);
-            const int n0 = 16 * (nt * kPxTile + t) + 4 * (lane >> 4);
-            if (ACC && wave == 0) old_y[t][i] = *reinterpret_cast<const uint2 *>(y + size_t(m) * N + n0);
-        }
+    // Wave w finishes tile (t, i) = (w / 2, w % 2): lane holds C^T rows
+    // n0 + 0..3 of column m. Its old Y goes out behind the operands.
+    const int ft = wave >> 1, fi = wave & 1;
+    const int m = 16 * (mt * kPxTile + fi) + (lane & 15);
+    const int n0 = 16 * (nt * kPxTile + ft) + 4 * (lane >> 4);
+    uint2 old_y = make_uint2(0, 0);
+    if (ACC) old_y = *reinterpret_cast<const uint2 *>(y + size_t(min(m, M - 1)) * N + n0);
     f32x4 acc[kPxTile][kPxTile];
 #pragma unroll
     for (int t = 0; t < kPxTile; ++t)
@@ -483,37 +481,22 @@ __global__ void __launch_bounds__(256) packedXGemmKernel(uint16_t *y, const u32x
         for (int t = 0; t < kPxTile; ++t)
 #pragma unroll
             for (int i = 0; i < kPxTile; ++i) acc[t][i] = mfma(w[j][t], xv[j][i], acc[t][i]);
-    if (wave > 0) {
-#pragma unroll
-        for (int t = 0; t < kPxTile; ++t)
-#pragma unroll
-            for (int i = 0; i < kPxTile; ++i) red[wave - 1][t][i][lane] = acc[t][i];
-    }
-    __syncthreads();
-    if (wave != 0) return;
 #pragma unroll
     for (int t = 0; t < kPxTile; ++t)
 #pragma unroll
-        for (int i = 0; i < kPxTile; ++i) {
-            const uint2 o = old_y[t][i];
-            f32x4 v = ACC ? f32x4{__uint_as_float(o.x << 16), __uint_as_float(o.x & 0xffff0000u),
-                                  __uint_as_float(o.y << 16), __uint_as_float(o.y & 0xffff0000u)}
-                          : f32x4{0.f, 0.f, 0.f, 0.f};
-            v += acc[t][i];
+        for (int i = 0; i < kPxTile; ++i) red[wave][t][i][lane] = acc[t][i];
+    __syncthreads();
+    if (m >= M) return;
+    f32x4 v = ACC ? f32x4{__uint_as_float(old_y.x << 16), __uint_as_float(old_y.x & 0xffff0000u),
+                          __uint_as_float(old_y.y << 16), __uint_as_float(old_y.y & 0xffff0000u)}
+                  : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 3; ++r) v += red[r][t][i][lane];
-            const int m = 16 * (mt * kPxTile + i) + (lane & 15);
-            const int n0 = 16 * (nt * kPxTile + t) + 4 * (lane >> 4);
-            if (m < M) {
-                const __bf16 e0 = (__bf16)v[0], e1 = (__bf16)v[1], e2 = (__bf16)v[2], e3 = (__bf16)v[3];
-                const uint32_t w0 = uint32_t(__builtin_bit_cast(uint16_t, e0)) |
-                                    (uint32_t(__builtin_bit_cast(uint16_t, e1)) << 16);
-                const uint32_t w1 = uint32_t(__builtin_bit_cast(uint16_t, e2)) |
-                                    (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
-                *reinterpret_cast<uint2 *>(y + size_t(m) * N + n0) = make_uint2(w0, w1);
-                if (y_packed) *reinterpret_cast<uint2 *>(y_packed + packedRowIndex(m, n0, N)) = make_uint2(w0, w1);
-            }
-        }
+    for (int q = 0; q < 4; ++q) v += red[q][ft][fi][lane]; // the k partials in wave order
+    const __bf16 e0 = (__bf16)v[0], e1 = (__bf16)v[1], e2 = (__bf16)v[2], e3 = (__bf16)v[3];
+    const uint32_t w0 = uint32_t(__builtin_bit_cast(uint16_t, e0)) | (uint32_t(__builtin_bit_cast(uint16_t, e1)) << 16);
+    const uint32_t w1 = uint32_t(__builtin_bit_cast(uint16_t, e2)) | (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
+    *reinterpret_cast<uint2 *>(y + size_t(m) * N + n0) = make_uint2(w0, w1);
+    if (y_packed) *reinterpret_cast<uint2 *>(y_packed + packedRowIndex(m, n0, N)) = make_uint2(w0, w1);
 }
 
 // QKV projection + qkvRopeAppend's epilogue. Workgroup (mt, g) owns rows
