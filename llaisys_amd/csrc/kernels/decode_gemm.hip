@@ -659,7 +659,7 @@ constexpr int kGuRows = 8; // 16-row m blocks (M <= 128)
 
 template <int NB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int di, float eps) {
+gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int di, float eps, int act_packed) {
     constexpr int KT = 4 * kPxSteps, MB = kGuRows, R = kGuRing;
     __shared__ f32x4 red[3][NB][MB][64];
     __shared__ float ssl[4][16 * MB];
@@ -746,8 +746,9 @@ gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int d
             const __bf16 b0 = (__bf16)(u0 * g0 / (1.f + expf(-g0)));
             const __bf16 b1 = (__bf16)(u1 * g1 / (1.f + expf(-g1)));
             const int col = 8 * (blk0 + t) + 4 * ((lane >> 4) & 1) + (lo ? 0 : 2);
+            // act_packed: in operand order (the two columns share one 8-column chunk)
             if (m < M)
-                *reinterpret_cast<uint32_t *>(act + size_t(m) * di + col) =
+                *reinterpret_cast<uint32_t *>(act + (act_packed ? packedRowIndex(m, col, di) : size_t(m) * di + col)) =
                     uint32_t(__builtin_bit_cast(uint16_t, b0)) | (uint32_t(__builtin_bit_cast(uint16_t, b1)) << 16);
         }
     }
@@ -757,7 +758,130 @@ int gateUpBlocksPerGroup(int di) {
     const int blocks = 2 * di / 16;
     return blocks % 5 == 0 ? 5 : blocks % 4 == 0 ? 4 : 0;
 }
+
+// Split-K partials over packed X (long K): workgroup (g, s) owns W row
+// blocks kSkBlocks g .. + kSkBlocks - 1 and k tiles [4 KSW s, 4 KSW (s + 1));
+// its 4 waves split that range (KSW tiles each) and stream W and X of one k
+// step together through a kSkRing-deep register ring, as gateUpSwiglu does.
+// With X streamed instead of staged in LDS, a workgroup can cover a longer
+// k range: fewer splits, so fewer fp32 partials to write and sum. The four
+// k partials meet in LDS; the wave that owns m blocks 2w, 2w + 1 adds them in
+// wave order and stores part[s][m][n] (m < M).
+constexpr int kSkBlocks = 4;
+constexpr int kSkRing = 3;
+
+template <int KSW>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+splitKPackedKernel(float *part, const u32x4 *xp, const u32x4 *wp, int M, int N, int KT, int S) {
+    constexpr int NB = kSkBlocks, MB = kGuRows, R = KSW < kSkRing ? KSW : kSkRing;
+    __shared__ f32x4 red[3][NB][MB][64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int g = int(blockIdx.x) / S, s = int(blockIdx.x) % S;
+    const int kb0 = (4 * s + wave) * KSW;
+    const int last_mb = (M - 1) >> 4;
+    const u32x4 *wl = wp + (size_t(NB * g) * KT + kb0) * 64 + lane;
+    const u32x4 *xl = xp + size_t(kb0) * 64 + lane;
+    u32x4 rw[R][NB], rx[R][MB];
+    auto issue = [&](int st, int j) {
+#pragma unroll
+        for (int t = 0; t < NB; ++t) rw[st][t] = __builtin_nontemporal_load(wl + (size_t(t) * KT + j) * 64);
+#pragma unroll
+        for (int i = 0; i < MB; ++i) rx[st][i] = xl[(size_t(min(i, last_mb)) * KT + j) * 64];
+    };
+#pragma unroll
+    for (int j = 0; j < R; ++j) issue(j, j);
+    f32x4 acc[NB][MB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t)
+#pragma unroll
+        for (int i = 0; i < MB; ++i) acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < KSW; ++j) {
+        const int st = j % R;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int t = 0; t < NB; ++t) acc[t][i] = mfma(rw[st][t], rx[st][i], acc[t][i]);
+        if (j + R < KSW) issue(st, j + R);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int owner = i / 2;
+        if (owner == wave) continue;
+        const int slot = wave < owner ? wave : wave - 1;
+#pragma unroll
+        for (int t = 0; t < NB; ++t) red[slot][t][i][lane] = acc[t][i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        if (i / 2 != wave) continue;
+        const int m = 16 * i + (lane & 15);
+        if (m >= M) continue;
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v += q == wave ? acc[t][i] : red[q < wave ? q : q - 1][t][i][lane];
+            const int n0 = 16 * (NB * g + t) + 4 * (lane >> 4);
+            *reinterpret_cast<f32x4 *>(part + (size_t(s) * M + m) * N + n0) = v;
+        }
+    }
+}
+
+// Splits S and k tiles per wave for splitKPackedKernel: the largest S with
+// S * (row blocks / kSkBlocks) workgroups on the chip and an instantiated
+// KT / (4 S); 0 if none.
+int splitKPackedSplits(int N, int K, int *ksw) {
+    const int KT = K / 32, groups = N / (16 * kSkBlocks);
+    for (int S = 16; S >= 1; --S) {
+        if (KT % (4 * S)) continue;
+        const int k = KT / (4 * S);
+        if ((k == 2 || k == 4 || k == 7 || k == 8) && groups * S <= computeUnitsOf()) {
+            *ksw = k;
+            return S;
+        }
+    }
+    return 0;
+}
 } // namespace
+
+bool splitKPackedSupported(int M, int N, int K) {
+    int ksw = 0;
+    return M >= 1 && M <= 16 * kGuRows && K % 32 == 0 && N % (16 * kSkBlocks) == 0 && K <= kSplitKMaxK &&
+           splitKPackedSplits(N, K, &ksw) > 0;
+}
+
+size_t splitKPackedWorkspaceBytes(int M, int N, int K) {
+    int ksw = 0;
+    return size_t(splitKPackedSplits(N, K, &ksw)) * M * N * sizeof(float);
+}
+
+void splitKPackedGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed, int M, int N, int K,
+                      bool accumulate, float *partials, void *stream, uint16_t *y_packed) {
+    LLAISYS_CHECK(splitKPackedSupported(M, N, K),
+                  "splitKPackedGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
+    int ksw = 0;
+    const int S = splitKPackedSplits(N, K, &ksw);
+    const dim3 grid(unsigned(N / (16 * kSkBlocks) * S));
+    auto st = static_cast<hipStream_t>(stream);
+    const auto *xp = reinterpret_cast<const u32x4 *>(x_packed);
+    const auto *wp = reinterpret_cast<const u32x4 *>(w_packed);
+    switch (ksw) {
+    case 2: hipLaunchKernelGGL(splitKPackedKernel<2>, grid, dim3(256), 0, st, partials, xp, wp, M, N, K / 32, S); break;
+    case 4: hipLaunchKernelGGL(splitKPackedKernel<4>, grid, dim3(256), 0, st, partials, xp, wp, M, N, K / 32, S); break;
+    case 7: hipLaunchKernelGGL(splitKPackedKernel<7>, grid, dim3(256), 0, st, partials, xp, wp, M, N, K / 32, S); break;
+    default: hipLaunchKernelGGL(splitKPackedKernel<8>, grid, dim3(256), 0, st, partials, xp, wp, M, N, K / 32, S); break;
+    }
+    HIP_CHECK(hipGetLastError());
+    const size_t threads = size_t(M) * (N / 4);
+    hipLaunchKernelGGL(splitKReduceKernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0, st, y, partials, M, N,
+                       S, accumulate ? 1 : 0, y_packed);
+    HIP_CHECK(hipGetLastError());
+}
 
 bool qkvRopeGemmSupported(int M, int nh, int nkvh, int K) {
     return nh > 0 && nkvh > 0 && packedXGemmSupported(M, (nh + 2 * nkvh) * kHeadDim, K);
@@ -782,7 +906,7 @@ bool gateUpSwigluSupported(int M, int di, int K) {
 }
 
 void gateUpSwiglu(uint16_t *act, const uint16_t *x_packed, const uint16_t *w_packed, int M, int di, int K, float eps,
-                  void *stream) {
+                  void *stream, bool act_packed) {
     LLAISYS_CHECK(gateUpSwigluSupported(M, di, K), "gateUpSwiglu: unsupported shape M=" << M << " di=" << di
                                                                                         << " K=" << K);
     const int nb = gateUpBlocksPerGroup(di);
@@ -791,9 +915,9 @@ void gateUpSwiglu(uint16_t *act, const uint16_t *x_packed, const uint16_t *w_pac
     const auto *xp = reinterpret_cast<const u32x4 *>(x_packed);
     const auto *wp = reinterpret_cast<const u32x4 *>(w_packed);
     if (nb == 5)
-        hipLaunchKernelGGL(gateUpSwigluKernel<5>, grid, dim3(256), 0, st, act, xp, wp, M, di, eps);
+        hipLaunchKernelGGL(gateUpSwigluKernel<5>, grid, dim3(256), 0, st, act, xp, wp, M, di, eps, act_packed ? 1 : 0);
     else
-        hipLaunchKernelGGL(gateUpSwigluKernel<4>, grid, dim3(256), 0, st, act, xp, wp, M, di, eps);
+        hipLaunchKernelGGL(gateUpSwigluKernel<4>, grid, dim3(256), 0, st, act, xp, wp, M, di, eps, act_packed ? 1 : 0);
     HIP_CHECK(hipGetLastError());
 }
 

@@ -206,7 +206,17 @@ void qkvRopeGemm(uint16_t *q, uint16_t *k_pool, uint16_t *v_pool, const uint16_t
                  int max_pages, int num_blocks, float eps, float theta, int *err, void *stream);
 bool gateUpSwigluSupported(int M, int di, int K);
 void gateUpSwiglu(uint16_t *act, const uint16_t *x_packed, const uint16_t *w_packed, int M, int di, int K, float eps,
-                  void *stream);
+                  void *stream, bool act_packed = false); // act_packed: act written in operand order
+// The split-K product over packed X (K > kDecodeGemmK, N % 64 == 0, M <=
+// kDecodeGemmMaxM; W packed by packWeight): X streams through registers
+// beside W instead of being staged in LDS, so each workgroup covers a longer
+// k range and the fp32 partials (splitKPackedWorkspaceBytes) are fewer; the
+// reduce adds the old Y (accumulate), rounds once and, given y_packed, also
+// writes Y in operand order.
+bool splitKPackedSupported(int M, int N, int K);
+size_t splitKPackedWorkspaceBytes(int M, int N, int K);
+void splitKPackedGemm(uint16_t *y, const uint16_t *x_packed, const uint16_t *w_packed, int M, int N, int K,
+                      bool accumulate, float *partials, void *stream, uint16_t *y_packed = nullptr);
 
 // ---- Qwen2 step glue (qwen2_step.hip), bf16
 // qkv [T, (nh + 2 nkvh) d] + bias -> q [T, nh, d] rotated by position, and k

@@ -73,6 +73,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     if (const char *e = std::getenv("LLAISYS_DECODE_UNIT_ROPE")) unit_rope_ = unit_rope_ && e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_PACKED_X")) packed_x_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_QKV_GEMM_EPILOGUE")) qkv_gemm_epilogue_ = e[0] != '0';
+    if (const char *e = std::getenv("LLAISYS_SPLITK_PACKED")) splitk_packed_ = e[0] != '0';
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -195,6 +196,7 @@ void Qwen2Model::ensureWorkspace(size_t T, size_t B, size_t ints32, size_t ints6
         attn_ = dev({cap, cfg_.nh, cfg_.dh}, dt, dev_);
         xp_ = dev({K::packedRowsElems(int(cap), int(cfg_.hs))}, dt, dev_);
         ap_ = dev({K::packedRowsElems(int(cap), int(q))}, dt, dev_);
+        actp_ = dev({K::packedRowsElems(int(cap), int(cfg_.di))}, dt, dev_);
         gu_ = dev({cap, 2 * cfg_.di}, dt, dev_);
         act_ = dev({cap, cfg_.di}, dt, dev_);
         cap_T_ = cap;
@@ -509,6 +511,8 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     const bool fused_mlp = px && L0.gate_up_wfp && K::gateUpSwigluSupported(M, di, hs);
     // and the QKV epilogue runs in the QKV projection's epilogue.
     const bool qkv_epi = px && qkv_gemm_epilogue_ && K::qkvRopeGemmSupported(M, int(cfg_.nh), int(cfg_.nkvh), hs);
+    // and the down projection reads the SwiGLU output packed.
+    const bool down_px = fused_mlp && splitk_packed_ && K::splitKPackedSupported(M, hs, di) && di % 32 == 0;
     if (px)
         K::embedRowsPacked(u16(x_), u16(xp_), i64(tok_), u16(in_embed_), M, int64_t(cfg_.voc), hs, rt.errorWord(),
                            s);
@@ -564,7 +568,8 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
         else
             project(x_, attn_, L.o_w, L.o_wp, M, hs, q, true, s);
         if (fused_mlp) {
-            K::gateUpSwiglu(u16(act_), u16(xp_), u16(L.gate_up_wfp), M, di, hs, cfg_.epsilon, s);
+            K::gateUpSwiglu(down_px ? u16(actp_) : u16(act_), u16(xp_), u16(L.gate_up_wfp), M, di, hs, cfg_.epsilon, s,
+                            down_px);
         } else {
             if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
             const tensor_t gup = fold ? L.gate_up_wfp : tensor_t();
@@ -573,7 +578,12 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
             // and up columns interleaved as well.
             K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s, takesDecodeGemm(gup, M, 2 * di, hs));
         }
-        project(x_, act_, L.down_w, L.down_wp, M, hs, di, true, s, px ? u16(xp_) : nullptr);
+        if (down_px) {
+            auto *part = static_cast<float *>(rt.scratch(K::splitKPackedWorkspaceBytes(M, hs, di)));
+            K::splitKPackedGemm(u16(x_), u16(actp_), u16(L.down_wp), M, hs, di, true, part, s, u16(xp_));
+        } else {
+            project(x_, act_, L.down_w, L.down_wp, M, hs, di, true, s, px ? u16(xp_) : nullptr);
+        }
     }
     K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);
     project(logits_, hl_, out_embed_, out_embed_p_, int(B), int(cfg_.voc), hs, false, s);

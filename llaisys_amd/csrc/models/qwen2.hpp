@@ -120,7 +120,7 @@ private:
     tensor_t x_, h_, qkv_, q_, attn_, gu_, act_, hl_, logits_, next_;
     // x and the attention output in MFMA operand order (packedRowIndex), for
     // the packed-operand qkv and o projections of decode steps.
-    tensor_t xp_, ap_;
+    tensor_t xp_, ap_, actp_; // actp_: the SwiGLU output, for the packed-X down projection
     tensor_t dev_i32_, dev_i64_;     // per-step indices, uploaded in one copy each
     core::storage_t host32_, host64_; // pinned staging of the same
     tensor_t table_, ctx_before_, ctx_after_, cu_, cow_, tok_, last_; // views of dev_i32_/dev_i64_
@@ -156,6 +156,10 @@ private:
     // the QKV projection's epilogue, and the attention reads q
     // (LLAISYS_QKV_GEMM_EPILOGUE=0: in the attention kernel instead).
     bool qkv_gemm_epilogue_ = true;
+    // On that path the down projection's split-K reads the SwiGLU output
+    // packed, streamed through registers (fewer splits than the LDS-staged
+    // split-K); LLAISYS_SPLITK_PACKED=0 keeps the LDS-staged kernel.
+    bool splitk_packed_ = true;
     void chooseDecodeAttention(size_t B, int32_t min_ctx, int32_t max_ctx);
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
     std::map<size_t, DecodeGraph> graphs_;       // one step (step())
