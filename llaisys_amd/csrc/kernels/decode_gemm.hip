@@ -55,6 +55,8 @@ struct GemmArgs {
     const u32x4 *wp;     // packed W
     int M, N, K, nblocks, accumulate;
     int mgroups; // workgroups per row block, each on its own 16 MB rows of X and Y
+    uint64_t *keys; // non-null (mgroups == 1): argmax key of each row over the workgroup's columns,
+                    // keys[m * gridDim.x + blockIdx.x]
 };
 
 __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
@@ -118,6 +120,16 @@ decodeGemmKernel(GemmArgs a) {
     for (int j = 0; j < KS; ++j) ring[j] = __builtin_nontemporal_load(wbase + (size_t(first) * KT + ktile(j)) * 64);
 
     constexpr int kOut = (MB + kWaves - 1) / kWaves; // m blocks this wave finalises (mb = wave + kWaves i)
+    // Running maximum of the rounded outputs and its column, per m block
+    // (a.keys): a lane's columns only grow, so a strict > keeps the first
+    // maximum, and a NaN beats any number (torch's argmax).
+    float best_v[kOut];
+    int best_c[kOut];
+#pragma unroll
+    for (int i = 0; i < kOut; ++i) {
+        best_v[i] = -INFINITY;
+        best_c[i] = -1;
+    }
     int it = 0;
     for (int nb = first; nb < a.nblocks; nb += stride, ++it) {
         const int nxt = nb + stride < a.nblocks ? nb + stride : nb; // past the end: re-read (L2 hit)
@@ -167,7 +179,30 @@ decodeGemmKernel(GemmArgs a) {
                 const uint32_t w1 = uint32_t(__builtin_bit_cast(uint16_t, e2)) |
                                     (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
                 *reinterpret_cast<uint2 *>(a.y + size_t(m) * a.N + n0) = make_uint2(w0, w1);
+                if (a.keys) {
+                    const float ev[4] = {float(e0), float(e1), float(e2), float(e3)};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const bool take = ev[q] != ev[q] ? best_v[i] == best_v[i] : ev[q] > best_v[i];
+                        best_v[i] = take ? ev[q] : best_v[i];
+                        best_c[i] = take ? n0 + q : best_c[i];
+                    }
+                }
             }
+        }
+    }
+    if (a.keys) {
+        // Lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same row m.
+#pragma unroll
+        for (int i = 0; i < kOut; ++i) {
+            uint64_t k = best_c[i] < 0 ? 0 : argmaxKey(best_v[i], best_c[i]);
+            uint64_t o = __shfl_xor(k, 16);
+            k = o > k ? o : k;
+            o = __shfl_xor(k, 32);
+            k = o > k ? o : k;
+            const int mb = wave + kWaves * i;
+            const int m = 16 * mblock(mb) + (lane & 15);
+            if (mb < MB && lane < 16 && m < a.M) a.keys[size_t(m) * gridDim.x + blockIdx.x] = k;
         }
     }
 }
@@ -972,13 +1007,16 @@ void packWeightGateUp(uint16_t *packed, const uint16_t *w, int di, int K, void *
 }
 
 void decodeGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
-                void *stream) {
+                void *stream, uint64_t *argmax_keys) {
     LLAISYS_CHECK(decodeGemmSupported(M, N, K),
                   "decodeGemm: unsupported shape M=" << M << " N=" << N << " K=" << K);
-    GemmArgs a{y, x, reinterpret_cast<const u32x4 *>(packed), M, N, K, N / 16, accumulate ? 1 : 0, 1};
+    LLAISYS_CHECK(!argmax_keys || M <= 64 || N >= kSplitMaxN, "decodeGemm: argmax keys need one workgroup per row set");
+    GemmArgs a{y, x, reinterpret_cast<const u32x4 *>(packed), M, N, K, N / 16, accumulate ? 1 : 0, 1, argmax_keys};
     launchByM(a, static_cast<hipStream_t>(stream));
     HIP_CHECK(hipGetLastError());
 }
+
+int decodeGemmKeyChunks(int N) { return std::max(1, std::min(N / 16, computeUnitsOf())); }
 
 bool splitKGemmSupported(int M, int N, int K) {
     return M >= 1 && M <= kDecodeGemmMaxM && N >= kSplitTileRows && N % kSplitTileRows == 0 && K % 32 == 0 &&

@@ -134,6 +134,8 @@ void embedding(void *out, const int64_t *idx, const void *weight, ElemType t, si
 // Row-wise argmax over the last dim: idx[rows] (first maximum; NaN counts as
 // the largest value), val[rows] (may be null); workspace of argmaxWorkspaceBytes().
 size_t argmaxWorkspaceBytes(size_t rows, int64_t n);
+// idx[r] = the column of the maximum of keys[r * chunks .. + chunks) (argmaxKey).
+void argmaxFinishKeys(int64_t *idx, const uint64_t *keys, size_t rows, int chunks, void *stream);
 void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, int64_t n, void *workspace,
             void *stream);
 void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *shape, const int64_t *out_strides,
@@ -160,7 +162,12 @@ void packWeight(uint16_t *packed, const uint16_t *w, const uint16_t *fold_g, int
 // 16b + e and up columns at 16b + 8 + e (swigluRows' interleaved layout).
 void packWeightGateUp(uint16_t *packed, const uint16_t *w, int di, int K, void *stream);
 void decodeGemm(uint16_t *y, const uint16_t *x, const uint16_t *packed, int M, int N, int K, bool accumulate,
-                void *stream);
+                void *stream, uint64_t *argmax_keys = nullptr);
+// argmax_keys (M <= 64 or N >= 8192): each workgroup also leaves, per row,
+// the argmax key of the bf16 values it stored (argmaxKey), at
+// argmax_keys[m * decodeGemmKeyChunks(N) + workgroup]; argmaxFinishKeys
+// turns them into the rows' first maximum.
+int decodeGemmKeyChunks(int N);
 // The same product for long K (kDecodeGemmK < K <= kSplitKMaxK, K % 32 == 0,
 // N % 128 == 0, M <= kDecodeGemmMaxM), same packed W: K splits over
 // workgroups into fp32 partials (splitKWorkspaceBytes of device memory),

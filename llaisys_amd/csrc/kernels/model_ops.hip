@@ -3,6 +3,7 @@
 // swiglu}.py), for the Qwen2 decode step built on the paged KV path. All math
 // is fp32; results are rounded once to the tensor dtype.
 #include "launch.hpp"
+#include "step_common.hpp"
 
 #include "../device/hip_check.hpp"
 
@@ -156,12 +157,6 @@ __global__ void embeddingKernel(T *out, const int64_t *idx, const T *weight, int
 // largest value at its first column.
 constexpr int kArgmaxChunk = 4096;
 
-__device__ __forceinline__ uint64_t argmaxKey(float v, int64_t col) {
-    uint32_t u = __float_as_uint(v);
-    if (v != v) u = 0x7fc00000u; // any NaN: the canonical positive NaN
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return (uint64_t(ord) << 32) | uint32_t(~uint32_t(col));
-}
 
 __device__ __forceinline__ uint64_t waveMax(uint64_t k) {
 #pragma unroll
@@ -341,6 +336,13 @@ void embedding(void *out, const int64_t *idx, const void *weight, ElemType t, si
     byType<EmbL>(t, out, idx, weight, rows, vocab, d, err, static_cast<hipStream_t>(stream));
     HIP_CHECK(hipGetLastError());
 }
+void argmaxFinishKeys(int64_t *idx, const uint64_t *keys, size_t rows, int chunks, void *stream) {
+    if (!rows) return;
+    hipLaunchKernelGGL(argmaxFinishKernel<__hip_bfloat16>, dim3(unsigned(rows)), dim3(64), 0,
+                       static_cast<hipStream_t>(stream), idx, nullptr, keys, nullptr, int64_t(0), chunks);
+    HIP_CHECK(hipGetLastError());
+}
+
 size_t argmaxWorkspaceBytes(size_t rows, int64_t n) {
     return rows * size_t((n + kArgmaxChunk - 1) / kArgmaxChunk) * sizeof(uint64_t);
 }

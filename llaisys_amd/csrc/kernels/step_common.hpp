@@ -60,4 +60,14 @@ struct RowChunks {
     }
 };
 
+// Row-wise argmax key: order-preserving bits of the value (NaN above +inf,
+// as torch.max propagates NaN) << 32 | ~column, so the maximum key is the
+// largest value at its first column.
+__device__ __forceinline__ uint64_t argmaxKey(float v, int64_t col) {
+    uint32_t u = __float_as_uint(v);
+    if (v != v) u = 0x7fc00000u; // any NaN: the canonical positive NaN
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (uint64_t(ord) << 32) | uint32_t(~uint32_t(col));
+}
+
 } // namespace llaisys::kernels

@@ -586,9 +586,19 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
         }
     }
     K::rmsNormRows(u16(hl_), u16(x_), i64(last_), u16(out_norm_), B, hs, cfg_.epsilon, s);
-    project(logits_, hl_, out_embed_, out_embed_p_, int(B), int(cfg_.voc), hs, false, s);
-    K::argmax(i64(next_), nullptr, logits_->data(), et, B, int64_t(cfg_.voc),
-              rt.scratch(K::argmaxWorkspaceBytes(B, int64_t(cfg_.voc))), s);
+    const int voc = int(cfg_.voc);
+    if (takesDecodeGemm(out_embed_p_, int(B), voc, hs) && (B <= 64 || voc >= 8192)) {
+        // The LM head's workgroups leave each row's argmax over their columns
+        // (no second pass over the logits).
+        const int chunks = K::decodeGemmKeyChunks(voc);
+        auto *keys = static_cast<uint64_t *>(rt.scratch(B * size_t(chunks) * sizeof(uint64_t)));
+        K::decodeGemm(u16(logits_), u16(hl_), u16(out_embed_p_), int(B), voc, hs, false, s, keys);
+        K::argmaxFinishKeys(i64(next_), keys, B, chunks, s);
+    } else {
+        project(logits_, hl_, out_embed_, out_embed_p_, int(B), voc, hs, false, s);
+        K::argmax(i64(next_), nullptr, logits_->data(), et, B, int64_t(cfg_.voc),
+                  rt.scratch(K::argmaxWorkspaceBytes(B, int64_t(cfg_.voc))), s);
+    }
 }
 
 // Largest M at which the decode GEMM beats the library GEMM for a weight of
