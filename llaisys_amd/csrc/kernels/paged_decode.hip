@@ -482,14 +482,17 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
 // work of qkvRopeAppend for one decode token): each wave forms the G query
 // heads in its own MFMA operand registers from the projection row (scaled by
 // the row's 1/rms when the RMSNorm is folded into the weights, plus bias,
-// rotated by position ctx - 1). Wave 0, which holds the fewest pairs, also
-// forms the new k and v before starting its pages, stores them into their
-// page slot for later steps and leaves them in LDS; the last wave, which
-// holds the unit's last pair, consumes that pair after a barrier at the end
-// of the loop with the new token patched into its registers, so no load
-// waits for the stores. The other waves start their first pages before the
-// epilogue's arithmetic.
-constexpr int kUnitWaves = 4;
+// rotated by position ctx - 1). The wave that holds the unit's last pair
+// forms the new k and v after its loop, patches them into that pair's
+// registers, consumes it and only then stores them into their page slot for
+// later steps. The waves start their first pages before the epilogue's
+// arithmetic.
+//
+// Two waves per unit (one workgroup per CU at 128 sequences x 2 kv heads, two
+// pairs in flight per wave): 45.5 us per layer in the config-5 step, against
+// 48.6 us with 4 waves, 47.0 with 1, 46.5 with 2 waves and 3 pairs in flight
+// (8 waves had measured slower than 4 earlier).
+constexpr int kUnitWaves = 2;
 constexpr int kRopeMaxGroup = 16; // query heads per kv head in the fused epilogue: one MFMA column each
 
 // The new token (slot tok of the last page) written into a loaded page pair's
@@ -966,9 +969,7 @@ void launchDecodeUnits(void *out, bool out_f32, const uint16_t *q, const uint16_
     a.max_pages = max_pages;
     a.num_blocks = num_blocks;
     a.scale_log2 = scale * 1.4426950408889634f;
-    // Two page pairs in flight per wave, two waves per SIMD: measured best
-    // in the config-5 step (3.37 ms; three in flight at one wave per SIMD:
-    // 3.47 ms; 8 waves per unit: 3.46 ms).
+    // Two page pairs in flight per wave (see kUnitWaves for the measurements).
     auto s = static_cast<hipStream_t>(stream);
     const dim3 grid(unsigned(B) * unsigned(nkvh)), block(64 * kUnitWaves);
     if (rope) {
