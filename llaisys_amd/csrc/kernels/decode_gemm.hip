@@ -689,7 +689,7 @@ __global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const 
 // owns m blocks 2w, 2w + 1 adds the four k partials in wave order, scales by
 // r, pairs each gate value with its up value (lane l and l ^ 32 hold the
 // same columns) and stores act.
-constexpr int kGuRing = 3; // (4: 20.6 us, 6: spills; 3: 20.4 us in the config-5 step)
+constexpr int kGuRing = 2; // (config-5 step: 2: 18.9 us, 3: 19.3, 4: 20.6, 6: spills)
 constexpr int kGuRows = 8; // 16-row m blocks (M <= 128)
 
 template <int NB>
@@ -803,7 +803,7 @@ int gateUpBlocksPerGroup(int di) {
 // k partials meet in LDS; the wave that owns m blocks 2w, 2w + 1 adds them in
 // wave order and stores part[s][m][n] (m < M).
 constexpr int kSkBlocks = 4;
-constexpr int kSkRing = 3; // (4: 12.36 us against 12.26)
+constexpr int kSkRing = 2; // (config-5 step: 2: 11.95 us, 3: 12.04, 4: 12.36)
 
 template <int KSW>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
