@@ -22,7 +22,15 @@
 //    barrier wave w sums the four partials of m blocks w, w + 4 and writes
 //    bf16 rows (+ the old Y when accumulating, before the one rounding; a
 //    bias enters the same way, preset as the rows of Y).
-// Double-buffered partials make that the only barrier per block.
+// Double-buffered partials make that the only barrier per block. Given
+// argmax_keys, the epilogue also keeps each row's maximum (the LM head).
+//
+// Further down, the kernels of the batched decode step whose X comes packed
+// in the same operand order (packedRowIndex; its producers write that copy):
+// packedXGemm (32 x 32 tiles, qkv and o), qkvRopeGemm (qkv with the QKV
+// epilogue), gateUpSwiglu (gate-up, row 1/rms and SwiGLU over interleaved
+// gate/up weights) and splitKPackedGemm (the down projection); and the
+// LDS-staged split-K GEMM for long K with row-major X.
 #include "launch.hpp"
 #include "step_common.hpp"
 
