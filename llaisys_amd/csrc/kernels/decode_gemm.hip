@@ -956,6 +956,7 @@ void gateUpSwiglu(uint16_t *act, const uint16_t *x_packed, const uint16_t *w_pac
                   void *stream, bool act_packed) {
     LLAISYS_CHECK(gateUpSwigluSupported(M, di, K), "gateUpSwiglu: unsupported shape M=" << M << " di=" << di
                                                                                         << " K=" << K);
+    LLAISYS_CHECK(!act_packed || di % 32 == 0, "gateUpSwiglu: a packed output needs di % 32 == 0, got " << di);
     const int nb = gateUpBlocksPerGroup(di);
     const dim3 grid(unsigned(2 * di / 16 / nb));
     auto st = static_cast<hipStream_t>(stream);
