@@ -490,8 +490,9 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
 //
 // Two waves per unit (one workgroup per CU at 128 sequences x 2 kv heads, two
 // pairs in flight per wave): 45.5 us per layer in the config-5 step, against
-// 48.6 us with 4 waves, 47.0 with 1, 46.5 with 2 waves and 3 pairs in flight
-// (8 waves had measured slower than 4 earlier).
+// 48.6 us with 4 waves, 47.0 with 1, 46.5 with 2 waves and 3 pairs in flight,
+// 46.1 without the 256-register cap (8 waves had measured slower than 4
+// earlier).
 constexpr int kUnitWaves = 2;
 constexpr int kRopeMaxGroup = 16; // query heads per kv head in the fused epilogue: one MFMA column each
 
