@@ -421,6 +421,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 // Y[m, n .. n + 3] = (old Y +) sum over s of part[s][m][n .. n + 3], rounded
 // once. Loads of 16 partials are in flight at a time; the sum runs in split
 // order.
+// (With 10 splits a batch of exactly 10 measured slower, 5.03 against 4.91
+// us: the re-reads past S are L2 hits.)
 constexpr int kReduceBatch = 16;
 
 __global__ void splitKReduceKernel(uint16_t *y, const float *part, int M, int N, int S, int accumulate,
