@@ -812,7 +812,7 @@ int gateUpBlocksPerGroup(int di) {
 // k range: fewer splits, so fewer fp32 partials to write and sum. The four
 // k partials meet in LDS; the wave that owns m blocks 2w, 2w + 1 adds them in
 // wave order and stores part[s][m][n] (m < M).
-constexpr int kSkBlocks = 4;
+constexpr int kSkBlocks = 4; // (config-5 down: 4 x 10 splits 11.95 us; 6 x 14: 12.75; 3 x 7: 12.84)
 constexpr int kSkRing = 2; // (config-5 step: 2: 11.95 us, 3: 12.04, 4: 12.36)
 
 template <int KSW>
