@@ -38,6 +38,14 @@ COMMON = [
 ]
 
 
+# Per-source extra flags. gemm.hip: keep MFMA accumulators in VGPRs (the
+# AGPR form of the gfx950 16x16x32 MFMAs makes the register allocator rotate
+# the loop-carried accumulators through v_accvgpr copies every k step).
+EXTRA = {
+    "kernels/gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _sources() -> list[Path]:
     return sorted(p for p in CSRC.rglob("*") if p.suffix in (".cpp", ".hip"))
 
@@ -45,7 +53,7 @@ def _sources() -> list[Path]:
 def _compile(src: Path) -> Path:
     rel = src.relative_to(CSRC)
     obj = OBJ / (str(rel).replace(os.sep, "__") + ".o")
-    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(rel.as_posix(), []), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,9 +71,7 @@ def build(verbose: bool = True) -> Path:
         objs = list(ex.map(_compile, srcs))
     LIB.parent.mkdir(exist_ok=True)
     tmp = LIB.with_suffix(".so.tmp")
-    rocm_lib = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), f"-L{rocm_lib}", "-lrocblas", "-lhipblaslt",
-           "-o", str(tmp)]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

@@ -1,0 +1,492 @@
+// Y[M, N] (+)= X[M, K] . W[N, K]^T (+ bias[N]) for any M, N, K: the
+// reference's linear (README.md:181-198, stub src/ops/linear/op.cpp:4-6) as a
+// hand-written MFMA GEMM for gfx950, in f32, f16 and bf16 with fp32
+// accumulation and one rounding of (old Y +) sum (+ bias) to the output type.
+//
+// Both operands are K-contiguous rows ("NT"), so one 16 B piece of a row is a
+// whole MFMA operand fragment per lane:
+//  * 16-bit types: v_mfma_f32_16x16x32_{bf16,f16}; lane l holds row l % 16,
+//    k 8 (l / 16) .. + 7 of a 32-k step.
+//  * f32: v_mfma_f32_16x16x4_f32 four times per 16 B piece; lane l holds row
+//    l % 16, k 4 (l / 16) .. + 3 of a 16-k step, and MFMA e takes element e
+//    of every lane (k 4 g + e, g = 0..3): the same k order on both operands,
+//    so the sum is over the same products.
+//
+// A workgroup of 4 waves (2 x 2) owns a BM x BN tile of Y; each wave a
+// (BM / 2) x (BN / 2) sub-tile. K advances in tiles of 128 B per row (64
+// 16-bit or 32 f32 elements): every thread loads its 16 B pieces of the next
+// k tile of X and W into registers by buffer loads (out-of-range rows and k
+// come back as zeros, so edge tiles need no other guard), the waves run the
+// current tile's MFMAs from LDS, then the registers go to the other LDS
+// buffer and one barrier closes the tile. In LDS a row is 8 pieces of 16 B,
+// piece c of row r kept at slot c ^ (r % 8): the 16 rows one fragment read
+// touches at one piece column land in 8 different bank groups.
+//
+// W is the MFMA's A operand and X its B operand, so a lane's accumulator
+// holds 4 consecutive columns n of one row m of Y: one 8 B (16-bit) or 16 B
+// (f32) store per lane and fragment.
+//
+// Workgroups go to the XCDs round-robin by id; the tile order puts each
+// XCD's workgroups on one contiguous run of tiles, walked m-fastest in groups
+// of kGroupN column tiles, so the workgroups resident on one XCD share both
+// their W columns and their X rows in that XCD's L2.
+#include "launch.hpp"
+
+#include "../common.hpp"
+#include "../device/hip_check.hpp"
+
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+namespace llaisys::kernels {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kXcds = 8;
+constexpr int kGroupN = 4;             // column tiles per m-fastest group
+constexpr int kRowBytes = 64;          // bytes of one row per k tile (one 32-k MFMA step of 16-bit data)
+constexpr int kStages = 4;             // k tiles in the LDS ring
+constexpr int kThreads = 256;
+constexpr uint32_t kRsrcWord3 = 0x00020000u; // raw buffer, 32-bit dwords (gfx9 family)
+constexpr uint32_t kMasked = 0x80000000u;    // an offset past any buffer: the load returns 0
+
+template <ElemType T> struct Elem;
+template <> struct Elem<ElemType::BF16> { using type = __bf16; static constexpr int size = 2; };
+template <> struct Elem<ElemType::F16> { using type = _Float16; static constexpr int size = 2; };
+template <> struct Elem<ElemType::F32> { using type = float; static constexpr int size = 4; };
+
+// acc += A . B for one 16 B piece per lane (one 32-k step for 16-bit types,
+// one 16-k step for f32).
+template <ElemType T> __device__ __forceinline__ f32x4 mfmaPiece(u32x4 a, u32x4 b, f32x4 acc) {
+    if constexpr (T == ElemType::BF16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       acc, 0, 0, 0);
+    } else if constexpr (T == ElemType::F16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), acc,
+                                                      0, 0, 0);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(b[e]), acc, 0, 0, 0);
+        return acc;
+    }
+}
+
+template <ElemType T> __device__ __forceinline__ float loadElem(const void *p, size_t i) {
+    using E = typename Elem<T>::type;
+    return float(static_cast<const E *>(p)[i]);
+}
+
+template <ElemType T> __device__ __forceinline__ void storeElem(void *p, size_t i, float v) {
+    using E = typename Elem<T>::type;
+    static_cast<E *>(p)[i] = E(v);
+}
+
+// Four consecutive elements (one 8 B or 16 B access), widened to fp32.
+template <ElemType T> __device__ __forceinline__ f32x4 load4(const void *p, size_t i) {
+    if constexpr (T == ElemType::F32) {
+        return *reinterpret_cast<const f32x4 *>(static_cast<const float *>(p) + i);
+    } else {
+        using E = typename Elem<T>::type;
+        typedef E e4 __attribute__((ext_vector_type(4)));
+        const e4 v = *reinterpret_cast<const e4 *>(static_cast<const E *>(p) + i);
+        return f32x4{float(v[0]), float(v[1]), float(v[2]), float(v[3])};
+    }
+}
+
+template <ElemType T> __device__ __forceinline__ void store4(void *p, size_t i, f32x4 v) {
+    if constexpr (T == ElemType::F32) {
+        *reinterpret_cast<f32x4 *>(static_cast<float *>(p) + i) = v;
+    } else {
+        using E = typename Elem<T>::type;
+        typedef E e4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<e4 *>(static_cast<E *>(p) + i) = e4{E(v[0]), E(v[1]), E(v[2]), E(v[3])};
+    }
+}
+
+struct GemmParams {
+    void *y;
+    const void *x, *w, *bias;
+    int M, N, K;
+    int accumulate;
+    int mtiles, ntiles;
+    uint32_t x_bytes, w_bytes; // buffer extents (range checks)
+    int splits;                // > 1: K split over workgroups, fp32 partials part[split][M][N]
+    float *part;
+};
+
+// Tile index of workgroup b: XCD b % 8 takes tiles [(b % 8) T / 8, ...) in
+// order b / 8 (T = tiles; when T % 8 != 0 the plain order is kept).
+__device__ __forceinline__ void tileOf(const GemmParams &p, int b, int &mt, int &nt) {
+    const int tiles = p.mtiles * p.ntiles;
+    int t = b;
+    if (tiles % kXcds == 0) t = (t % kXcds) * (tiles / kXcds) + t / kXcds;
+    // m-fastest within groups of kGroupN column tiles
+    const int per_group = kGroupN * p.mtiles;
+    const int g = t / per_group, r = t % per_group;
+    const int gn = min(kGroupN, p.ntiles - g * kGroupN);
+    mt = r / gn;
+    nt = g * kGroupN + r % gn;
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One k tile of an operand is ROWS rows x 64 B (4 pieces of 16 B), kept in
+// LDS as blocks of 16 rows x 64 B: one 64-lane global_load_lds instruction
+// fills one block, lane i writing bytes 16 i .. 16 i + 15 of it (row i / 4,
+// slot i % 4). Piece c of row r sits at slot c ^ ((r / 4) % 4), so the 16
+// rows of an MFMA fragment read at one piece column fall on 16 different
+// 4-bank groups. Lane i therefore fetches piece (i % 4) ^ ((i / 16) % 4).
+__device__ __forceinline__ int slotOf(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+template <ElemType T, int BM, int BN>
+__global__ void __launch_bounds__(kThreads) gemmKernel(GemmParams p) {
+    constexpr int ES = Elem<T>::size;
+    constexpr int KT = kRowBytes / ES;              // elements per k tile
+    constexpr int TM = BM / 32, TN = BN / 32;       // 16-row fragments per wave
+    constexpr int XB = BM / 16, WB = BN / 16;       // 1 KiB blocks per operand per k tile
+    constexpr int XW = XB / 4, WW = WB / 4;         // ... issued by each wave
+    constexpr int STAGE = (BM + BN) * kRowBytes / 16; // u32x4 per stage
+    constexpr int kLoadsPerStage = XW + WW;          // per wave
+    static_assert(XB % 4 == 0 && WB % 4 == 0, "each wave issues whole blocks");
+    extern __shared__ u32x4 lds[];                   // [kStages][X blocks | W blocks]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    // Workgroup b: split b / tiles over k tiles [s nk / S, (s + 1) nk / S)
+    // of tile b % tiles.
+    const int tiles = p.mtiles * p.ntiles;
+    const int split = int(blockIdx.x) / tiles;
+    int mt, nt;
+    tileOf(p, int(blockIdx.x) % tiles, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.x), (short)0, int(p.x_bytes), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.w), (short)0, int(p.w_bytes), kRsrcWord3);
+    const uint32_t row_bytes = uint32_t(p.K) * ES;
+
+    // Lane's piece of a block: row lr = lane / 4 of the block, global piece lc.
+    const int lr = lane >> 2, lc = (lane & 3) ^ ((lane >> 4) & 3);
+    // Block b of the wave is block wave + 4 b of the operand (rows 16 (wave + 4 b) ..).
+    const uint32_t xbase = uint32_t(m0 + 16 * wave + lr) * row_bytes + 16 * lc;
+    const uint32_t wbase = uint32_t(n0 + 16 * wave + lr) * row_bytes + 16 * lc;
+    const uint32_t bstride = 64u * row_bytes; // 4 blocks of 16 rows
+    const int nk_all = (p.K + KT - 1) / KT;
+    const int kt0 = split * nk_all / p.splits;
+    const int nk = (split + 1) * nk_all / p.splits - kt0;
+    auto issue = [&](int kt) {
+        u32x4 *st = lds + (kt % kStages) * STAGE;
+        const uint32_t kb = uint32_t(kt0 + kt) * kRowBytes;
+        const bool in_k = kt < nk && kb + 16 * lc < row_bytes;
+#pragma unroll
+        for (int b = 0; b < XW; ++b)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *)(st + (wave + 4 * b) * 64), 16,
+                                                     int(in_k ? xbase + kb + b * bstride : kMasked), 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < WW; ++b)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void *)(st + (XB + wave + 4 * b) * 64), 16,
+                                                     int(in_k ? wbase + kb + b * bstride : kMasked), 0, 0, 0);
+    };
+
+    f32x4 acc[TN][TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s) issue(s);
+    // Fragment reads: lane reads row l % 16 of a 16-row block, piece l / 16.
+    const int fr = lane & 15, fslot = slotOf(fr, lane >> 4);
+    const int xblk0 = wm * (BM / 32), wblk0 = XB + wn * (BN / 32);
+    for (int kt = 0; kt < nk; ++kt) {
+        // Stage kt has landed once at most kStages - 2 stages of this wave's
+        // loads are still in flight; the barrier then covers every wave's.
+        // (The compiler does not count global_load_lds against LDS reads.)
+        static_assert(kStages == 4, "the wait count below assumes 2 stages in flight");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * kLoadsPerStage) : "memory");
+        // Slot (kt - 1) % kStages was read by every wave before this barrier.
+        issue(kt + kStages - 1);
+        const u32x4 *st = lds + (kt % kStages) * STAGE;
+        u32x4 a[TN], b[TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i) a[i] = st[(wblk0 + i) * 64 + fr * 4 + fslot];
+#pragma unroll
+        for (int j = 0; j < TM; ++j) b[j] = st[(xblk0 + j) * 64 + fr * 4 + fslot];
+        if constexpr (T == ElemType::F32) {
+            // element e of every piece, all tiles, then e + 1: dependent
+            // MFMAs on one accumulator are TN x TM instructions apart
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[i][e]),
+                                                                         __uint_as_float(b[j][e]), acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) acc[i][j] = mfmaPiece<T>(a[i], b[j], acc[i][j]);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the trailing (zero) stages
+
+    // Epilogue: lane holds Y[m][n .. n + 3], m = row l % 16 of X fragment j,
+    // n = 4 (l / 16) of W fragment i; (old Y +) sum (+ bias), rounded once;
+    // or, split, the fp32 partial for the reduce.
+    const int fg = lane >> 4;
+    const bool vec = (p.N & 3) == 0;
+    if (p.splits > 1) {
+        float *part = p.part + size_t(split) * p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < TM; ++j) {
+            const int m = m0 + wm * (BM / 2) + 16 * j + fr;
+            if (m >= p.M) continue;
+#pragma unroll
+            for (int i = 0; i < TN; ++i) {
+                const int n = n0 + wn * (BN / 2) + 16 * i + 4 * fg;
+                if (n >= p.N) continue;
+                const size_t base = size_t(m) * p.N + n;
+                if (vec) {
+                    *reinterpret_cast<f32x4 *>(part + base) = acc[i][j];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < p.N) part[base + r] = acc[i][j][r];
+                }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int m = m0 + wm * (BM / 2) + 16 * j + fr;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+            const int n = n0 + wn * (BN / 2) + 16 * i + 4 * fg;
+            if (n >= p.N) continue;
+            const size_t base = size_t(m) * p.N + n;
+            f32x4 v = acc[i][j];
+            if (vec) {
+                if (p.accumulate) v = load4<T>(p.y, base) + v;
+                if (p.bias) v += load4<T>(p.bias, n);
+                store4<T>(p.y, base, v);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (n + r >= p.N) break;
+                    float e = v[r];
+                    if (p.accumulate) e = loadElem<T>(p.y, base + r) + e;
+                    if (p.bias) e += loadElem<T>(p.bias, n + r);
+                    storeElem<T>(p.y, base + r, e);
+                }
+            }
+        }
+    }
+}
+
+// Shapes whose rows are not whole 16 B pieces (K * element size % 16 != 0,
+// e.g. the reference test's K = 4): one thread per output, fp32 sum in k
+// order, the same epilogue.
+template <ElemType T>
+__global__ void __launch_bounds__(256) gemmRowsKernel(void *y, const void *x, const void *w, const void *bias, int M,
+                                                      int N, int K, int accumulate) {
+    const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= size_t(M) * N) return;
+    const int m = int(idx / N), n = int(idx % N);
+    float sum = 0.f;
+    for (int k = 0; k < K; ++k) sum = fmaf(loadElem<T>(x, size_t(m) * K + k), loadElem<T>(w, size_t(n) * K + k), sum);
+    if (accumulate) sum = loadElem<T>(y, idx) + sum;
+    if (bias) sum += loadElem<T>(bias, n);
+    storeElem<T>(y, idx, sum);
+}
+
+// Y[m, n] = (old Y +) sum over s of part[s][m][n] (+ bias[n]), in split
+// order, rounded once; one thread per 4 columns (N % 4 == 0) or per element.
+template <ElemType T>
+__global__ void __launch_bounds__(256) gemmReduceKernel(void *y, const float *part, const void *bias, int M, int N,
+                                                        int S, int accumulate) {
+    const size_t idx = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t stride = size_t(M) * N;
+    if ((N & 3) == 0) {
+        if (idx >= stride / 4) return;
+        const size_t base = 4 * idx;
+        f32x4 v = *reinterpret_cast<const f32x4 *>(part + base);
+        for (int s = 1; s < S; ++s) v += *reinterpret_cast<const f32x4 *>(part + s * stride + base);
+        if (accumulate) v = load4<T>(y, base) + v;
+        if (bias) v += load4<T>(bias, base % N);
+        store4<T>(y, base, v);
+    } else {
+        if (idx >= stride) return;
+        float v = part[idx];
+        for (int s = 1; s < S; ++s) v += part[s * stride + idx];
+        if (accumulate) v = loadElem<T>(y, idx) + v;
+        if (bias) v += loadElem<T>(bias, idx % N);
+        storeElem<T>(y, idx, v);
+    }
+}
+
+int cusOf() {
+    static std::mutex mu;
+    static std::vector<int> cache;
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    if (size_t(dev) >= cache.size()) cache.resize(dev + 1, 0);
+    if (!cache[dev]) HIP_CHECK(hipDeviceGetAttribute(&cache[dev], hipDeviceAttributeMultiprocessorCount, dev));
+    return cache[dev];
+}
+
+template <ElemType T, int BM, int BN> void launchTile(GemmParams p, hipStream_t s) {
+    const size_t lds = size_t(kStages) * (BM + BN) * kRowBytes;
+    static bool attr = [] {
+        HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(kStages * (BM + BN) * kRowBytes)));
+        return true;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL((gemmKernel<T, BM, BN>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)), dim3(kThreads), lds, s,
+                       p);
+}
+
+// The tile with the least estimated time: rounds of workgroups over the CUs
+// (workgroups per CU from the LDS ring) times a tile's MFMA work over its
+// relative efficiency (bigger wave tiles read less LDS per MFMA). A grid
+// that still leaves CUs idle splits K (at least kMinSplitTiles k tiles per
+// split) into fp32 partials that a second kernel sums in split order.
+struct Plan {
+    int tile = 0; // index into kTiles
+    int mtiles = 0, ntiles = 0, splits = 1;
+};
+struct TileShape { int bm, bn, per_cu; double eff; };
+constexpr TileShape kTiles[] = {{128, 256, 1, 1.0}, {256, 128, 1, 1.0}, {128, 128, 2, 0.8}, {64, 64, 4, 0.45}};
+constexpr int kMinSplitTiles = 8;
+
+Plan planGemm(ElemType t, int M, int N, int K) {
+    const long cus = cusOf();
+    Plan best;
+    double best_t = 1e300;
+    for (int i = 0; i < 4; ++i) {
+        const TileShape &c = kTiles[i];
+        const long tiles = long((M + c.bm - 1) / c.bm) * long((N + c.bn - 1) / c.bn);
+        const long rounds = (tiles + cus * c.per_cu - 1) / (cus * c.per_cu);
+        const double tm = double(rounds) * c.per_cu * c.bm * c.bn / c.eff;
+        if (tm < best_t) {
+            best_t = tm;
+            best.tile = i;
+            best.mtiles = (M + c.bm - 1) / c.bm;
+            best.ntiles = (N + c.bn - 1) / c.bn;
+        }
+    }
+    const long tiles = long(best.mtiles) * best.ntiles;
+    const int nk = (K * (t == ElemType::F32 ? 4 : 2) + kRowBytes - 1) / kRowBytes;
+    if (tiles < cus) best.splits = int(std::max(1L, std::min(cus / tiles, long(nk / kMinSplitTiles))));
+    return best;
+}
+
+template <ElemType T> void launchGemm(GemmParams p, const Plan &plan, hipStream_t s) {
+    p.mtiles = plan.mtiles;
+    p.ntiles = plan.ntiles;
+    p.splits = plan.splits;
+    switch (plan.tile) {
+    case 0: launchTile<T, 128, 256>(p, s); break;
+    case 1: launchTile<T, 256, 128>(p, s); break;
+    case 2: launchTile<T, 128, 128>(p, s); break;
+    default: launchTile<T, 64, 64>(p, s); break;
+    }
+    HIP_CHECK(hipGetLastError());
+    if (plan.splits > 1) {
+        const size_t n = (p.N & 3) == 0 ? size_t(p.M) * p.N / 4 : size_t(p.M) * p.N;
+        hipLaunchKernelGGL(gemmReduceKernel<T>, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, p.y, p.part, p.bias,
+                           p.M, p.N, plan.splits, p.accumulate);
+        HIP_CHECK(hipGetLastError());
+    }
+}
+
+// Rows of X per launch so that one launch's X stays inside a buffer's
+// 32-bit range. (A tile overhangs the last row by < 256 rows: with rows
+// under 8 MiB the byte offsets stay below 2^32.)
+constexpr size_t kMaxBufferBytes = size_t(1) << 31;
+constexpr size_t kMaxRowBytes = size_t(1) << 23;
+
+bool tiled(ElemType t, int K) { return K > 0 && (size_t(K) * (t == ElemType::F32 ? 4 : 2)) % 16 == 0; }
+
+int rowsPerLaunch(ElemType t, int M, int K) {
+    const size_t row_bytes = size_t(K) * (t == ElemType::F32 ? 4 : 2);
+    return int(std::min<size_t>(size_t(M), (kMaxBufferBytes - 1) / row_bytes));
+}
+
+} // namespace
+
+size_t linearWorkspaceBytes(ElemType t, int M, int N, int K) {
+    if (M <= 0 || N <= 0 || !tiled(t, K)) return 0;
+    const Plan plan = planGemm(t, rowsPerLaunch(t, M, K), N, K);
+    return plan.splits > 1 ? size_t(plan.splits) * rowsPerLaunch(t, M, K) * N * sizeof(float) : 0;
+}
+
+void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream,
+            bool accumulate, void *workspace) {
+    if (M <= 0 || N <= 0) return;
+    auto s = static_cast<hipStream_t>(stream);
+    if (!tiled(t, K)) {
+        const size_t n = size_t(M) * N;
+        const dim3 grid(unsigned((n + 255) / 256));
+        const int acc = accumulate ? 1 : 0, k = std::max(K, 0);
+        switch (t) {
+        case ElemType::BF16:
+            hipLaunchKernelGGL(gemmRowsKernel<ElemType::BF16>, grid, dim3(256), 0, s, y, x, w, bias, M, N, k, acc);
+            break;
+        case ElemType::F16:
+            hipLaunchKernelGGL(gemmRowsKernel<ElemType::F16>, grid, dim3(256), 0, s, y, x, w, bias, M, N, k, acc);
+            break;
+        case ElemType::F32:
+            hipLaunchKernelGGL(gemmRowsKernel<ElemType::F32>, grid, dim3(256), 0, s, y, x, w, bias, M, N, k, acc);
+            break;
+        }
+        HIP_CHECK(hipGetLastError());
+        return;
+    }
+    const size_t es = t == ElemType::F32 ? 4 : 2;
+    const size_t row_bytes = size_t(K) * es;
+    LLAISYS_CHECK(size_t(N) * row_bytes < kMaxBufferBytes && row_bytes < kMaxRowBytes,
+                  "linear: the weight (" << N << " x " << K << ") must be under 2 GiB, its rows under 8 MiB");
+    const int rows_per_launch = rowsPerLaunch(t, M, K);
+    for (int r0 = 0; r0 < M; r0 += rows_per_launch) {
+        const int m = std::min(rows_per_launch, M - r0);
+        const Plan plan = planGemm(t, m, N, K);
+        LLAISYS_CHECK(plan.splits == 1 || workspace, "linear: this shape needs linearWorkspaceBytes() of workspace");
+        GemmParams p{};
+        p.y = static_cast<char *>(y) + size_t(r0) * N * es;
+        p.x = static_cast<const char *>(x) + size_t(r0) * row_bytes;
+        p.w = w;
+        p.bias = bias;
+        p.M = m;
+        p.N = N;
+        p.K = K;
+        p.accumulate = accumulate ? 1 : 0;
+        p.x_bytes = uint32_t(size_t(m) * row_bytes);
+        p.w_bytes = uint32_t(size_t(N) * row_bytes);
+        p.part = static_cast<float *>(workspace);
+        switch (t) {
+        case ElemType::BF16: launchGemm<ElemType::BF16>(p, plan, s); break;
+        case ElemType::F16: launchGemm<ElemType::F16>(p, plan, s); break;
+        case ElemType::F32: launchGemm<ElemType::F32>(p, plan, s); break;
+        }
+    }
+}
+
+} // namespace llaisys::kernels

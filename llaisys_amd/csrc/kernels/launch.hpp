@@ -140,10 +140,13 @@ void argmax(int64_t *idx, void *val, const void *vals, ElemType t, size_t rows, 
             void *stream);
 void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *shape, const int64_t *out_strides,
                const int64_t *in_strides, void *stream);
-// Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]), row-major, fp32 accumulation.
-// accumulate: Y += X . W^T instead (a residual add folded into the GEMM).
+// Y[M, N] = X[M, K] . W[N, K]^T (+ bias[N]), row-major, fp32 accumulation
+// (gemm.hip's MFMA GEMM). accumulate: Y += X . W^T (+ bias) instead (a
+// residual add folded into the GEMM). Shapes that leave CUs idle split K
+// into fp32 partials in `workspace` (linearWorkspaceBytes; 0 = none needed).
+size_t linearWorkspaceBytes(ElemType t, int M, int N, int K);
 void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream,
-            bool accumulate = false);
+            bool accumulate, void *workspace);
 
 // ---- decode-sized projections (decode_gemm.hip), bf16
 // Y[M, N] (+)= X[M, K] . W[N, K]^T for M <= kDecodeGemmMaxM, K == kDecodeGemmK,

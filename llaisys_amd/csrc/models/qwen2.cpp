@@ -46,11 +46,12 @@ int64_t *i64(const tensor_t &t) { return reinterpret_cast<int64_t *>(t->data());
 int32_t *i32(const tensor_t &t) { return reinterpret_cast<int32_t *>(t->data()); }
 tensor_t rows(const tensor_t &t, size_t n) { return t->slice(0, 0, n); }
 
-// Y[M, N] = X W^T (+ bias) (+ Y) through the library GEMM.
+// Y[M, N] = X W^T (+ bias) (+ Y) through the MFMA GEMM over row-major W.
 void gemm(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &bias, int M, int N, int K,
           bool accumulate, void *s) {
+    void *ws = core::context().runtime().scratch(K::linearWorkspaceBytes(K::ElemType::BF16, M, N, K));
     K::linear(y->data(), x->data(), w->data(), bias ? bias->data() : nullptr, K::ElemType::BF16, M, N, K, s,
-              accumulate);
+              accumulate, ws);
 }
 
 } // namespace

@@ -120,8 +120,10 @@ void linear(const tensor_t &out, const tensor_t &in, const tensor_t &weight, con
     if (onHost(op, {&out, &in, &weight, &bias}))
         return C::linear(out->data(), in->data(), weight->data(), bias ? bias->data() : nullptr, floatType(out, op),
                          int(M), int(N), int(Kd));
-    K::linear(out->data(), in->data(), weight->data(), bias ? bias->data() : nullptr, floatType(out, op), int(M),
-              int(N), int(Kd), stream());
+    const auto t = floatType(out, op);
+    void *ws = core::context().runtime().scratch(K::linearWorkspaceBytes(t, int(M), int(N), int(Kd)));
+    K::linear(out->data(), in->data(), weight->data(), bias ? bias->data() : nullptr, t, int(M), int(N), int(Kd),
+              stream(), false, ws);
 }
 
 void linearPackWeight(const tensor_t &packed, const tensor_t &weight) {

@@ -31,11 +31,10 @@ LIB_PATH = Path(os.environ.get("LLAISYS_LIBRARY") or Path(__file__).resolve().pa
 
 
 def _share_hip_runtime():
-    """Map the HIP runtime (and the GEMM libraries) this process should use before
-    libllaisys.so binds them.
+    """Map the HIP runtime this process should use before libllaisys.so binds it.
 
-    libllaisys.so needs libamdhip64.so.7, librocblas.so.5 and libhipblaslt.so.1. PyTorch-ROCm
-    ships its own copies under the same sonames; if libllaisys.so were loaded
+    libllaisys.so needs libamdhip64.so.7 (and no other ROCm library). PyTorch-ROCm
+    ships its own copy under the same soname; if libllaisys.so were loaded
     first it would pull in /opt/rocm's and a later `import torch` would bring
     a second HIP runtime into the process, whose device pointers the first
     cannot use. So when torch is installed its copies are mapped first (by
@@ -48,8 +47,7 @@ def _share_hip_runtime():
         spec = importlib.util.find_spec("torch")
         if spec and spec.submodule_search_locations:
             torch_lib = Path(list(spec.submodule_search_locations)[0]) / "lib"
-            # The GEMM library too: both share sonames with /opt/rocm's copies.
-            libs = [os.fspath(torch_lib / n) for n in ("libamdhip64.so", "librocblas.so", "libhipblaslt.so") if (torch_lib / n).is_file()]
+            libs = [os.fspath(torch_lib / n) for n in ("libamdhip64.so",) if (torch_lib / n).is_file()]
     for lib in libs:
         ctypes.CDLL(lib, mode=ctypes.RTLD_GLOBAL)
 

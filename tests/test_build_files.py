@@ -21,11 +21,20 @@ def test_hip_lua_flags_equal_build_py():
     assert _lua_flags() == py
 
 
+def test_hip_lua_extra_flags_equal_build_py():
+    text = (ROOT / "xmake" / "hip.lua").read_text()
+    block = text.split("-- HIP_EXTRA_BEGIN", 1)[1].split("-- HIP_EXTRA_END", 1)[0]
+    lua = {k: re.findall(r'"([^"]+)"', v) for k, v in re.findall(r'\["([^"]+)"\]\s*=\s*\{([^}]*)\}', block)}
+    assert lua == B.EXTRA
+    assert all((B.CSRC / k).is_file() for k in B.EXTRA)
+
+
 def test_hip_lua_globs_cover_every_source():
     text = (ROOT / "xmake" / "hip.lua").read_text()
     assert 'add_files("../llaisys_amd/csrc/**.cpp", "../llaisys_amd/csrc/**.hip")' in text
     assert {p.suffix for p in B._sources()} <= {".cpp", ".hip"}
-    assert "-lrocblas" in Path(B.__file__).read_text() and 'add_links("rocblas", "hipblaslt")' in text
+    # every kernel is this project's own: no GEMM library is linked
+    assert "-lrocblas" not in Path(B.__file__).read_text() and "add_links" not in text
 
 
 def test_root_xmake_has_amd_gpu_option_including_hip_lua():

@@ -18,6 +18,14 @@ local hip_flags = {
 }
 -- HIP_FLAGS_END
 
+-- Per-source extra flags (llaisys_amd/build.py's EXTRA), keyed by the path
+-- under llaisys_amd/csrc.
+-- HIP_EXTRA_BEGIN
+local hip_extra = {
+    ["kernels/gemm.hip"] = {"-mllvm", "-amdgpu-mfma-vgpr-form"},
+}
+-- HIP_EXTRA_END
+
 -- Compile one source with hipcc as HIP; the argument vector is passed as is
 -- (paired -Xclang options must not be merged or de-duplicated).
 rule("hip-gfx950")
@@ -28,6 +36,8 @@ rule("hip-gfx950")
         os.mkdir(path.directory(objectfile))
         local argv = {"-x", "hip"}
         for _, f in ipairs(hip_flags) do table.insert(argv, f) end
+        local rel = path.relative(sourcefile, path.join(os.projectdir(), "llaisys_amd", "csrc")):gsub("\\", "/")
+        for _, f in ipairs(hip_extra[rel] or {}) do table.insert(argv, f) end
         table.insert(argv, "-I" .. path.join(os.projectdir(), "include"))
         table.insert(argv, "-c")
         table.insert(argv, sourcefile)
@@ -43,8 +53,6 @@ target("llaisys")
     add_files("../llaisys_amd/csrc/**.cpp", "../llaisys_amd/csrc/**.hip")
     set_toolset("sh", hipcc)
     add_shflags("--offload-arch=gfx950", {force = true})
-    add_linkdirs(path.join(rocm, "lib"))
-    add_links("rocblas", "hipblaslt")
     after_build(function (target)
         -- the ctypes loader reads the library from the package directory
         -- (as python/llaisys/libllaisys/__init__.py:17-40 does)
