@@ -9,8 +9,11 @@
 #include "llaisys/runtime.h"
 #include "llaisys/serving.h"
 #include "llaisys/tensor.h"
+#include "llaisys/testing.h"
 
 #include "common.hpp"
+#include "device/hip_check.hpp"
+#include "kernels/launch.hpp"
 #include "core/core.hpp"
 #include "device/runtime_api.hpp"
 #include "kvcache/block_manager.hpp"
@@ -182,6 +185,24 @@ private:
     LlaisysQwen2Model *m_;
 };
 
+} // namespace
+
+// ---- test hooks' plumbing (testing.h)
+namespace {
+// The AMD runtime of the current HIP device, its stream, and a sync after the launch.
+template <typename F> void testHook(F &&f) {
+    guardedVoid([&] {
+        int dev = 0;
+        HIP_CHECK(hipGetDevice(&dev));
+        auto &ctx = llaisys::core::context();
+        ctx.setDevice(LLAISYS_DEVICE_AMD, dev);
+        void *stream = ctx.runtime().stream();
+        f(stream, ctx.runtime());
+        HIP_CHECK(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    });
+}
+uint16_t *w16(void *p) { return static_cast<uint16_t *>(p); }
+const uint16_t *r16(const void *p) { return static_cast<const uint16_t *>(p); }
 } // namespace
 
 __C {
@@ -645,6 +666,50 @@ int llaisysSchedulerStats(LlaisysScheduler *s, int64_t *out) {
             return 0;
         },
         -1);
+}
+
+// ---------------- testing.h (the decode step's kernels called alone)
+
+void llaisysTestPackWeight(void *packed, const void *w, const void *fold_g, int N, int K) {
+    testHook([&](void *s, auto &) { llaisys::kernels::packWeight(w16(packed), r16(w), r16(fold_g), N, K, s); });
+}
+
+void llaisysTestPackWeightGateUp(void *packed, const void *w, int di, int K) {
+    testHook([&](void *s, auto &) { llaisys::kernels::packWeightGateUp(w16(packed), r16(w), di, K, s); });
+}
+
+void llaisysTestPackedXGemm(void *y, const void *x_packed, const void *w_packed, int M, int N, int K, int accumulate,
+                            void *y_packed) {
+    testHook([&](void *s, auto &) {
+        llaisys::kernels::packedXGemm(w16(y), r16(x_packed), r16(w_packed), M, N, K, accumulate != 0, s,
+                                      w16(y_packed));
+    });
+}
+
+void llaisysTestQkvRopeGemm(void *q, void *k_pool, void *v_pool, const void *x_packed, const void *w_packed,
+                            const void *bias, const int32_t *table, const int32_t *ctx, int M, int nh, int nkvh,
+                            int K, int max_pages, int num_blocks, float eps, float theta) {
+    testHook([&](void *s, auto &rt) {
+        llaisys::kernels::qkvRopeGemm(w16(q), w16(k_pool), w16(v_pool), r16(x_packed), r16(w_packed), r16(bias),
+                                      table, ctx, M, nh, nkvh, K, max_pages, num_blocks, eps, theta, rt.errorWord(),
+                                      s);
+    });
+}
+
+void llaisysTestGateUpSwiglu(void *act, const void *x_packed, const void *w_packed, int M, int di, int K, float eps,
+                             int act_packed) {
+    testHook([&](void *s, auto &) {
+        llaisys::kernels::gateUpSwiglu(w16(act), r16(x_packed), r16(w_packed), M, di, K, eps, s, act_packed != 0);
+    });
+}
+
+void llaisysTestSplitKPackedGemm(void *y, const void *x_packed, const void *w_packed, int M, int N, int K,
+                                 int accumulate, void *y_packed) {
+    testHook([&](void *s, auto &rt) {
+        auto *part = static_cast<float *>(rt.scratch(llaisys::kernels::splitKPackedWorkspaceBytes(M, N, K)));
+        llaisys::kernels::splitKPackedGemm(w16(y), r16(x_packed), r16(w_packed), M, N, K, accumulate != 0, part, s,
+                                           w16(y_packed));
+    });
 }
 
 } // extern "C"

@@ -25,6 +25,7 @@ from .ops import load_ops
 from .runtime import LlaisysRuntimeAPI, load_runtime
 from .serving import llaisysScheduler_t, load_serving
 from .tensor import llaisysTensor_t, load_tensor
+from .testing import load_testing
 
 # LLAISYS_LIBRARY may name another build of the same library (e.g. a tuning variant).
 LIB_PATH = Path(os.environ.get("LLAISYS_LIBRARY") or Path(__file__).resolve().parent / "libllaisys.so")
@@ -71,6 +72,7 @@ load_ops(LIB_LLAISYS)
 load_kv_cache(LIB_LLAISYS)
 load_qwen2(LIB_LLAISYS)
 load_serving(LIB_LLAISYS)
+load_testing(LIB_LLAISYS)
 
 
 class LlaisysError(RuntimeError):
