@@ -23,6 +23,10 @@ eps 1e-6, RoPE theta 1e4, bf16 weights ~ N(0, 0.02)) with 128 sequences of
   bf16 roundings grow over 28 layers to ~3 % of the logits' max (measured).
 * 64 greedy steps in one llaisysQwen2ModelDecode call give the tokens of 64
   single llaisysQwen2ModelStep calls from an identical (forked) state.
+* The same dimensions with 1 and 2 layers (hidden 1536, FFN 8960, vocabulary
+  151936, 128 sequences x 2048 tokens, so the decode step runs the config-5
+  kernels at M = 128): the logits of a prefill and two decode steps within
+  3 % of the reference's max, per-layer error well under the 28-layer 10 %.
 """
 import numpy as np
 import pytest
@@ -68,11 +72,14 @@ def setup():
 @pytest.fixture(scope="module")
 def hf(setup):
     """transformers' Qwen2 in fp32 holding the library model's bf16 weights."""
+    return hf_of(setup[0], SHAPE["nlayer"])
+
+
+def hf_of(model, nlayer):
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
-    model = setup[0]
     cfg = Qwen2Config(vocab_size=SHAPE["voc"], hidden_size=SHAPE["hs"], intermediate_size=SHAPE["di"],
-                      num_hidden_layers=SHAPE["nlayer"], num_attention_heads=SHAPE["nh"],
+                      num_hidden_layers=nlayer, num_attention_heads=SHAPE["nh"],
                       num_key_value_heads=SHAPE["nkvh"], head_dim=128, max_position_embeddings=4096,
                       rms_norm_eps=1e-6, rope_theta=10000.0, tie_word_embeddings=False, attn_implementation="sdpa")
     _log("transformers model")
@@ -122,6 +129,38 @@ def check_tokens(toks, want, got):
         best = int(row.argmax())
         if t != best:
             assert (row[best] - row[t]).item() <= 2 * tol, f"token {t} vs reference {best}"
+
+
+@pytest.mark.parametrize("nlayer", [1, 2])
+def test_one_and_two_layers_at_config5_dims(nlayer):
+    maxseq = CTX + 8
+    pages = (maxseq + 15) // 16
+    meta = Qwen2Meta(**{**SHAPE, "nlayer": nlayer}, maxseq=maxseq, epsilon=1e-6, theta=10000.0, end_token=-1)
+    model = Qwen2.random(meta, seed=7 + nlayer, std=0.02, num_blocks=B * pages + 16)
+    rng = np.random.default_rng(7)
+    prompts = [rng.integers(0, SHAPE["voc"], CTX).tolist() for _ in range(B)]
+    ids = [model.create_sequence()[0] for _ in range(B)]
+    nxt = []
+    for s in range(0, B, 16):
+        nxt += model.step(ids[s:s + 16], prompts[s:s + 16])
+    ref = hf_of(model, nlayer)
+    hist = [list(p) for p in prompts[:CHECKED]]
+    try:
+        for step in range(2):  # decode steps of the whole batch (M = 128)
+            feed = list(nxt)
+            for i in range(CHECKED):
+                hist[i].append(feed[i])
+            nxt = model.step(ids, [[t] for t in feed])
+            got = to_torch(model.logits())[:CHECKED].float()
+            want = hf_last_logits(ref, hist)
+            scale, err = want.abs().max().item(), (got - want).abs().max().item()
+            _log(f"{nlayer} layer(s), decode step {step}: max|diff| {err:.3g} of max|logit| {scale:.3g}")
+            assert err <= 3e-2 * scale
+        assert L.device_error_flags() == 0
+    finally:
+        del ref
+        del model
+        torch.cuda.empty_cache()
 
 
 def test_prefill_and_teacher_forced_decode_match_transformers(setup, hf):
