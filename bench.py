@@ -57,6 +57,9 @@ def parse():
     p.add_argument("--profiles-dir", default=str(ROOT / "profiles"), help="where the --summarize* outputs go")
     p.add_argument("--summarize-step", nargs=2, metavar=("TRACE_DIR", "TAG"),
                    help="per-step kernel table of a --workload qwen2 kernel trace into profiles/TAG.md")
+    p.add_argument("--step-pmc", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                   help="with --summarize-step: FETCH_SIZE / WRITE_SIZE runs of the same workload and of "
+                        "--workload copy, for per-kernel HBM bytes per step")
     p.add_argument("--summarize-mfma", nargs="+", metavar="DIR",
                    help="STATS_DIR UTIL_DIR MOPS_DIR [INSTS_DIR] TAG: per-kernel MFMA use from a kernel trace and "
                         "two (three) counter runs into profiles/TAG.md")
@@ -349,10 +352,11 @@ def cpu_baseline_decode(inst, budget_s):
         "cores": threads,
         "kind": "port",
         "sample": f"oracle/oracle.c paged attention (fp32, OpenMP over sequences, {threads} threads of the "
-                  f"{allowed} CPUs this process may use; os.cpu_count() = {ncpu}) on the first {nseq} of "
+                  f"{allowed} CPUs this process may use, capped at 16 = a one-GPU box's CPU share; "
+                  f"os.cpu_count() = {ncpu}) on the first {nseq} of "
                   f"{len(inst.ctx)} sequences ({int(inst.ctx[:nseq].sum())} tokens), {reps} reps in "
                   f"{total:.1f} s; GPU bf16 vs CPU max|err| {max_err:.2e}",
-        "host_cpus": {"used": threads, "affinity": allowed, "os_cpu_count": ncpu},
+        "host_cpus": {"used": threads, "affinity": allowed, "os_cpu_count": ncpu, "cap": 16},
         "single_thread": {
             "value": round(bytes1 / per1 / 1e9, 3), "unit": "GB/s", "cores": 1,
             "sample": f"the same code with one thread on the first {n1} sequences "
@@ -595,7 +599,8 @@ def run_qwen2(args):
                    "single_step_call_ms": round(single_ms, 4),
                    "prefill_tokens_per_s": round(B * ctx0 / t_prefill, 1), "setup_s": round(t_init, 2)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("qwen2_1.5b_decode_step_b128"),
                      "algorithmic_bytes_per_step": int(nbytes), "weight_bytes": int(wbytes),
                      "kv_bytes": int(kvbytes)},
     }
@@ -696,13 +701,28 @@ def run_append_gather(args):
     def step(i):  # one launch: the append fused into the gather
         L.Ops.paged_kv_append_gather(ko, vo, kp, vp, kn, vn, tab, ctx, cut)
 
+    # Back-to-back launches over enough copies of the pools and outputs that
+    # each call's bytes left the 256 MB MALL since their last use: the per-call
+    # time is the kernel's cold-cache duration plus the dispatch gap, the
+    # figure rocprofv3's average kernel duration reports for the same calls.
+    per_copy = 2 * pool_k.numel() * 2 + 2 * T * 256 * 2
+    copies = max(2, -(-(640 << 20) // per_copy))
+    rot = [(to_llaisys(pool_k), to_llaisys(pool_v),
+            to_llaisys(torch.zeros((T, 2, 128), dtype=torch.bfloat16, device="cuda")),
+            to_llaisys(torch.zeros((T, 2, 128), dtype=torch.bfloat16, device="cuda"))) for _ in range(copies)]
+
+    def step_rot(i):
+        k_, v_, ko_, vo_ = rot[i % copies]
+        L.Ops.paged_kv_append_gather(ko_, vo_, k_, v_, kn, vn, tab, ctx, cut)
+
     def step_two_calls(i):
         L.Ops.paged_kv_append(kp, vp, kn, vn, tab, ctx)
         L.Ops.paged_kv_gather(ko, vo, kp, vp, tab, cut)
 
     # The pool (64 MiB) and the output fit in the MALL: time each step after a
     # flush so the inputs come from HBM, and report the cache-warm rate beside it.
-    kern_ms, wall_ms = time_steps_flushed(step, stream, args.steps, args.warmup)
+    kern_ms, wall_ms = time_steps(step_rot, stream, args.steps, args.warmup)
+    single_ms, _ = time_steps_flushed(step, stream, args.steps, args.warmup)
     warm_ms, _ = time_steps(step, stream, args.steps, args.warmup)
     two_ms = two_warm_ms = None
     if not getattr(args, "ag_fused_only", False):
@@ -724,12 +744,13 @@ def run_append_gather(args):
                 "what": "llaisysPagedKVAppendGather on LLAISYS_DEVICE_CPU tensors, same inputs"}
     # The practical ceiling at this size: torch's contiguous device copy of the
     # same bytes (half read, half written), timed the same two ways.
-    src = torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")
-    dst = torch.empty_like(src)
+    pairs = [(torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda"),
+              torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")) for _ in range(copies)]
     cstream = torch.cuda.current_stream()
-    copy_ms, _ = time_steps_flushed(lambda i: dst.copy_(src), cstream, args.steps, args.warmup)
-    copy_warm_ms, _ = time_steps(lambda i: dst.copy_(src), cstream, args.steps, args.warmup)
-    del src, dst
+    copy_ms, _ = time_steps(lambda i: pairs[i % copies][1].copy_(pairs[i % copies][0]), cstream, args.steps,
+                            args.warmup)
+    copy_warm_ms, _ = time_steps(lambda i: pairs[0][1].copy_(pairs[0][0]), cstream, args.steps, args.warmup)
+    del pairs, rot
     return {
         "metric": "paged KV append+gather achieved HBM GB/s, 1 GPU", "value": round(gbs, 2), "unit": "GB/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 5),
@@ -737,7 +758,12 @@ def run_append_gather(args):
         "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "BASELINE config 2: 32 seqs len U[1,2048], 4096-block pool, append 1 + gather",
                    "entry_point": "llaisysPagedKVAppendGather (append fused into the gather, one launch)",
-                   "timing": "HIP events per step, L2/MALL flushed by an untimed 512 MiB read before each step"},
+                   "timing": f"HIP events around {args.steps} back-to-back calls rotating over {copies} copies of "
+                             "the pools and outputs (each call's bytes cold in the MALL)"},
+        "single_call_flushed": {"kernel_ms": round(single_ms, 5),
+                                "GB/s": round(nbytes / (single_ms * 1e-3) / 1e9, 2),
+                                "timing": "HIP events around one call after an untimed 512 MiB read (the launch "
+                                          "and the event gaps are inside)"},
         "mall_resident": {"kernel_ms": round(warm_ms, 5), "GB/s": round(nbytes / (warm_ms * 1e-3) / 1e9, 2),
                           "timing": "back-to-back steps, inputs left in the MALL"},
         "two_calls": None if two_ms is None else {
@@ -746,7 +772,8 @@ def run_append_gather(args):
             "mall_resident_kernel_ms": round(two_warm_ms, 5)},
         "cpu_host_path": host,
         "same_bytes_device_copy": {
-            "what": "torch copy_ of nbytes/2 contiguous bytes (reads + writes = the step's bytes)",
+            "what": "torch copy_ of nbytes/2 contiguous bytes (reads + writes = the step's bytes), timed as the "
+                    "step: back-to-back over the same number of rotating copies",
             "kernel_ms": round(copy_ms, 5), "mall_resident_kernel_ms": round(copy_warm_ms, 5),
             "step_time_over_copy_time": round(kern_ms / copy_ms, 3)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -771,6 +798,37 @@ def run_copy(args):
             "unit": "GB/s", "bytes_per_launch_read": n, "bytes_per_launch_written": n, "kernel_ms": kern_ms,
             "from_hbm": {"kernel_ms": flushed_ms, "GB/s": round(2 * n / (flushed_ms * 1e-3) / 1e9, 2),
                          "timing": "L2/MALL flushed by an untimed 512 MiB read before each step"}}
+
+
+def _csvs(d, suffix):
+    import glob
+
+    return glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)
+
+
+def _counter_means(d, last_steps=None):
+    """Mean counter value per kernel name over a --pmc run's dispatches; with
+    last_steps, over the dispatches of the run's last `last_steps` decode steps
+    only (a step ends with the argmax finish kernel)."""
+    import csv
+    from collections import defaultdict
+
+    rows = []
+    for f in _csvs(d, "counter_collection.csv"):
+        rows += [(int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])) for r in csv.DictReader(open(f))]
+    rows.sort()
+    if last_steps:
+        ends = [i for i, r in enumerate(rows) if "argmaxFinish" in r[1]]
+        rows = rows[ends[-last_steps - 1] + 1: ends[-1] + 1]
+    acc = defaultdict(list)
+    for _, name, v in rows:
+        acc[name].append(v)
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def _counter_scale(copy_dir, copy_bytes=512 << 20):
+    """Bytes per counter unit (KiB) from a run of --workload copy over copy_bytes."""
+    return copy_bytes / 1024 / max(v for k, v in _counter_means(copy_dir).items() if "copy" in k.lower())
 
 
 def summarize(args):
@@ -886,20 +944,54 @@ def summarize_step(args):
         agg[key][0] += 1
         agg[key][1] += (en - st) / 1e3
     busy = sum(v[1] for v in agg.values()) / k
+    pmc = args.step_pmc
+    fetch = write = None
+    if pmc:
+        fs, ws = _counter_scale(pmc[2]), _counter_scale(pmc[3])
+        fetch = {short(n): v * 1024 * fs for n, v in _counter_means(pmc[0], last_steps=2).items()}
+        write = {short(n): v * 1024 * ws for n, v in _counter_means(pmc[1], last_steps=2).items()}
+    cmds = [f"rocprofv3 --kernel-trace --output-format csv -d {trace_dir} -o run -- python3 bench.py --workload qwen2 "
+            f"--steps {k} --warmup 2 --no-cpu"]
+    if pmc:
+        for c, d in (("FETCH_SIZE", pmc[0]), ("WRITE_SIZE", pmc[1])):
+            cmds.append(f"rocprofv3 --pmc {c} --output-format csv -d {d} -o run -- python3 bench.py --workload qwen2 "
+                        f"--steps 2 --warmup 1 --no-cpu")
+        for c, d in (("FETCH_SIZE", pmc[2]), ("WRITE_SIZE", pmc[3])):
+            cmds.append(f"rocprofv3 --pmc {c} --output-format csv -d {d} -o run -- python3 bench.py --workload copy "
+                        f"--steps 5 --warmup 2")
+    cmds.append(f"python3 bench.py --summarize-step {trace_dir} {tag} --steps {k}"
+                + (f" --step-pmc {' '.join(pmc)}" if pmc else ""))
     lines = [f"# {tag}: one decode step of the Qwen2-1.5B-shape model (rocprofv3 kernel trace)", "",
-             "Command (from the repo root, on the MI355X box):", "", "```",
-             f"rocprofv3 --kernel-trace --output-format csv -d {trace_dir} -o run -- python3 bench.py --workload qwen2 "
-             f"--steps {k} --warmup 2 --no-cpu",
-             f"python3 bench.py --summarize-step {trace_dir} {tag} --steps {k}", "```", "",
+             "Commands (from the repo root, on the MI355X box):", "", "```", *cmds, "```", "",
              f"Last {k} steps: GPU span {span_us:.1f} us per step, kernels busy {busy:.1f} us per step "
-             f"({len(sel) / k:.0f} dispatches per step).", "",
-             "| kernel | grid (work-items) | per step | us per step | avg us |", "|---|---|---|---|---|"]
+             f"({len(sel) / k:.0f} dispatches per step).", ""]
+    if pmc:
+        lines += [f"HBM bytes per dispatch: FETCH_SIZE / WRITE_SIZE (KiB) scaled by a plain 512 MiB device copy "
+                  f"(x{fs:.3f} / x{ws:.3f}), averaged over the kernel's dispatches in the last two decode steps "
+                  f"of the PMC runs.", "",
+                  "| kernel | grid (work-items) | per step | us per step | avg us | read MB | written MB | TB/s |",
+                  "|---|---|---|---|---|---|---|---|"]
+    else:
+        lines += ["| kernel | grid (work-items) | per step | us per step | avg us |", "|---|---|---|---|---|"]
+    step_bytes = 0.0
     for (name, grid), (n, t) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
-        lines.append(f"| `{name}` | {grid} | {n / k:.0f} | {t / k:.1f} | {t / n:.2f} |")
+        row = f"| `{name}` | {grid} | {n / k:.0f} | {t / k:.1f} | {t / n:.2f} |"
+        if pmc:
+            rb, wb = fetch.get(name, 0.0), write.get(name, 0.0)
+            step_bytes += (rb + wb) * n / k
+            row += f" {rb / 1e6:.2f} | {wb / 1e6:.2f} | {(rb + wb) / (t / n * 1e-6) / 1e12:.2f} |"
+        lines.append(row)
+    if pmc:
+        lines += ["", f"HBM bytes per step (every kernel's per-dispatch bytes x its dispatches per step): "
+                  f"{step_bytes / 1e9:.3f} GB"]
     print("\n".join(lines))
     outdir = Path(args.profiles_dir)
     outdir.mkdir(parents=True, exist_ok=True)
     (outdir / f"{tag}.md").write_text("\n".join(lines) + "\n")
+    if pmc:
+        (outdir / f"{tag}_traffic.json").write_text(json.dumps(
+            {"tag": tag, "hbm_bytes_per_launch": int(step_bytes), "unit": "bytes per decode step",
+             "step_span_us": round(span_us, 1)}, indent=1) + "\n")
 
 
 def summarize_mfma(args):

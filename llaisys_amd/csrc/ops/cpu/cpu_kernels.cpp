@@ -100,7 +100,9 @@ void widen(float *dst, const void *src, ElemType t, size_t n);
 class Pool {
 public:
     static Pool &get() {
-        static Pool *p = new Pool(threads() - 1); // never destroyed: workers may outlive static teardown
+        // Destroyed at exit (its workers joined); no job runs past main's return.
+        static Pool pool(threads() - 1);
+        static Pool *p = &pool;
         return *p;
     }
 
@@ -133,7 +135,18 @@ private:
 
     explicit Pool(int nworkers) {
         for (int i = 0; i < nworkers; ++i) workers_.emplace_back([this] { loop(); });
-        for (auto &w : workers_) w.detach();
+    }
+
+    // At process exit the workers leave their wait and are joined, so no
+    // thread outlives the library.
+    ~Pool() {
+        {
+            std::lock_guard<std::mutex> g(m_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto &w : workers_)
+            if (w.joinable()) w.join();
     }
 
     void work(const Job &j) {
@@ -151,7 +164,8 @@ private:
             Job j;
             {
                 std::unique_lock<std::mutex> g(m_);
-                cv_.wait(g, [&] { return generation_ != seen; });
+                cv_.wait(g, [&] { return stop_ || generation_ != seen; });
+                if (stop_) return;
                 seen = generation_;
                 j = job_;
             }
@@ -168,6 +182,7 @@ private:
     std::atomic<size_t> cursor_{0};
     size_t pending_ = 0;
     uint64_t generation_ = 0;
+    bool stop_ = false;
 };
 
 // Run fn(i) for i in [0, n) over the host threads, in chunks of at least
