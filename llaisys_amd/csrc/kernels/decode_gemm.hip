@@ -31,6 +31,7 @@
 // epilogue), gateUpSwiglu (gate-up, row 1/rms and SwiGLU over interleaved
 // gate/up weights) and splitKPackedGemm (the down projection); and the
 // LDS-staged split-K GEMM for long K with row-major X.
+#include "lanes.hpp"
 #include "launch.hpp"
 #include "step_common.hpp"
 
@@ -56,6 +57,12 @@ __device__ __forceinline__ float addSquares(float ss, uint32_t w) {
     return __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
 }
 
+
+// silu(g) * u with the hardware exp2 and reciprocal (each ~1 ulp; the
+// result is rounded to bf16, 2^-9).
+__device__ __forceinline__ float siluTimes(float g, float u) {
+    return u * g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
 
 struct GemmArgs {
     uint16_t *y;
@@ -628,10 +635,7 @@ __global__ void __launch_bounds__(256) qkvRopeGemmKernel(const u32x4 *xp, const 
             for (int c = 0; c < 4; ++c) ss[i] = addSquares(ss[i], xv[j][i][c]);
         }
 #pragma unroll
-    for (int i = 0; i < kPxTile; ++i) {
-        ss[i] += __shfl_xor(ss[i], 16);
-        ss[i] += __shfl_xor(ss[i], 32);
-    }
+    for (int i = 0; i < kPxTile; ++i) ss[i] = sumOverGroups(ss[i]);
     if (lane < 16) {
 #pragma unroll
         for (int i = 0; i < kPxTile; ++i) ssl[wave][16 * i + lane] = ss[i];
@@ -754,10 +758,7 @@ gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int d
     }
     // Row m = 16 i + lane % 16: the lane's 8 k per step, then its 4 k groups.
 #pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        ss[i] += __shfl_xor(ss[i], 16);
-        ss[i] += __shfl_xor(ss[i], 32);
-    }
+    for (int i = 0; i < MB; ++i) ss[i] = sumOverGroups(ss[i]);
     if (lane < 16) {
 #pragma unroll
         for (int i = 0; i < MB; ++i) ssl[wave][16 * i + lane] = ss[i];
@@ -785,11 +786,11 @@ gateUpSwigluKernel(uint16_t *act, const u32x4 *xp, const u32x4 *wp, int M, int d
             // the up rows of the same columns; lane < 32 finishes elements
             // 0, 1, lane >= 32 elements 2, 3.
             const bool lo = lane < 32;
-            const float p0 = __shfl_xor(lo ? v[2] : v[0], 32), p1 = __shfl_xor(lo ? v[3] : v[1], 32);
+            const float p0 = partner32(lo ? v[2] : v[0]), p1 = partner32(lo ? v[3] : v[1]);
             const float g0 = r * (lo ? v[0] : p0), g1 = r * (lo ? v[1] : p1);
             const float u0 = r * (lo ? p0 : v[2]), u1 = r * (lo ? p1 : v[3]);
-            const __bf16 b0 = (__bf16)(u0 * g0 / (1.f + expf(-g0)));
-            const __bf16 b1 = (__bf16)(u1 * g1 / (1.f + expf(-g1)));
+            const __bf16 b0 = (__bf16)siluTimes(g0, u0);
+            const __bf16 b1 = (__bf16)siluTimes(g1, u1);
             const int col = 8 * (blk0 + t) + 4 * ((lane >> 4) & 1) + (lo ? 0 : 2);
             // act_packed: in operand order (the two columns share one 8-column chunk)
             if (m < M)

@@ -17,6 +17,7 @@
 // Nothing crosses lanes except the running max (2 shuffles).
 #pragma once
 
+#include "lanes.hpp"
 #include "launch.hpp"
 
 #include <hip/hip_runtime.h>
@@ -38,19 +39,9 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 
 __device__ __forceinline__ float exp2Fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Max over the lanes n, n+16, n+32, n+48 (the four key groups of a column),
-// by the gfx950 lane swaps: v_permlane32_swap with one value in both operands
-// leaves each lane its own value and its partner 32 lanes away, one in each
-// result; v_permlane16_swap does the same 16 lanes away. Plain VALU, no LDS
-// round trip as a ds_bpermute shuffle would take.
-__device__ __forceinline__ float maxOverGroups(float x) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, x);
-    const auto h = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    const float y = fmaxf(__builtin_bit_cast(float, h[0]), __builtin_bit_cast(float, h[1]));
-    const uint32_t v = __builtin_bit_cast(uint32_t, y);
-    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
-}
+// maxOverGroups (lanes.hpp): max over the lanes n, n+16, n+32, n+48 (the
+// four key groups of a column).
+using kernels::maxOverGroups;
 
 // Inclusive prefix sum over the 64 lanes of a wave with DPP: row shifts by
 // 1, 2, 4, 8 sum within each row of 16 lanes (lanes without a source add 0),

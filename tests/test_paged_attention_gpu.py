@@ -311,3 +311,42 @@ def test_bad_block_id_and_overlong_context_flag_errors():
     L.Ops.paged_attention(out, q, kp, vp, to_llaisys(torch.from_numpy(case.table)),
                           to_llaisys(torch.from_numpy(long_ctx)), SCALE)
     assert L.device_error_flags() & 2
+
+
+def spread_case(seed, ctx, nh=12, nkvh=2):
+    """Scores that differ by far more than fp32's exponent range within every
+    page: keys in slots 4-15 of a page have a dot product with q about 2^8
+    larger (in exp2 units) than those in slots 0-3. A softmax whose running
+    max leaves out any of a page's key groups overflows exp2 to inf on such
+    keys; the normalised result is the mean of V over the largest keys."""
+    case = make_case(seed, np.asarray(ctx, np.int32), nh=nh, nkvh=nkvh)
+    big = np.zeros(16, bool)
+    big[4:] = True
+    k = oracle.bf16_to_f32(case.k_log) * 0.25
+    k[:, :, big, :] += 12.0
+    case.k_log[:] = oracle.f32_to_bf16(k)
+    q = oracle.f32_to_bf16(np.abs(oracle.randn(seed + 5, (case.B, nh, 128))) * 0.5 + 1.0)
+    return case, q
+
+
+@pytest.mark.parametrize("ctx", [[40, 300, 1000], [16, 17, 2049]])
+def test_decode_softmax_max_covers_every_key_group(ctx):
+    case, q = spread_case(77, ctx)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE)
+    got32, got16 = run_decode(case, q, torch.float32), run_decode(case, q, torch.bfloat16)
+    assert np.isfinite(got32).all() and np.isfinite(got16).all()
+    check(got32, got16, ref)
+
+
+def test_varlen_softmax_max_covers_every_key_group():
+    # one prefill chunk of 40 queries over 300 prior tokens, plus two decodes
+    ctx = np.array([340, 200, 1000], np.int32)
+    case, _ = spread_case(78, ctx)
+    lq = np.array([40, 1, 1])
+    cu_q = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    q = oracle.f32_to_bf16(np.abs(oracle.randn(83, (int(cu_q[-1]), 12, 128))) * 0.5 + 1.0)
+    ref = oracle.paged_attention(q, case.k_log, case.v_log, case.table, case.ctx, SCALE, cu_q=cu_q)
+    got32 = run_varlen(case, q, cu_q, torch.float32)
+    got16 = run_varlen(case, q, cu_q, torch.bfloat16)
+    assert np.isfinite(got32).all() and np.isfinite(got16).all()
+    check(got32, got16, ref)
