@@ -12,8 +12,8 @@
 //    of every lane (k 4 g + e, g = 0..3): the same k order on both operands,
 //    so the sum is over the same products.
 //
-// A workgroup of 4 waves (2 x 2) owns a BM x BN tile of Y; each wave a
-// (BM / 2) x (BN / 2) sub-tile. K advances in tiles of 128 B per row (64
+// A workgroup of 4 or 8 waves (2 x 2, 2 x 4 or 4 x 2) owns a BM x BN tile
+// of Y; each wave one sub-tile of it (64 x 64 to 128 x 64). K advances in tiles of 128 B per row (64
 // 16-bit or 32 f32 elements): every thread loads its 16 B pieces of the next
 // k tile of X and W into registers by buffer loads (out-of-range rows and k
 // come back as zeros, so edge tiles need no other guard), the waves run the
@@ -38,6 +38,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -147,21 +148,23 @@ typedef __attribute__((address_space(3))) void lds_void;
 // 4-bank groups. Lane i therefore fetches piece (i % 4) ^ ((i / 16) % 4).
 __device__ __forceinline__ int slotOf(int r, int c) { return c ^ ((r >> 2) & 3); }
 
-template <ElemType T, int BM, int BN>
-__global__ void __launch_bounds__(kThreads) gemmKernel(GemmParams p) {
+// WGM x WGN waves, wave (wm, wn) owning the (BM / WGM) x (BN / WGN) sub-tile.
+template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
+    constexpr int NW = WGM * WGN;
     constexpr int ES = Elem<T>::size;
     constexpr int KT = kRowBytes / ES;              // elements per k tile
-    constexpr int TM = BM / 32, TN = BN / 32;       // 16-row fragments per wave
+    constexpr int TM = BM / (16 * WGM), TN = BN / (16 * WGN); // 16-row fragments per wave
     constexpr int XB = BM / 16, WB = BN / 16;       // 1 KiB blocks per operand per k tile
-    constexpr int XW = XB / 4, WW = WB / 4;         // ... issued by each wave
+    constexpr int XW = XB / NW, WW = WB / NW;       // ... issued by each wave
     constexpr int STAGE = (BM + BN) * kRowBytes / 16; // u32x4 per stage
     constexpr int kLoadsPerStage = XW + WW;          // per wave
-    static_assert(XB % 4 == 0 && WB % 4 == 0, "each wave issues whole blocks");
+    static_assert(XB % NW == 0 && WB % NW == 0, "each wave issues whole blocks");
     extern __shared__ u32x4 lds[];                   // [kStages][X blocks | W blocks]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % WGM, wn = wave / WGM;
     // Workgroup b: split b / tiles over k tiles [s nk / S, (s + 1) nk / S)
     // of tile b % tiles.
     const int tiles = p.mtiles * p.ntiles;
@@ -181,7 +184,7 @@ __global__ void __launch_bounds__(kThreads) gemmKernel(GemmParams p) {
     // Block b of the wave is block wave + 4 b of the operand (rows 16 (wave + 4 b) ..).
     const uint32_t xbase = uint32_t(m0 + 16 * wave + lr) * row_bytes + 16 * lc;
     const uint32_t wbase = uint32_t(n0 + 16 * wave + lr) * row_bytes + 16 * lc;
-    const uint32_t bstride = 64u * row_bytes; // 4 blocks of 16 rows
+    const uint32_t bstride = 16u * NW * row_bytes; // NW blocks of 16 rows
     const int nk_all = (p.K + KT - 1) / KT;
     const int kt0 = split * nk_all / p.splits;
     const int nk = (split + 1) * nk_all / p.splits - kt0;
@@ -191,11 +194,11 @@ __global__ void __launch_bounds__(kThreads) gemmKernel(GemmParams p) {
         const bool in_k = kt < nk && kb + 16 * lc < row_bytes;
 #pragma unroll
         for (int b = 0; b < XW; ++b)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *)(st + (wave + 4 * b) * 64), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void *)(st + (wave + NW * b) * 64), 16,
                                                      int(in_k ? xbase + kb + b * bstride : kMasked), 0, 0, 0);
 #pragma unroll
         for (int b = 0; b < WW; ++b)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void *)(st + (XB + wave + 4 * b) * 64), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void *)(st + (XB + wave + NW * b) * 64), 16,
                                                      int(in_k ? wbase + kb + b * bstride : kMasked), 0, 0, 0);
     };
 
@@ -209,7 +212,7 @@ __global__ void __launch_bounds__(kThreads) gemmKernel(GemmParams p) {
     for (int s = 0; s < kStages - 1; ++s) issue(s);
     // Fragment reads: lane reads row l % 16 of a 16-row block, piece l / 16.
     const int fr = lane & 15, fslot = slotOf(fr, lane >> 4);
-    const int xblk0 = wm * (BM / 32), wblk0 = XB + wn * (BN / 32);
+    const int xblk0 = wm * TM, wblk0 = XB + wn * TN;
     for (int kt = 0; kt < nk; ++kt) {
         // Stage kt has landed once at most kStages - 2 stages of this wave's
         // loads are still in flight; the barrier then covers every wave's.
@@ -253,11 +256,11 @@ __global__ void __launch_bounds__(kThreads) gemmKernel(GemmParams p) {
         float *part = p.part + size_t(split) * p.M * p.N;
 #pragma unroll
         for (int j = 0; j < TM; ++j) {
-            const int m = m0 + wm * (BM / 2) + 16 * j + fr;
+            const int m = m0 + wm * (BM / WGM) + 16 * j + fr;
             if (m >= p.M) continue;
 #pragma unroll
             for (int i = 0; i < TN; ++i) {
-                const int n = n0 + wn * (BN / 2) + 16 * i + 4 * fg;
+                const int n = n0 + wn * (BN / WGN) + 16 * i + 4 * fg;
                 if (n >= p.N) continue;
                 const size_t base = size_t(m) * p.N + n;
                 if (vec) {
@@ -273,11 +276,11 @@ __global__ void __launch_bounds__(kThreads) gemmKernel(GemmParams p) {
     }
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
-        const int m = m0 + wm * (BM / 2) + 16 * j + fr;
+        const int m = m0 + wm * (BM / WGM) + 16 * j + fr;
         if (m >= p.M) continue;
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
-            const int n = n0 + wn * (BN / 2) + 16 * i + 4 * fg;
+            const int n = n0 + wn * (BN / WGN) + 16 * i + 4 * fg;
             if (n >= p.N) continue;
             const size_t base = size_t(m) * p.N + n;
             f32x4 v = acc[i][j];
@@ -351,15 +354,16 @@ int cusOf() {
     return cache[dev];
 }
 
-template <ElemType T, int BM, int BN> void launchTile(GemmParams p, hipStream_t s) {
+template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2> void launchTile(GemmParams p, hipStream_t s) {
     const size_t lds = size_t(kStages) * (BM + BN) * kRowBytes;
     static bool attr = [] {
-        HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN>),
+        HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(kStages * (BM + BN) * kRowBytes)));
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL((gemmKernel<T, BM, BN>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)), dim3(kThreads), lds, s,
+    hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
+                       dim3(64 * WGM * WGN), lds, s,
                        p);
 }
 
@@ -372,15 +376,20 @@ struct Plan {
     int tile = 0; // index into kTiles
     int mtiles = 0, ntiles = 0, splits = 1;
 };
+// eff: MFMA rate relative to the 128 x 256 tile, from timings of the kernel
+// on the config shapes (the 8-wave 256 x 256 tile runs ~1.2x faster).
 struct TileShape { int bm, bn, per_cu; double eff; };
-constexpr TileShape kTiles[] = {{128, 256, 1, 1.0}, {256, 128, 1, 1.0}, {128, 128, 2, 0.8}, {64, 64, 4, 0.45}};
+constexpr TileShape kTiles[] = {{128, 256, 1, 1.0}, {256, 128, 1, 1.0}, {128, 128, 2, 0.8}, {64, 64, 4, 0.45},
+                                 {256, 256, 1, 1.2}};
 constexpr int kMinSplitTiles = 8;
 
 Plan planGemm(ElemType t, int M, int N, int K) {
     const long cus = cusOf();
     Plan best;
     double best_t = 1e300;
-    for (int i = 0; i < 4; ++i) {
+    // LLAISYS_GEMM_BIG=0 leaves out the 256 x 256 tile (8 waves of 128 x 64).
+    static const int ntiles = [] { const char *e = std::getenv("LLAISYS_GEMM_BIG"); return e && e[0] == '0' ? 4 : 5; }();
+    for (int i = 0; i < (t == ElemType::F32 ? 4 : ntiles); ++i) { // f32: 128 accumulators at most
         const TileShape &c = kTiles[i];
         const long tiles = long((M + c.bm - 1) / c.bm) * long((N + c.bn - 1) / c.bn);
         const long rounds = (tiles + cus * c.per_cu - 1) / (cus * c.per_cu);
@@ -398,14 +407,34 @@ Plan planGemm(ElemType t, int M, int N, int K) {
     return best;
 }
 
+// 128 x 256 and 256 x 128 tiles with 8 waves (two per SIMD, 64 x 64 each)
+// unless LLAISYS_GEMM_W8=0 (4 waves of 64 x 128): the second wave of a SIMD
+// runs its MFMAs while the first waits on its fragment reads.
+bool w8() {
+    static const bool v = [] { const char *e = std::getenv("LLAISYS_GEMM_W8"); return !(e && e[0] == '0'); }();
+    return v;
+}
+
 template <ElemType T> void launchGemm(GemmParams p, const Plan &plan, hipStream_t s) {
     p.mtiles = plan.mtiles;
     p.ntiles = plan.ntiles;
     p.splits = plan.splits;
     switch (plan.tile) {
-    case 0: launchTile<T, 128, 256>(p, s); break;
-    case 1: launchTile<T, 256, 128>(p, s); break;
+    case 0:
+        if (w8()) launchTile<T, 128, 256, 2, 4>(p, s);
+        else launchTile<T, 128, 256>(p, s);
+        break;
+    case 1:
+        if (w8()) launchTile<T, 256, 128, 4, 2>(p, s);
+        else launchTile<T, 256, 128>(p, s);
+        break;
     case 2: launchTile<T, 128, 128>(p, s); break;
+    case 4:
+        if constexpr (T != ElemType::F32) {
+            launchTile<T, 256, 256, 2, 4>(p, s);
+            break;
+        }
+        [[fallthrough]];
     default: launchTile<T, 64, 64>(p, s); break;
     }
     HIP_CHECK(hipGetLastError());
