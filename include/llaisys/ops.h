@@ -44,7 +44,8 @@ __C {
     /* ops.h:9: out[i] = weight[index[i]], index I64 (README.md:171-177). */
     __export void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index, llaisysTensor_t weight);
     /* ops.h:10: out = in . weight^T + bias, weight [out, in], bias may be NULL
-     * (README.md:181-198); rocBLAS GEMM, fp32 accumulation. */
+     * (README.md:181-198); a hand-written MFMA GEMM, fp32 accumulation,
+     * one rounding; no GEMM library is linked. */
     __export void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, llaisysTensor_t bias);
     /* New; no counterpart in the reference (whose linear is ops.h:10). The
      * weight of llaisysLinear, rewritten once into the layout the decode GEMM

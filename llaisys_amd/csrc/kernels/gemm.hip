@@ -13,14 +13,17 @@
 //    so the sum is over the same products.
 //
 // A workgroup of 4 or 8 waves (2 x 2, 2 x 4 or 4 x 2) owns a BM x BN tile
-// of Y; each wave one sub-tile of it (64 x 64 to 128 x 64). K advances in tiles of 128 B per row (64
-// 16-bit or 32 f32 elements): every thread loads its 16 B pieces of the next
-// k tile of X and W into registers by buffer loads (out-of-range rows and k
-// come back as zeros, so edge tiles need no other guard), the waves run the
-// current tile's MFMAs from LDS, then the registers go to the other LDS
-// buffer and one barrier closes the tile. In LDS a row is 8 pieces of 16 B,
-// piece c of row r kept at slot c ^ (r % 8): the 16 rows one fragment read
-// touches at one piece column land in 8 different bank groups.
+// of Y; each wave one sub-tile of it (64 x 64 to 128 x 64). K advances in
+// tiles of 64 B per row (32 16-bit or 16 f32 elements) through a 4-stage LDS
+// ring: each wave moves whole 16-row blocks of X and W straight from global
+// memory into LDS by 16 B global_load_lds (buffer loads: out-of-range rows
+// and k come back as zeros, so edge tiles need no other guard), two stages
+// stay in flight while the waves run the current stage's MFMAs, and one
+// barrier per k tile both publishes a stage and frees the slot the next
+// issue refills. In LDS, piece c of row r sits at slot c ^ ((r / 4) % 4), so
+// a fragment read is free of bank conflicts. Shapes that leave CUs idle
+// split K over workgroups into fp32 partials that a second kernel sums in
+// split order (deterministic) before the single rounding.
 //
 // W is the MFMA's A operand and X its B operand, so a lane's accumulator
 // holds 4 consecutive columns n of one row m of Y: one 8 B (16-bit) or 16 B
@@ -181,7 +184,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
 
     // Lane's piece of a block: row lr = lane / 4 of the block, global piece lc.
     const int lr = lane >> 2, lc = (lane & 3) ^ ((lane >> 4) & 3);
-    // Block b of the wave is block wave + 4 b of the operand (rows 16 (wave + 4 b) ..).
+    // Block b of the wave is block wave + NW b of the operand (rows 16 (wave + NW b) ..).
     const uint32_t xbase = uint32_t(m0 + 16 * wave + lr) * row_bytes + 16 * lc;
     const uint32_t wbase = uint32_t(n0 + 16 * wave + lr) * row_bytes + 16 * lc;
     const uint32_t bstride = 16u * NW * row_bytes; // NW blocks of 16 rows

@@ -127,8 +127,7 @@ Qwen2Model::~Qwen2Model() {
 // kernels, same arguments, the per-step indices read from the same device
 // buffers. A graph is (re)captured when the table width, any workspace buffer
 // or the runtime's split workspace moved; the step that captures runs eagerly
-// first (so library GEMM tuning and workspace growth happen outside the
-// capture) and its results are the eager ones.
+// first (so workspace growth happens outside the capture) and its results are the eager ones.
 Qwen2Model::DecodeGraph Qwen2Model::capture(const std::function<void()> &work, size_t width) {
     auto &rt = core::context().runtime();
     auto s = static_cast<hipStream_t>(rt.stream());
@@ -423,7 +422,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
         if (!valid) {
             if (g.exec) HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(g.exec)));
             g.exec = nullptr;
-            oneStep(); // eager: library tuning and workspace growth stay outside the capture
+            oneStep(); // eager: workspace growth stays outside the capture
             done = 1;
             g = capture(oneStep, width);
         }
@@ -602,13 +601,12 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     }
 }
 
-// Largest M at which the decode GEMM beats the library GEMM for a weight of
-// N rows (K = 1536, weights cold in HBM, MI355X; bench-measured): the LM head
+// Largest M at which the decode GEMM over packed weights takes a projection
+// of N rows (K = 1536) instead of the general MFMA GEMM (linear): the LM head
 // (N = 151936) at every M <= 128, gate-up (N = 17920) up to 96, qkv and o
-// (N = 2048, 1536) up to 64, where the library's own launches win on latency.
-// Measured in the graph-replayed config-5 step (M = 128), the library's
-// autotuned kernels still win for qkv, o and gate-up: 3.55 ms per step with
-// these limits, 3.75 ms with qkv and o at 128, 3.86 ms with all at 128.
+// (N = 2048, 1536) up to 64. The limits were measured on MI355X with weights
+// cold in HBM; config-5 decode steps (M = 128) take the packed-operand
+// kernels instead (packedXGemm, qkvRopeGemm, gateUpSwiglu).
 namespace {
 int decodeGemmMaxM(int N) { return N >= 65536 ? 128 : N >= 8192 ? 96 : 64; }
 
@@ -624,9 +622,9 @@ void Qwen2Model::project(const tensor_t &y, const tensor_t &x, const tensor_t &w
         K::decodeGemm(u16(y), u16(x), u16(packed), M, N, K, accumulate, s);
         return;
     }
-    // Long K (the down projection): the split-K kernel beats the library at
-    // every M <= 128 (weights cold, MI355X: 11.5 vs 19.3 us at M = 1, 19.5
-    // vs 22.5 us autotuned at M = 128).
+    // Long K (the down projection): the split-K kernel over packed weights at
+    // every M <= 128 (weights cold, MI355X: 11.5 us at M = 1, 19.5 us at
+    // M = 128, GEMM + reduce).
     if (packed && K::splitKGemmSupported(M, N, K)) {
         auto *part = static_cast<float *>(core::context().runtime().scratch(K::splitKWorkspaceBytes(M, N, K)));
         K::splitKGemm(u16(y), u16(x), u16(packed), M, N, K, accumulate, part, s, y_packed);

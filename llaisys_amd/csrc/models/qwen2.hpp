@@ -92,8 +92,8 @@ private:
     // their folded copies were made (a check of version counters per step).
     void ensureFolded();
     // Y[M, N] (+)= X W^T: the hand-written decode GEMM over `packed` when it
-    // exists and M is at most the size where it beats the library for this N,
-    // else the library GEMM over the row-major `w`. y_packed: also write Y in
+    // exists and M is at most the size where it wins for this N, else the
+    // general MFMA GEMM (linear) over the row-major `w`. y_packed: also write Y in
     // operand order (only the split-K path can; the caller checks it is taken).
     void project(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &packed, int M, int N, int K,
                  bool accumulate, void *s, uint16_t *y_packed = nullptr) const;
@@ -111,7 +111,7 @@ private:
     tensor_t in_embed_, out_embed_, out_norm_;
     tensor_t out_embed_p_; // packed LM head for the decode GEMM (null when the shape does not qualify)
     uint64_t out_embed_packed_from_ = ~0ull;
-    bool decode_gemm_ = true; // LLAISYS_DECODE_GEMM=0: library GEMMs only
+    bool decode_gemm_ = true; // LLAISYS_DECODE_GEMM=0: the general GEMM only
     std::vector<Qwen2LayerWeights> layers_;
     std::vector<tensor_t> k_pool_, v_pool_;
 
@@ -150,7 +150,7 @@ private:
     // Decode steps on that path (M <= 128, K = 1536) run the qkv and o
     // projections with both operands packed: the embedding, the split-K
     // reduce and the attention write packed copies of their rows.
-    // LLAISYS_PACKED_X=0 keeps the library GEMMs there.
+    // LLAISYS_PACKED_X=0 keeps row-major X there (project()).
     bool packed_x_ = true;
     // On that path the QKV epilogue (bias, 1/rms, RoPE, k/v append) runs in
     // the QKV projection's epilogue, and the attention reads q

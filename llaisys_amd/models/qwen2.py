@@ -245,10 +245,9 @@ class Qwen2:
 
     def warm_up(self, max_tokens: int = 256):
         """Run one throwaway step of b single-token sequences for b = 1, 2, 4,
-        ... up to max_tokens (and the free blocks), so the library tunes its
-        GEMM kernel for every token-count bucket of decode-sized steps (and of
-        the LM head) before serving, instead of inside the first step that
-        meets each bucket."""
+        ... up to max_tokens (and the free blocks), so the step workspaces
+        reach their serving sizes before serving, instead of growing inside
+        the first step that meets each size."""
         b = 1
         while b <= min(max_tokens, self.num_free_blocks()):
             ids = [self.create_sequence()[0] for _ in range(b)]

@@ -101,7 +101,7 @@ def test_linear(shapes, use_bias, dtype, atol, rtol):
     ref = torch.matmul(x.double(), w.double().T)
     if use_bias:
         ref += b.double()
-    # f32 through rocBLAS accumulates in fp32: K=4096 sums of |x w| <= 1e-3 each
+    # f32 through the MFMA GEMM accumulates in fp32: K=4096 sums of |x w| <= 1e-3 each
     close(to_torch(out), ref.to(dtype), atol, rtol)
 
 
