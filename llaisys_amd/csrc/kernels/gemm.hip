@@ -14,13 +14,14 @@
 //
 // A workgroup of 4 or 8 waves (2 x 2, 2 x 4 or 4 x 2) owns a BM x BN tile
 // of Y; each wave one sub-tile of it (64 x 64 to 128 x 64). K advances in
-// tiles of 64 B per row (32 16-bit or 16 f32 elements) through a 4-stage LDS
+// tiles of 64 B per row (32 16-bit or 16 f32 elements) through a 5-stage LDS
 // ring: each wave moves whole 16-row blocks of X and W straight from global
 // memory into LDS by 16 B global_load_lds (buffer loads: out-of-range rows
 // and k come back as zeros, so edge tiles need no other guard), two stages
-// stay in flight while the waves run the current stage's MFMAs, and one
-// barrier per k tile both publishes a stage and frees the slot the next
-// issue refills. In LDS, piece c of row r sits at slot c ^ ((r / 4) % 4), so
+// stay in flight beyond the next one, and one barrier per k tile both
+// publishes a stage and frees the slot the next issue refills. Each wave
+// reads the next stage's fragments from LDS while the current stage's
+// MFMAs run (two register sets, reads spread between the MFMAs). In LDS, piece c of row r sits at slot c ^ ((r / 4) % 4), so
 // a fragment read is free of bank conflicts. Shapes that leave CUs idle
 // split K over workgroups into fp32 partials that a second kernel sums in
 // split order (deterministic) before the single rounding.
@@ -57,7 +58,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kXcds = 8;
 constexpr int kGroupN = 4;             // column tiles per m-fastest group
 constexpr int kRowBytes = 64;          // bytes of one row per k tile (one 32-k MFMA step of 16-bit data)
-constexpr int kStages = 4;             // k tiles in the LDS ring
 constexpr int kThreads = 256;
 constexpr uint32_t kRsrcWord3 = 0x00020000u; // raw buffer, 32-bit dwords (gfx9 family)
 constexpr uint32_t kMasked = 0x80000000u;    // an offset past any buffer: the load returns 0
@@ -151,9 +151,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 // 4-bank groups. Lane i therefore fetches piece (i % 4) ^ ((i / 16) % 4).
 __device__ __forceinline__ int slotOf(int r, int c) { return c ^ ((r >> 2) & 3); }
 
+// Stages of the LDS ring: 4, or 5 when the fragments of the next k tile
+// are read from LDS while the current tile's MFMAs run (PIPE).
+template <bool PIPE> constexpr int ringStages() { return PIPE ? 5 : 4; }
+
 // WGM x WGN waves, wave (wm, wn) owning the (BM / WGM) x (BN / WGN) sub-tile.
-template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2>
+template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2, bool PIPE = false>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
+    constexpr int NS = ringStages<PIPE>();
     constexpr int NW = WGM * WGN;
     constexpr int ES = Elem<T>::size;
     constexpr int KT = kRowBytes / ES;              // elements per k tile
@@ -163,7 +168,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
     constexpr int STAGE = (BM + BN) * kRowBytes / 16; // u32x4 per stage
     constexpr int kLoadsPerStage = XW + WW;          // per wave
     static_assert(XB % NW == 0 && WB % NW == 0, "each wave issues whole blocks");
-    extern __shared__ u32x4 lds[];                   // [kStages][X blocks | W blocks]
+    extern __shared__ u32x4 lds[];                   // [NS][X blocks | W blocks]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -192,7 +197,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
     const int kt0 = split * nk_all / p.splits;
     const int nk = (split + 1) * nk_all / p.splits - kt0;
     auto issue = [&](int kt) {
-        u32x4 *st = lds + (kt % kStages) * STAGE;
+        u32x4 *st = lds + (kt % NS) * STAGE;
         const uint32_t kb = uint32_t(kt0 + kt) * kRowBytes;
         const bool in_k = kt < nk && kb + 16 * lc < row_bytes;
 #pragma unroll
@@ -212,24 +217,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue(s);
+    for (int s = 0; s < NS - 1; ++s) issue(s);
     // Fragment reads: lane reads row l % 16 of a 16-row block, piece l / 16.
     const int fr = lane & 15, fslot = slotOf(fr, lane >> 4);
     const int xblk0 = wm * TM, wblk0 = XB + wn * TN;
-    for (int kt = 0; kt < nk; ++kt) {
-        // Stage kt has landed once at most kStages - 2 stages of this wave's
-        // loads are still in flight; the barrier then covers every wave's.
-        // (The compiler does not count global_load_lds against LDS reads.)
-        static_assert(kStages == 4, "the wait count below assumes 2 stages in flight");
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * kLoadsPerStage) : "memory");
-        // Slot (kt - 1) % kStages was read by every wave before this barrier.
-        issue(kt + kStages - 1);
-        const u32x4 *st = lds + (kt % kStages) * STAGE;
-        u32x4 a[TN], b[TM];
+    auto readFrags = [&](int kt, u32x4 (&a)[TN], u32x4 (&b)[TM]) {
+        const u32x4 *st = lds + (kt % NS) * STAGE;
 #pragma unroll
         for (int i = 0; i < TN; ++i) a[i] = st[(wblk0 + i) * 64 + fr * 4 + fslot];
 #pragma unroll
         for (int j = 0; j < TM; ++j) b[j] = st[(xblk0 + j) * 64 + fr * 4 + fslot];
+    };
+    auto mfmaTile = [&](const u32x4 (&a)[TN], const u32x4 (&b)[TM]) {
         if constexpr (T == ElemType::F32) {
             // element e of every piece, all tiles, then e + 1: dependent
             // MFMAs on one accumulator are TN x TM instructions apart
@@ -246,6 +245,56 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
             for (int i = 0; i < TN; ++i)
 #pragma unroll
                 for (int j = 0; j < TM; ++j) acc[i][j] = mfmaPiece<T>(a[i], b[j], acc[i][j]);
+        }
+    };
+    // (The compiler does not count global_load_lds against LDS reads, so
+    // the waits for the ring are explicit; the barrier after each makes
+    // every wave's part of a stage visible.)
+    if constexpr (PIPE) {
+        // Stage 0 has landed once at most NS - 2 stages are in flight.
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * kLoadsPerStage) : "memory");
+        // One k tile: wait for stage kt + 1, refill the slot of stage kt - 1,
+        // read stage kt + 1's fragments into (an, bn) while the MFMAs of
+        // stage kt run from (a, b). Two sets alternate (the loop below runs
+        // two steps per turn), so no fragment is copied between registers.
+        auto step = [&](int kt, const u32x4 (&a)[TN], const u32x4 (&b)[TM], u32x4 (&an)[TN], u32x4 (&bn)[TM]) {
+            // Stage kt + 1 has landed once at most NS - 3 stages are in
+            // flight; this wave's fragments of stage kt are in registers.
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 3) * kLoadsPerStage) : "memory");
+            // Slot (kt - 1) % NS was last read (fragments of stage kt - 1)
+            // before the previous barrier.
+            issue(kt + NS - 1);
+            readFrags(kt + 1, an, bn); // past the end: the zero-filled stages
+            mfmaTile(a, b);
+            // Spread the LDS reads over the MFMAs (left to itself the
+            // scheduler puts them all after the MFMAs, right before the
+            // next barrier, where nothing hides their latency).
+            constexpr int kReads = TN + TM;
+            constexpr int kMfmas = TN * TM * (T == ElemType::F32 ? 4 : 1);
+            constexpr int kPer = kMfmas / kReads > 0 ? kMfmas / kReads : 1;
+#pragma unroll
+            for (int g = 0; g < kReads; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // one LDS read
+                __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0); // then MFMAs
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kPer * kReads > 0 ? kMfmas - kPer * kReads : 0, 0);
+        };
+        u32x4 a0[TN], b0[TM], a1[TN], b1[TM];
+        readFrags(0, a0, b0);
+        for (int kt = 0; kt < nk; kt += 2) {
+            step(kt, a0, b0, a1, b1);
+            if (kt + 1 < nk) step(kt + 1, a1, b1, a0, b0);
+        }
+    } else {
+        for (int kt = 0; kt < nk; ++kt) {
+            // Stage kt has landed once at most NS - 2 stages of this wave's
+            // loads are still in flight; the barrier then covers every wave's.
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * kLoadsPerStage) : "memory");
+            // Slot (kt - 1) % NS was read by every wave before this barrier.
+            issue(kt + NS - 1);
+            u32x4 a[TN], b[TM];
+            readFrags(kt, a, b);
+            mfmaTile(a, b);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the trailing (zero) stages
@@ -357,17 +406,30 @@ int cusOf() {
     return cache[dev];
 }
 
-template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2> void launchTile(GemmParams p, hipStream_t s) {
-    const size_t lds = size_t(kStages) * (BM + BN) * kRowBytes;
-    static bool attr = [] {
-        HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(kStages * (BM + BN) * kRowBytes)));
+template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE> void launchTileAs(GemmParams p, hipStream_t s) {
+    const size_t lds = size_t(ringStages<PIPE>()) * (BM + BN) * kRowBytes;
+    static bool attr = [lds] {
+        HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN, PIPE>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
         return true;
     }();
     (void)attr;
-    hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
-                       dim3(64 * WGM * WGN), lds, s,
-                       p);
+    hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN, PIPE>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
+                       dim3(64 * WGM * WGN), lds, s, p);
+}
+
+// LLAISYS_GEMM_PIPE=0: the 4-stage ring whose waves read a stage's
+// fragments only after its barrier.
+bool pipelined() {
+    static const bool v = [] { const char *e = std::getenv("LLAISYS_GEMM_PIPE"); return !(e && e[0] == '0'); }();
+    return v;
+}
+
+template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2> void launchTile(GemmParams p, hipStream_t s) {
+    if (pipelined())
+        launchTileAs<T, BM, BN, WGM, WGN, true>(p, s);
+    else
+        launchTileAs<T, BM, BN, WGM, WGN, false>(p, s);
 }
 
 // The tile with the least estimated time: rounds of workgroups over the CUs
