@@ -125,6 +125,14 @@ int *Runtime::queueCounters() {
 }
 
 int Runtime::takeErrorFlags() {
+    const int pending = pending_error_flags_;
+    pending_error_flags_ = 0;
+    return pending | takeDeviceErrorFlags();
+}
+
+void Runtime::stashErrorFlags() { pending_error_flags_ |= takeDeviceErrorFlags(); }
+
+int Runtime::takeDeviceErrorFlags() {
     if (type_ == LLAISYS_DEVICE_CPU) return __atomic_exchange_n(&host_error_word_, 0, __ATOMIC_RELAXED);
     if (type_ != LLAISYS_DEVICE_AMD || !error_word_) return 0;
     int flags = 0;
@@ -135,16 +143,6 @@ int Runtime::takeErrorFlags() {
         api_->memcpy_sync(error_word_, &zero, sizeof(int), LLAISYS_MEMCPY_H2D);
     }
     return flags;
-}
-
-void Runtime::clearErrorFlagsAsync() {
-    if (type_ == LLAISYS_DEVICE_CPU) {
-        __atomic_store_n(&host_error_word_, 0, __ATOMIC_RELAXED);
-        return;
-    }
-    if (type_ != LLAISYS_DEVICE_AMD || !error_word_) return;
-    if (hipMemsetAsync(error_word_, 0, sizeof(int), static_cast<hipStream_t>(stream())) != hipSuccess)
-        LLAISYS_RAISE("hipMemsetAsync failed");
 }
 
 Context::Context() {

@@ -94,11 +94,14 @@ public:
     // Two int32 work-queue counters for persistent kernels, zeroed once; the
     // kernels return them to zero before they end.
     int *queueCounters();
+    // Bits raised since the last call (llaisysGetDeviceErrorFlags), then zero.
     int takeErrorFlags();
-    // Zero the error word in stream order, without waiting: a caller that
-    // checks its own launches' flags afterwards is not failed by bits an
-    // earlier, unrelated call left unread.
-    void clearErrorFlagsAsync();
+    // For callers that check their own launches' bits (the model): first move
+    // the bits raised so far into a host-side pending word (waits for the
+    // stream), then, after their launches, read and clear the device word
+    // alone. The pending bits stay for takeErrorFlags().
+    void stashErrorFlags();
+    int takeDeviceErrorFlags();
 
     void activate();
 
@@ -113,6 +116,7 @@ private:
     int *error_word_ = nullptr;
     int *queue_counters_ = nullptr;
     int host_error_word_ = 0;
+    int pending_error_flags_ = 0; // stashed by stashErrorFlags(), returned by takeErrorFlags()
     int *slot_hdr_ = nullptr;
     size_t slot_hdr_ints_ = 0;
     void *slot_rec_ = nullptr;

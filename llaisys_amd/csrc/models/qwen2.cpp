@@ -261,7 +261,7 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     ensureFolded();
     auto &rt = core::context().runtime();
-    rt.clearErrorFlagsAsync(); // this call's kernels alone decide its error check
+    rt.stashErrorFlags(); // earlier calls' bits stay for llaisysGetDeviceErrorFlags
     const size_t B = nseq;
     size_t T = 0;
     for (size_t i = 0; i < B; ++i) {
@@ -327,7 +327,7 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     int64_t *hnext = h64 + n64;
     api->memcpy_async(hnext, next_->data(), B * sizeof(int64_t), LLAISYS_MEMCPY_D2H, rt.stream());
     api->stream_synchronize(rt.stream());
-    const int flags = rt.takeErrorFlags();
+    const int flags = rt.takeDeviceErrorFlags(); // this call's kernels only
     LLAISYS_CHECK(flags == 0, "qwen2 step: kernels reported error flags " << flags);
     std::memcpy(next, hnext, B * sizeof(int64_t));
     last_B_ = B;
@@ -347,7 +347,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     ensureFolded();
     auto &rt = core::context().runtime();
-    rt.clearErrorFlagsAsync(); // this call's kernels alone decide its error check
+    rt.stashErrorFlags(); // earlier calls' bits stay for llaisysGetDeviceErrorFlags
     const size_t B = nseq;
     for (size_t i = 0; i < B; ++i) {
         LLAISYS_CHECK(size_t(blocks_.length(ids[i])) + nsteps <= cfg_.maxseq,
@@ -435,7 +435,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     int64_t *hout = h64 + 3 * B;
     api->memcpy_async(hout, history, nsteps * B * sizeof(int64_t), LLAISYS_MEMCPY_D2H, s);
     api->stream_synchronize(s);
-    const int flags = rt.takeErrorFlags();
+    const int flags = rt.takeDeviceErrorFlags(); // this call's kernels only
     LLAISYS_CHECK(flags == 0, "qwen2 decode: kernels reported error flags " << flags);
     std::memcpy(out, hout, nsteps * B * sizeof(int64_t));
     last_B_ = B;

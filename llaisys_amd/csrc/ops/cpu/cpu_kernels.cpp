@@ -372,37 +372,37 @@ void embedding(void *out, const int64_t *idx, const void *weight, ElemType t, si
     });
 }
 
+// Tiles of 4 rows x 4 output columns per task keep 16 accumulators in
+// registers and reuse each loaded X/W element 4 times. Elements are widened
+// as they are read, so no fp32 copy of the weight is made (an LM head's
+// would be ~1 GB).
+template <typename T> struct LinearOp {
+    static void run(void *out, const void *in, const void *weight, const void *bias, int M, int N, int K) {
+        const int mt = (M + 3) / 4, nt = (N + 3) / 4;
+        parallelFor(size_t(mt) * nt, 4, [&](size_t task) {
+            const int m0 = int(task / nt) * 4, n0 = int(task % nt) * 4;
+            float acc[4][4] = {};
+            const int mm = std::min(4, M - m0), nn = std::min(4, N - n0);
+            for (int k = 0; k < K; ++k) {
+                float xv[4], wv[4];
+                for (int i = 0; i < 4; ++i) xv[i] = i < mm ? Elem<T>::ld(in, size_t(m0 + i) * K + k) : 0.f;
+                for (int j = 0; j < 4; ++j) wv[j] = j < nn ? Elem<T>::ld(weight, size_t(n0 + j) * K + k) : 0.f;
+                for (int i = 0; i < 4; ++i)
+                    for (int j = 0; j < 4; ++j) acc[i][j] += xv[i] * wv[j];
+            }
+            for (int i = 0; i < mm; ++i)
+                for (int j = 0; j < nn; ++j) {
+                    float v = acc[i][j];
+                    if (bias) v += Elem<T>::ld(bias, n0 + j);
+                    Elem<T>::st(out, size_t(m0 + i) * N + n0 + j, v);
+                }
+        });
+    }
+};
+
 void linear(void *out, const void *in, const void *weight, const void *bias, ElemType t, int M, int N, int K) {
     if (M == 0 || N == 0) return;
-    std::vector<float> X(size_t(M) * K), W(size_t(N) * K);
-    widen(X.data(), in, t, X.size());
-    widen(W.data(), weight, t, W.size());
-    // Tiles of 4 rows x 4 output columns per task keep 16 accumulators in
-    // registers and reuse each loaded X/W row 4 times.
-    const int mt = (M + 3) / 4, nt = (N + 3) / 4;
-    parallelFor(size_t(mt) * nt, 4, [&](size_t task) {
-        const int m0 = int(task / nt) * 4, n0 = int(task % nt) * 4;
-        float acc[4][4] = {};
-        const int mm = std::min(4, M - m0), nn = std::min(4, N - n0);
-        for (int k = 0; k < K; ++k) {
-            float xv[4], wv[4];
-            for (int i = 0; i < 4; ++i) xv[i] = i < mm ? X[size_t(m0 + i) * K + k] : 0.f;
-            for (int j = 0; j < 4; ++j) wv[j] = j < nn ? W[size_t(n0 + j) * K + k] : 0.f;
-            for (int i = 0; i < 4; ++i)
-                for (int j = 0; j < 4; ++j) acc[i][j] += xv[i] * wv[j];
-        }
-        for (int i = 0; i < mm; ++i)
-            for (int j = 0; j < nn; ++j) {
-                float v = acc[i][j];
-                if (bias) v += ldAny(t, bias, n0 + j);
-                const size_t o = size_t(m0 + i) * N + n0 + j;
-                switch (t) {
-                case ElemType::F32: Elem<float>::st(out, o, v); break;
-                case ElemType::F16: Elem<F16>::st(out, o, v); break;
-                case ElemType::BF16: Elem<BF16>::st(out, o, v); break;
-                }
-            }
-    });
+    byType<LinearOp>(t, out, in, weight, bias, M, N, K);
 }
 
 void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *shape, const int64_t *out_strides,

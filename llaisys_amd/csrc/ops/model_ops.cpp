@@ -136,6 +136,15 @@ void linearPackWeight(const tensor_t &packed, const tensor_t &weight) {
     const int N = int(weight->shape()[0]), Kd = int(weight->shape()[1]);
     LLAISYS_CHECK(N % 16 == 0 && Kd % 32 == 0, op << ": needs N % 16 == 0 and K % 32 == 0");
     LLAISYS_CHECK(!onHost(op, {&packed, &weight}), op << ": AMD device tensors only");
+    LLAISYS_CHECK(packed->isContiguous() && weight->isContiguous(), op << ": contiguous tensors only");
+    {
+        // The kernel reads W while it writes the tiled copy: overlapping
+        // storage (e.g. packing in place) would corrupt both.
+        const auto *p = static_cast<const std::byte *>(packed->data());
+        const auto *w = static_cast<const std::byte *>(weight->data());
+        const size_t bytes = size_t(N) * size_t(Kd) * 2;
+        LLAISYS_CHECK(p + bytes <= w || w + bytes <= p, op << ": packed and weight must not overlap");
+    }
     K::packWeight(reinterpret_cast<uint16_t *>(packed->data()), reinterpret_cast<const uint16_t *>(weight->data()),
                   nullptr, N, Kd, stream());
 }

@@ -42,7 +42,11 @@ class Ops:
 
     @staticmethod
     def linear_packed(out: Tensor, inp: Tensor, packed: Tensor, bias: Tensor = None):
-        """linear with a packed weight, for decode-sized batches (M <= 128, K == 1536)."""
+        """out = inp . W^T + bias with W given packed by linear_pack_weight, for
+        decode-sized batches: bf16, M <= 128, and either K == 1536 or
+        1536 < K <= 16384 with N % 128 == 0 (split over K into fp32 partials
+        summed in a fixed order); the contract of llaisysLinearPacked in
+        include/llaisys/ops.h."""
         LIB_LLAISYS.llaisysLinearPacked(_h(out), _h(inp), _h(packed), _h(bias))
         check_last_error()
 

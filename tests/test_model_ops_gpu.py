@@ -248,6 +248,18 @@ def test_linear_packed_split_k(M, N, K, use_bias):
             assert torch.equal(first, got), "split-K result differs between identical calls"
 
 
+def test_linear_pack_weight_refuses_overlapping_storage():
+    # The pack kernel reads W while it writes the tiled copy: in place would
+    # corrupt both, so it is refused.
+    w = to_llaisys(torch.zeros(64, 1536, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(L.LlaisysError, match="overlap"):
+        L.Ops.linear_pack_weight(w, w)
+    with pytest.raises(L.LlaisysError, match="overlap"):
+        L.Ops.linear_pack_weight(w.slice(0, 16, 48), w.slice(0, 0, 32))
+    # disjoint halves of one allocation are fine
+    L.Ops.linear_pack_weight(w.slice(0, 32, 64), w.slice(0, 0, 32))
+
+
 def test_linear_packed_refuses_unsupported_shapes():
     x = to_llaisys(torch.zeros(129, 1536, dtype=torch.bfloat16, device=DEV))
     w = to_llaisys(torch.zeros(32, 1536, dtype=torch.bfloat16, device=DEV))

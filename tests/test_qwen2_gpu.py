@@ -527,7 +527,8 @@ def test_unfolded_norm_path_matches_transformers(monkeypatch):
 
 def test_stale_flags_of_an_earlier_op_do_not_fail_a_model_step():
     # A standalone paged op with a bad block id leaves error bit 1 unread; the
-    # next model step clears the word in stream order and succeeds.
+    # next model step judges only its own kernels' bits and succeeds, and the
+    # earlier bit is still there for device_error_flags() afterwards.
     from utils import to_llaisys
     model, hf = build("tiny")
     pool = to_llaisys(torch.zeros((2, 1, 16, 128), dtype=torch.bfloat16, device=DEV))
@@ -538,6 +539,8 @@ def test_stale_flags_of_an_earlier_op_do_not_fail_a_model_step():
     nxt = model.infer(toks)
     ref = hf_logits(hf, toks)[-1]
     check_token(nxt, ref, check_logits(to_torch(model.logits())[0], ref))
+    assert L.device_error_flags() == 1
+    assert L.device_error_flags() == 0
 
 
 def test_load_weight_refuses_a_source_of_another_shape():
