@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=None, help="timed steps (default: 200; qwen2: 64)")
     p.add_argument("--warmup", type=int, default=None, help="untimed steps (default: 20; qwen2: 4)")
-    p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy", "qwen2", "serve"])
+    p.add_argument("--workload", default="decode", choices=["decode", "mixed", "append_gather", "copy", "qwen2", "serve", "linear"])
     p.add_argument("--ag-fused-only", action="store_true",
                    help="--workload append_gather: time only the fused entry point (profiling runs)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
@@ -506,6 +506,54 @@ def run_mixed(args):
         "cpu_host_path": host,
         "roofline": {"bound": "mfma", "achieved": round(flops / (kern_ms * 1e-3) / 1e12, 3), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(flops / (kern_ms * 1e-3) / 1e12 / 2500.0, 4), "traffic": None},
+    }
+
+
+# The Qwen2-1.5B projections of prefill and mixed serving steps (M token rows):
+# qkv, o, gate-up, down.
+LINEAR_SHAPES = [(m, n, k) for m in (2048, 8192) for n, k in ((2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960))]
+
+
+def run_linear(args):
+    """llaisysLinear (the hand-written MFMA GEMM) on the model's prefill and
+    serving projection shapes, bf16, against torch.matmul (hipBLASLt) on the
+    same inputs and stream."""
+    import torch
+
+    import llaisys_amd as L
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from utils import to_llaisys
+
+    stream = torch.cuda.ExternalStream(L.context_stream())
+    rows, tot_flops, tot_ours, tot_torch = [], 0.0, 0.0, 0.0
+    steps, warmup = min(args.steps, 50), min(args.warmup, 5)
+    for m, n, k in LINEAR_SHAPES:
+        g = torch.Generator(device="cuda").manual_seed(args.seed + m + n + k)
+        x = (torch.randn(m, k, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+        w = (torch.randn(n, k, device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+        xl, wl = to_llaisys(x), to_llaisys(w)
+        out = to_llaisys(torch.zeros(m, n, dtype=torch.bfloat16, device="cuda"))
+        ours, _ = time_steps(lambda i: L.Ops.linear(out, xl, wl, None), stream, steps, warmup)
+        y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        with torch.cuda.stream(stream):
+            theirs, _ = time_steps(lambda i: torch.matmul(x, w.T, out=y), stream, steps, warmup)
+        flops = 2.0 * m * n * k
+        tot_flops, tot_ours, tot_torch = tot_flops + flops, tot_ours + ours, tot_torch + theirs
+        rows.append({"M": m, "N": n, "K": k, "us": round(ours * 1e3, 2), "TFLOP/s": round(flops / ours / 1e9, 1),
+                     "torch_us": round(theirs * 1e3, 2)})
+    assert L.device_error_flags() == 0
+    tf = tot_flops / (tot_ours * 1e-3) / 1e12
+    return {
+        "metric": "llaisysLinear bf16 TFLOP/s over the Qwen2-1.5B prefill/serving projection shapes, 1 GPU",
+        "value": round(tf, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(tot_ours, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) activations, N(0,0.05) weights)",
+        "config": {"workload": "llaisysLinear on M in {2048, 8192} x (qkv, o, gate-up, down) of Qwen2-1.5B"},
+        "torch_matmul_TFLOP/s": round(tot_flops / (tot_torch * 1e-3) / 1e12, 1),
+        "shapes": rows,
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tf / 2500.0, 4), "traffic": None},
     }
 
 
@@ -1107,7 +1155,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     line = {"decode": run_decode, "mixed": run_mixed, "append_gather": run_append_gather, "copy": run_copy,
-            "qwen2": run_qwen2, "serve": run_serve}[args.workload](args)
+            "qwen2": run_qwen2, "serve": run_serve, "linear": run_linear}[args.workload](args)
     print(json.dumps(line), flush=True)
 
 

@@ -432,43 +432,53 @@ template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2> void launchTile(
         launchTileAs<T, BM, BN, WGM, WGN, false>(p, s);
 }
 
-// The tile with the least estimated time: rounds of workgroups over the CUs
-// (workgroups per CU from the LDS ring) times a tile's MFMA work over its
-// relative efficiency (bigger wave tiles read less LDS per MFMA). A grid
-// that still leaves CUs idle splits K (at least kMinSplitTiles k tiles per
-// split) into fp32 partials that a second kernel sums in split order.
+// The (tile, K split) with the least estimated time. A launch runs
+// ceil(workgroups / CUs) rounds; a round costs a fixed kFixedUs (first loads,
+// epilogue) plus the tile's k loop, bm x bn x (K / split) at the tile's
+// relative MFMA rate eff (bigger wave tiles read less LDS per MFMA); a split
+// adds the reduce kernel, priced by its bytes (fp32 partials written and read
+// back, the output written). Fitted to timings of the kernel on MI355X
+// (bf16, M = 2048 / 8192 by the Qwen2 projection widths): e.g. 2048 x 2048 x
+// 1536 runs 21.0 us on 128 x 128 tiles against 29 us on 128 x 256 tiles split
+// in two, and 2048 x 1536 x 8960 85.8 us split in two against 93.5 us not.
 struct Plan {
     int tile = 0; // index into kTiles
     int mtiles = 0, ntiles = 0, splits = 1;
 };
-// eff: MFMA rate relative to the 128 x 256 tile, from timings of the kernel
-// on the config shapes (the 8-wave 256 x 256 tile runs ~1.2x faster).
-struct TileShape { int bm, bn, per_cu; double eff; };
-constexpr TileShape kTiles[] = {{128, 256, 1, 1.0}, {256, 128, 1, 1.0}, {128, 128, 2, 0.8}, {64, 64, 4, 0.45},
-                                 {256, 256, 1, 1.2}};
-constexpr int kMinSplitTiles = 8;
+struct TileShape { int bm, bn; double eff; };
+constexpr TileShape kTiles[] = {{128, 256, 1.0}, {256, 128, 1.0}, {128, 128, 0.8}, {64, 64, 0.45}, {256, 256, 1.2}};
+constexpr int kMinSplitTiles = 8;            // k tiles per split at least
+constexpr double kFixedUs = 6.0;             // per round of workgroups
+constexpr double kMacsPerUs = 2.1e6;         // bm * bn * k per us at eff 1 (bf16)
+constexpr double kReduceBytesPerUs = 5.0e6;  // HBM rate of the reduce kernel
+constexpr double kReduceLaunchUs = 2.0;
 
 Plan planGemm(ElemType t, int M, int N, int K) {
     const long cus = cusOf();
+    const int es = t == ElemType::F32 ? 4 : 2;
+    const int nk = (K * es + kRowBytes - 1) / kRowBytes;
     Plan best;
     double best_t = 1e300;
     // LLAISYS_GEMM_BIG=0 leaves out the 256 x 256 tile (8 waves of 128 x 64).
     static const int ntiles = [] { const char *e = std::getenv("LLAISYS_GEMM_BIG"); return e && e[0] == '0' ? 4 : 5; }();
     for (int i = 0; i < (t == ElemType::F32 ? 4 : ntiles); ++i) { // f32: 128 accumulators at most
         const TileShape &c = kTiles[i];
-        const long tiles = long((M + c.bm - 1) / c.bm) * long((N + c.bn - 1) / c.bn);
-        const long rounds = (tiles + cus * c.per_cu - 1) / (cus * c.per_cu);
-        const double tm = double(rounds) * c.per_cu * c.bm * c.bn / c.eff;
-        if (tm < best_t) {
-            best_t = tm;
-            best.tile = i;
-            best.mtiles = (M + c.bm - 1) / c.bm;
-            best.ntiles = (N + c.bn - 1) / c.bn;
+        const long mt = (M + c.bm - 1) / c.bm, nt = (N + c.bn - 1) / c.bn;
+        for (int sp = 1; sp <= 8; sp *= 2) {
+            if (sp > 1 && nk / sp < kMinSplitTiles) break;
+            const long rounds = (mt * nt * sp + cus - 1) / cus;
+            double tm = double(rounds) * (kFixedUs + double(c.bm) * c.bn * (double(K) / sp) / (c.eff * kMacsPerUs));
+            if (sp > 1)
+                tm += kReduceLaunchUs + (2.0 * sp * 4.0 + es) * double(M) * N / kReduceBytesPerUs;
+            if (tm < best_t) {
+                best_t = tm;
+                best.tile = i;
+                best.mtiles = int(mt);
+                best.ntiles = int(nt);
+                best.splits = sp;
+            }
         }
     }
-    const long tiles = long(best.mtiles) * best.ntiles;
-    const int nk = (K * (t == ElemType::F32 ? 4 : 2) + kRowBytes - 1) / kRowBytes;
-    if (tiles < cus) best.splits = int(std::max(1L, std::min(cus / tiles, long(nk / kMinSplitTiles))));
     return best;
 }
 
