@@ -63,6 +63,9 @@ def parse():
     p.add_argument("--summarize-mfma", nargs="+", metavar="DIR",
                    help="STATS_DIR UTIL_DIR MOPS_DIR [INSTS_DIR] TAG: per-kernel MFMA use from a kernel trace and "
                         "two (three) counter runs into profiles/TAG.md")
+    p.add_argument("--summarize-linear", nargs=3, metavar=("TRACE_DIR", "BENCH_LINE", "TAG"),
+                   help="kernel table of a --workload linear kernel trace (and the JSON line that run printed) "
+                        "into profiles/TAG.md")
     p.add_argument("--profiled-args", default="--no-cpu --no-model --steps 200",
                    help="bench arguments of the kernel-trace run")
     p.add_argument("--pmc-args", default="--no-cpu --no-model --steps 20 --warmup 5",
@@ -1120,6 +1123,52 @@ def summarize_mfma(args):
     (outdir / f"{tag}.md").write_text("\n".join(lines) + "\n")
 
 
+def summarize_linear(args):
+    """profiles/TAG.md from a kernel trace of `bench.py --workload linear`
+    (llaisysLinear's kernels and torch.matmul's hipBLASLt kernels) and the
+    JSON line the traced run printed."""
+    import csv
+    import re
+
+    trace_dir, line_file, tag = args.summarize_linear
+    stats = next(p for p in _csvs(trace_dir, "_kernel_stats.csv"))
+    rows = list(csv.DictReader(open(stats)))
+    line = next(json.loads(l) for l in open(line_file) if l.startswith('{"metric"'))
+    out = [f"# {tag}: llaisysLinear (hand-written MFMA GEMM) vs torch.matmul (rocprofv3 kernel trace)", "",
+           "Commands (from the repo root, on the MI355X box):", "", "```",
+           f"rocprofv3 --kernel-trace --stats --output-format csv -d {trace_dir} -o run -- python3 bench.py "
+           f"--workload linear > {line_file}",
+           f"python3 bench.py --summarize-linear {trace_dir} {line_file} {tag}", "```", "",
+           "`bench.py --workload linear` times `llaisysLinear` and then `torch.matmul` (hipBLASLt) on the same bf16",
+           "inputs for M in {2048, 8192} x the four Qwen2-1.5B projections (qkv 2048x1536, o 1536x1536, gate-up",
+           "17920x1536, down 1536x8960), 55 calls per shape each (5 warm-up + 50 timed).", "",
+           "## Kernel time (kernel trace, all shapes together)", "",
+           "| kernel | calls | avg us | share of trace |", "|---|---|---|---|"]
+    for r in rows:
+        name = r["Name"]
+        if "gemmKernel" in name:
+            short = "gemmKernel<bf16, " + name.split("ElemType)2, ")[1].split(">(")[0] + "> (this library)"
+        elif "gemmReduceKernel" in name:
+            short = "gemmReduceKernel (this library, split-K sum)"
+        elif "Cijk" in name:
+            mt = re.search(r"MT\d+x\d+x\d+", name)
+            short = "hipBLASLt " + (mt.group(0) if mt else name[:30]) + " (torch)"
+        else:
+            short = name.split("(")[0][:70]
+        out.append(f"| `{short}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} % |")
+    out += ["", "## The bench line of the traced run (HIP events)", "",
+            f"Aggregate over the eight shapes: **{line['value']} TFLOP/s** for llaisysLinear, "
+            f"{line['torch_matmul_TFLOP/s']} TFLOP/s for torch.matmul "
+            f"({line['value'] / line['torch_matmul_TFLOP/s'] * 100:.0f} %); roofline frac {line['roofline']['frac']} "
+            "of 2.5 PFLOP/s dense bf16. (The profiler slows the short torch calls more than ours.)", "",
+            "| M x N x K | llaisysLinear us | TFLOP/s | torch us |", "|---|---|---|---|"]
+    for r in line["shapes"]:
+        out.append(f"| {r['M']} x {r['N']} x {r['K']} | {r['us']} | {r['TFLOP/s']} | {r['torch_us']} |")
+    path = Path(args.profiles_dir) / f"{tag}.md"
+    path.write_text("\n".join(out) + "\n")
+    print(f"wrote {path}")
+
+
 def traffic_from_profiles(kernel_tag):
     """HBM bytes per launch measured by rocprofv3 PMC, if a summary is committed under profiles/."""
     f = ROOT / "profiles" / f"{kernel_tag}_traffic.json"
@@ -1144,6 +1193,9 @@ def main():
         return
     if args.summarize_mfma:
         summarize_mfma(args)
+        return
+    if args.summarize_linear:
+        summarize_linear(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the KV-cache path "
