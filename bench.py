@@ -66,6 +66,9 @@ def parse():
     p.add_argument("--summarize-linear", nargs=3, metavar=("TRACE_DIR", "BENCH_LINE", "TAG"),
                    help="kernel table of a --workload linear kernel trace (and the JSON line that run printed) "
                         "into profiles/TAG.md")
+    p.add_argument("--summarize-ag-modes", nargs=3, metavar=("TRACE_DIR", "BENCH_LINE", "TAG"),
+                   help="appendGatherKernel durations by timing mode from a kernel trace of --workload "
+                        "append_gather --ag-fused-only (and the JSON line that run printed) into profiles/TAG.md")
     p.add_argument("--profiled-args", default="--no-cpu --no-model --steps 200",
                    help="bench arguments of the kernel-trace run")
     p.add_argument("--pmc-args", default="--no-cpu --no-model --steps 20 --warmup 5",
@@ -1169,6 +1172,44 @@ def summarize_linear(args):
     print(f"wrote {path}")
 
 
+def summarize_ag_modes(args):
+    """profiles/TAG.md: appendGatherKernel's dispatches of one `bench.py
+    --workload append_gather --ag-fused-only` run, split by the bench's three
+    timing modes (they run in this order, warm-up + timed calls each)."""
+    import csv
+
+    trace_dir, line_file, tag = args.summarize_ag_modes
+    line = next(json.loads(l) for l in open(line_file) if l.startswith('{"metric"'))
+    steps, warmup = line["steps"], line["warmup"]
+    trace = next(p for p in _csvs(trace_dir, "_kernel_trace.csv"))
+    ev = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(open(trace))
+                if "appendGatherKernel" in r["Kernel_Name"])
+    assert len(ev) == 3 * (steps + warmup), f"expected {3 * (steps + warmup)} dispatches, found {len(ev)}"
+    modes = [f"back-to-back, rotating over copies of pools and outputs (the bench line's kernel_ms: "
+             f"{line['kernel_ms'] * 1e3:.2f} us)",
+             f"one call after an untimed 512 MiB read (single_call_flushed: "
+             f"{line['single_call_flushed']['kernel_ms'] * 1e3:.2f} us by HIP events)",
+             f"back-to-back on one copy, inputs MALL-resident (mall_resident: "
+             f"{line['mall_resident']['kernel_ms'] * 1e3:.2f} us by HIP events)"]
+    out = [f"# {tag}: kernel durations by timing mode (rocprofv3 kernel trace)", "",
+           "Commands (from the repo root, on the MI355X box):", "", "```",
+           f"rocprofv3 --kernel-trace --stats --output-format csv -d {trace_dir} -o run -- python3 bench.py "
+           f"--workload append_gather --no-cpu --ag-fused-only > {line_file}",
+           f"python3 bench.py --summarize-ag-modes {trace_dir} {line_file} {tag}", "```", "",
+           f"`bench.py --workload append_gather --ag-fused-only` times `appendGatherKernel` three ways, {warmup} warm-up "
+           f"+ {steps} calls each, in this order; the table splits the trace's {len(ev)} dispatches accordingly "
+           "(warm-up calls left out).", "", "| timing mode | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for i, mode in enumerate(modes):
+        d = [(e - s) / 1e3 for s, e in ev[i * (steps + warmup) + warmup:(i + 1) * (steps + warmup)]]
+        out.append(f"| {mode} | {len(d)} | {sum(d) / len(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
+    out += ["", f"Algorithmic bytes per call: {line['roofline']['algorithmic_bytes_per_launch'] / 1e6:.2f} MB. The rotated "
+            "calls are the line's value: a steady state in which no copy's data is still in the MALL when it is "
+            "reused. The flushed single call's HIP events also hold its launch and the event overhead."]
+    path = Path(args.profiles_dir) / f"{tag}.md"
+    path.write_text("\n".join(out) + "\n")
+    print(f"wrote {path}")
+
+
 def traffic_from_profiles(kernel_tag):
     """HBM bytes per launch measured by rocprofv3 PMC, if a summary is committed under profiles/."""
     f = ROOT / "profiles" / f"{kernel_tag}_traffic.json"
@@ -1196,6 +1237,9 @@ def main():
         return
     if args.summarize_linear:
         summarize_linear(args)
+        return
+    if args.summarize_ag_modes:
+        summarize_ag_modes(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: the KV-cache path "
