@@ -192,6 +192,29 @@ def test_linear_bf16_decode_batches(M, N, K, use_bias):
     assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
 
 
+# Prefill and serving shapes of the Qwen2-1.5B projections (M token rows), and
+# ragged ones: together they take every tile of the GEMM planner, with and
+# without a K split (fp32 partials summed by the reduce kernel).
+PREFILL = [(2048, 2048, 1536), (2048, 1536, 8960), (8192, 1536, 1536), (600, 17920, 1536), (600, 1536, 1536),
+           (1000, 2048, 1536), (333, 1536, 8960), (4099, 264, 1536), (2048, 17920, 1536)]
+
+
+@pytest.mark.parametrize("M,N,K", PREFILL, ids=[f"{m}x{n}x{k}" for m, n, k in PREFILL])
+def test_linear_bf16_prefill_shapes(M, N, K):
+    # Row-sampled float64 check (all columns of every 7th row and the last
+    # row): one bf16 rounding plus fp32 accumulation, bias included.
+    x, w = rnd((M, K), torch.bfloat16, 0.5, seed=M + N), rnd((N, K), torch.bfloat16, 0.05, seed=N + K)
+    b = rnd((N,), torch.bfloat16, seed=29)
+    out = to_llaisys(torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=DEV))
+    L.Ops.linear(out, to_llaisys(x), to_llaisys(w), to_llaisys(b))
+    rows = torch.cat([torch.arange(0, M, 7, device=DEV), torch.tensor([M - 1], device=DEV)])
+    xs = x[rows].double()
+    ref = xs @ w.double().T + b.double()
+    got = to_torch(out)[rows].double()
+    bound = ref.abs() * 2.0 ** -8 + 1e-6 * (xs.abs() @ w.double().abs().T) * K ** 0.5 + 1e-30
+    assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
+
+
 PACKED = [(1, 16), (7, 2048), (16, 1536), (33, 2048), (64, 4096), (100, 1536), (128, 2048), (128, 17920),
           (128, 1536), (120, 151936)]
 
