@@ -146,10 +146,16 @@ typedef __attribute__((address_space(3))) void lds_void;
 // One k tile of an operand is ROWS rows x 64 B (4 pieces of 16 B), kept in
 // LDS as blocks of 16 rows x 64 B: one 64-lane global_load_lds instruction
 // fills one block, lane i writing bytes 16 i .. 16 i + 15 of it (row i / 4,
-// slot i % 4). Piece c of row r sits at slot c ^ ((r / 4) % 4), so the 16
-// rows of an MFMA fragment read at one piece column fall on 16 different
-// 4-bank groups. Lane i therefore fetches piece (i % 4) ^ ((i / 16) % 4).
-__device__ __forceinline__ int slotOf(int r, int c) { return c ^ ((r >> 2) & 3); }
+// slot i % 4). Piece c of row r sits at slot c ^ key(r). A fragment read
+// (lane l: row l % 16, piece l / 16) serves 8 lanes per LDS cycle with 32
+// banks of 4 B (16 with 64): rows r and r + 2 start on the same banks, so
+// the key must differ across the rows of one parity within every 8 rows and
+// across the rows of one residue mod 4 within the 16: bit 1 = r2 ^ r3,
+// bit 0 = r1 ^ r3 does both. (The key (r / 4) % 4 left half of all LDS
+// cycles as bank conflicts: SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE 0.50.)
+// Lane i therefore fetches piece (i % 4) ^ key(i / 4).
+__device__ __forceinline__ int rowKey(int r) { return ((((r >> 2) ^ (r >> 3)) & 1) << 1) | (((r >> 1) ^ (r >> 3)) & 1); }
+__device__ __forceinline__ int slotOf(int r, int c) { return c ^ rowKey(r); }
 
 // Stages of the LDS ring: 4, or 5 when the fragments of the next k tile
 // are read from LDS while the current tile's MFMAs run (PIPE).
@@ -188,7 +194,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
     const uint32_t row_bytes = uint32_t(p.K) * ES;
 
     // Lane's piece of a block: row lr = lane / 4 of the block, global piece lc.
-    const int lr = lane >> 2, lc = (lane & 3) ^ ((lane >> 4) & 3);
+    const int lr = lane >> 2, lc = (lane & 3) ^ rowKey(lr);
     // Block b of the wave is block wave + NW b of the operand (rows 16 (wave + NW b) ..).
     const uint32_t xbase = uint32_t(m0 + 16 * wave + lr) * row_bytes + 16 * lc;
     const uint32_t wbase = uint32_t(n0 + 16 * wave + lr) * row_bytes + 16 * lc;
