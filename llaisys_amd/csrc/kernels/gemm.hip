@@ -542,10 +542,19 @@ int rowsPerLaunch(ElemType t, int M, int K) {
 
 } // namespace
 
+// The fp32 partials of the largest launch: rows go out in launches of
+// rowsPerLaunch rows and a last, shorter one, whose plan may split K where
+// the full launches' does not.
 size_t linearWorkspaceBytes(ElemType t, int M, int N, int K) {
     if (M <= 0 || N <= 0 || !tiled(t, K)) return 0;
-    const Plan plan = planGemm(t, rowsPerLaunch(t, M, K), N, K);
-    return plan.splits > 1 ? size_t(plan.splits) * rowsPerLaunch(t, M, K) * N * sizeof(float) : 0;
+    const int rpl = rowsPerLaunch(t, M, K);
+    size_t need = 0;
+    for (const int m : {rpl, M % rpl}) {
+        if (m <= 0) continue;
+        const Plan plan = planGemm(t, m, N, K);
+        if (plan.splits > 1) need = std::max(need, size_t(plan.splits) * size_t(m) * N * sizeof(float));
+    }
+    return need;
 }
 
 void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream,
