@@ -414,12 +414,20 @@ int cusOf() {
 
 template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE> void launchTileAs(GemmParams p, hipStream_t s) {
     const size_t lds = size_t(ringStages<PIPE>()) * (BM + BN) * kRowBytes;
-    static bool attr = [lds] {
-        HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN, PIPE>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
-        return true;
-    }();
-    (void)attr;
+    // The LDS limit is raised once per device the kernel runs on.
+    static std::mutex mu;
+    static std::vector<bool> raised;
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (size_t(dev) >= raised.size()) raised.resize(dev + 1, false);
+        if (!raised[dev]) {
+            HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN, PIPE>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+            raised[dev] = true;
+        }
+    }
     hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN, PIPE>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
                        dim3(64 * WGM * WGN), lds, s, p);
 }
