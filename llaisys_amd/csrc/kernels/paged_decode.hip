@@ -471,7 +471,7 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
 
 
 // Decode attention with one workgroup per (sequence, kv head) unit: its
-// kUnitWaves waves split the unit's page pairs evenly, stream them through a
+// kUnitWaves waves take the unit's page pairs in turn, stream them through a
 // register ring into the same MFMA step as the stream-K kernel, and merge
 // their (O, m, l) in LDS; wave 0 writes the normalised output. No records and
 // no second launch, no length scan: each workgroup reads its own length.
@@ -578,6 +578,23 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         vb = *reinterpret_cast<const uint32_t *>(r.bias + vcol + 2 * lane);
         xr.load(r.x ? r.x + size_t(b) * r.hs : prow, xd);
     };
+    // The waves take the unit's page pairs in turn: wave w owns pairs
+    // w, w + kUnitWaves, ... (its k-th pair is unit pair w + kUnitWaves k).
+    // So a wave's first block-table window does not depend on the length,
+    // and its loads go out beside the length's: the first pages wait for
+    // one memory round trip before them instead of two.
+    const int32_t *row = a.table + size_t(b) * a.max_pages;
+    // Window state: lane i holds the block ids of the wave's pair base + i
+    // (windows of up to 64 pairs), read clamped to the table row: entries
+    // past the sequence's pages are read but never used (the issue below
+    // selects page A for a missing page B, and clamps to the wave's count).
+    int base = 0, cnt = 0, bidA = 0, bidB = 0;
+    auto loadWindow = [&]() {
+        const int pa = 2 * (wave + kUnitWaves * (base + lane));
+        bidA = row[min(pa, a.max_pages - 1)];
+        bidB = row[min(pa + 1, a.max_pages - 1)];
+    };
+    if (!ROPE) loadWindow();
     int c = a.ctx[b];
     if (c < 1 || c > a.max_pages * 16) { // invalid length: zero output, error flag
         if (threadIdx.x == 0) atomicOr(a.err, kErrTooLong);
@@ -586,35 +603,28 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
     c = __builtin_amdgcn_readfirstlane(c);
     const int np = (c + 15) >> 4;
     const int npr = (np + 1) >> 1;
-    const int p0 = wave * npr / kUnitWaves, p1 = (wave + 1) * npr / kUnitWaves;
+    const int nw = npr > wave ? (npr - wave + kUnitWaves - 1) / kUnitWaves : 0; // this wave's pairs
+    cnt = min(kPairsPerWave, nw);
     Acc acc;
     acc.reset();
     bool bad_block = false;
     const u32x4 *kp = reinterpret_cast<const u32x4 *>(a.k_pool) + lane;
     const u32x4 *vp = reinterpret_cast<const u32x4 *>(a.v_pool) + lane;
-    const int32_t *row = a.table + size_t(b) * a.max_pages;
 
-    // Window state: lane i holds the block ids of pair base + i (windows of
-    // up to 64 pairs). Loads are never conditional: past the window's end
-    // they re-read its last pair (an L2 hit).
-    int base = p0, cnt = min(kPairsPerWave, p1 - p0), bidA = 0, bidB = 0;
-    auto loadWindow = [&]() { // (clamped reads of row[0] when the wave has no pairs)
-        const int pa = max(2 * (base + min(lane, cnt - 1)), 0);
-        bidA = row[pa];
-        bidB = row[max(min(pa + 1, np - 1), 0)];
-    };
     PagePair ring[NSTAGE];
+    // Pair k of the window into ring slot st (past the window's end its last
+    // pair again, an L2 hit, so loads are never conditional).
     auto issue = [&](int st, int k) {
         const int kk = max(min(k, cnt - 1), 0);
+        const int j = wave + kUnitWaves * (base + kk); // unit pair
         int bA = __builtin_amdgcn_readlane(bidA, kk);
-        int bB = __builtin_amdgcn_readlane(bidB, kk);
+        int bB = 2 * j + 1 < np ? __builtin_amdgcn_readlane(bidB, kk) : bA;
         const bool bad = unsigned(bA) >= unsigned(a.num_blocks) || unsigned(bB) >= unsigned(a.num_blocks);
         bad_block |= bad && cnt > 0; // a wave with no pairs loads a stand-in
         bA = bad ? 0 : bA;
         bB = bad ? 0 : bB;
         loadPair(ring[st], kp, vp, (size_t(bA) * a.nkvh + h) * 256, (size_t(bB) * a.nkvh + h) * 256);
     };
-    if (!ROPE && p1 > p0) loadWindow();
 
     u32x4 qop[4];
     // Fused epilogue (ROPE): the wave that holds the unit's last pair forms
@@ -623,7 +633,7 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
     // count in the same in-order counter as loads, so a store issued before
     // the loop would hold up the waits on every page issued after it.
     __shared__ __align__(16) uint16_t kflat[ROPE ? kHeadDim : 8], vflat[ROPE ? kHeadDim : 8];
-    const bool last_wave = ROPE && p1 > p0 && p1 == npr;
+    const bool last_wave = ROPE && nw > 0 && (npr - 1) % kUnitWaves == wave;
     const int tok = (c - 1) & 15;
     bool issued = false; // the first window's first stages already in flight
     float rs = 1.f;      // the row's 1/rms (ROPE)
@@ -694,9 +704,9 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
             qop[t4] = n < G ? qop[t4] : u32x4{0, 0, 0, 0};
         }
     }
-    for (; base < p1; base += kPairsPerWave) {
-        cnt = min(kPairsPerWave, p1 - base);
-        if (base != p0) loadWindow();
+    for (; base < nw; base += kPairsPerWave) {
+        cnt = min(kPairsPerWave, nw - base);
+        if (base != 0) loadWindow();
         if (!issued) {
 #pragma unroll
             for (int st = 0; st < NSTAGE; ++st) issue(st, st);
@@ -704,13 +714,13 @@ __global__ void __launch_bounds__(64 * kUnitWaves)
         issued = false;
         // The fused epilogue's last wave leaves the unit's last pair to the
         // tail below (the patch stays out of the loop's registers).
-        const int cnt_c = cnt - (last_wave && base + cnt == npr ? 1 : 0);
+        const int cnt_c = cnt - (last_wave && base + cnt == nw ? 1 : 0);
         for (int k0 = 0; k0 < cnt; k0 += NSTAGE) {
 #pragma unroll
             for (int st = 0; st < NSTAGE; ++st) {
                 const int k = k0 + st;
                 if (k < cnt_c) {
-                    const int j = base + k;
+                    const int j = wave + kUnitWaves * (base + k);
                     consumePair<OUT_F32>(acc, ring[st], qop, 32 * j, c - 1, c, 2 * j + 1 < np, grp, a.scale_log2);
                 }
                 issue(st, k + NSTAGE);
