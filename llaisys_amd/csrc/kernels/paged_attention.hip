@@ -518,7 +518,8 @@ __device__ __forceinline__ int lastAtMost(const int *v, int n, int x) {
 // round trips. Here every workgroup reads cu_q and ctx once and builds the
 // item tables in LDS (per sequence: unit and group prefix sums; per unit: its
 // split count and prefix of full splits; the units whose last split is
-// partial), then takes items from a device counter: all full (pps-page)
+// partial), then takes items (its first by its own index, the rest from a
+// device counter): all full (pps-page)
 // splits first in unit order, then the partial last splits, so the longest
 // items start earliest. The last workgroup to finish returns the counter and
 // the done count to zero for the next launch. Items are the old kernel's
@@ -585,17 +586,26 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // the number of valid sequences with a longer context, or as long and
     // listed earlier (deterministic, so every workgroup builds the same order;
     // O(B^2), so the host gives this kernel the decode items only for batches
-    // of at most kQueueSortSeqs sequences).
-    for (int b = tid; WITH_DECODE && b < B; b += nthreads) {
-        const int kb = dkey[b];
-        if (kb < 0) continue;
-        int rank = 0;
-        for (int o = 0; o < B; ++o) {
-            const int ko = dkey[o];
-            rank += (ko > kb || (ko == kb && o < b)) ? 1 : 0;
+    // of at most kQueueSortSeqs sequences). Wave w ranks sequences w,
+    // w + kWaves, ...: its lanes compare 64 others at a time and a ballot
+    // counts them (one loop over the batch per thread was 2 us of LDS
+    // latency at B = 64).
+    if constexpr (WITH_DECODE) {
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+        for (int b = wave; b < B; b += kWaves) {
+            const int kb = dkey[b];
+            if (kb < 0) continue;
+            int rank = 0;
+            for (int o0 = 0; o0 < B; o0 += 64) {
+                const int o = o0 + lane;
+                const int ko = o < B ? dkey[o] : -1;
+                rank += __popcll(__ballot(ko > kb || (ko == kb && o < b)));
+            }
+            if (lane == 0) {
+                dseq[rank] = b;
+                atomicAdd(&s_ndec, 1);
+            }
         }
-        dseq[rank] = b;
-        atomicAdd(&s_ndec, 1);
     }
     __syncthreads();
     const int n_dec_seqs = s_ndec;
@@ -628,10 +638,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         if (nspl[u] > fpre[u + 1] - fpre[u]) punit[ppos[u]] = u;
     __syncthreads();
     const int n_items = n_full + n_part + n_dec;
+    // Workgroup g's first item is item g; later ones come from the counter,
+    // past the grid.
     for (int it = 0;; ++it) {
-        if (tid == 0) s_item[it & 1] = atomicAdd(a.queue, 1);
+        if (it > 0 && tid == 0) s_item[it & 1] = int(gridDim.x) + atomicAdd(a.queue, 1);
         __syncthreads();
-        const int item = __builtin_amdgcn_readfirstlane(s_item[it & 1]);
+        const int item = it == 0 ? int(blockIdx.x) : __builtin_amdgcn_readfirstlane(s_item[it & 1]);
         if (item >= n_items) break;
         // Order: the full prefill splits, the single-query sequences' kv heads
         // (longest first), then the partial last splits.
