@@ -471,30 +471,37 @@ __device__ __forceinline__ void decodeItem(const Args &a, StageBuf &kvs, int b, 
     }
 }
 
-// Exclusive prefix sum of v[0..n) in place (n <= 64 * 64), by the whole
-// workgroup; returns the total. tmp: 65 ints of LDS. Barriers inside.
-__device__ int blockExclusiveScan(int *v, int n, int *tmp) {
+// Exclusive prefix sums of va[0..n) and vb[0..n) in place (n <= 64 * 64), in
+// one pass by the whole workgroup; the totals go to *total_a and *total_b.
+// tmp: 130 ints of LDS. Barriers inside.
+__device__ void blockExclusiveScan2(int *va, int *vb, int n, int *tmp, int *total_a, int *total_b) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nch = (n + 63) >> 6;
-    for (int ch = wave; ch < nch; ch += kWaves) {
-        const int i = ch * 64 + lane;
+    for (int ch = wave; ch < 2 * nch; ch += kWaves) {
+        const int which = ch >= nch ? 1 : 0, c = ch - which * nch;
+        int *v = which ? vb : va;
+        const int i = c * 64 + lane;
         const int x = i < n ? v[i] : 0;
         const int incl = waveInclusiveSum(x);
         if (i < n) v[i] = incl - x;
-        if (lane == 63) tmp[ch] = incl;
+        if (lane == 63) tmp[65 * which + c] = incl;
     }
     __syncthreads();
-    if (wave == 0) {
-        const int x = lane < nch ? tmp[lane] : 0;
+    if (wave < 2) {
+        int *t = tmp + 65 * wave;
+        const int x = lane < nch ? t[lane] : 0;
         const int incl = waveInclusiveSum(x);
-        if (lane < nch) tmp[lane] = incl - x;
-        if (lane == 63) tmp[64] = incl;
+        if (lane < nch) t[lane] = incl - x;
+        if (lane == 63) t[64] = incl;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 64 * kWaves) v[i] += tmp[i >> 6];
-    const int total = tmp[64];
+    for (int i = threadIdx.x; i < n; i += 64 * kWaves) {
+        va[i] += tmp[i >> 6];
+        vb[i] += tmp[65 + (i >> 6)];
+    }
+    *total_a = tmp[64];
+    *total_b = tmp[65 + 64];
     __syncthreads();
-    return total;
 }
 
 // Largest i in [0, n) with v[i] <= x, for non-decreasing v with v[0] <= x.
@@ -532,7 +539,7 @@ __device__ __forceinline__ int lastAtMost(const int *v, int n, int x) {
 // items and 4 us worse for prefill-only batches.)
 constexpr int kQueueMaxSeqs = 1024;
 constexpr int kQueueSortSeqs = 256; // decode items ranked by length up to this batch size
-constexpr int kQueueMaxUnits = 4000; // the unit scans (U + 1 entries) fit blockExclusiveScan
+constexpr int kQueueMaxUnits = 4000; // the unit scans (U + 1 entries) fit blockExclusiveScan2
 
 __host__ __device__ constexpr size_t queueTableInts(int B, int units) {
     return size_t(6) * (B + 1) + size_t(4) * (units + 1);
@@ -542,14 +549,13 @@ template <bool OUT_F32, bool WITH_DECODE>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
     prefillQueueKernel(Args a) {
     __shared__ StageBuf kvs;
-    __shared__ int scan_tmp[65];
+    __shared__ int scan_tmp[2 * 65];
     __shared__ int s_item[2];
     extern __shared__ int tables[];
     const int B = a.B, tid = threadIdx.x, nthreads = 64 * kWaves;
     int *cu = tables, *ctx = cu + (B + 1), *ubase = ctx + (B + 1), *gbase = ubase + (B + 1);
     int *nspl = gbase + (B + 1), *fpre = nspl + (a.block_units + 1), *ppos = fpre + (a.block_units + 1);
     int *punit = ppos + (a.block_units + 1), *dkey = punit + (a.block_units + 1), *dseq = dkey + (B + 1);
-    __shared__ int s_ndec;
     for (int i = tid; i <= B; i += nthreads) {
         cu[i] = a.cu_q[i];
         ctx[i] = i < B ? a.ctx[i] : 0;
@@ -579,38 +585,45 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         }
         if (b < B) dkey[b] = key;
     }
-    if (tid == 0) s_ndec = 0;
     __syncthreads();
-    blockExclusiveScan(gbase, B + 1, scan_tmp);
+    int U = 0, n_groups = 0;
+    blockExclusiveScan2(gbase, ubase, B + 1, scan_tmp, &n_groups, &U);
+    U = min(U, a.block_units);
     // Decode sequences longest first: dseq[rank] = b, the rank of b being
     // the number of valid sequences with a longer context, or as long and
     // listed earlier (deterministic, so every workgroup builds the same order;
     // O(B^2), so the host gives this kernel the decode items only for batches
-    // of at most kQueueSortSeqs sequences). Wave w ranks sequences w,
-    // w + kWaves, ...: its lanes compare 64 others at a time and a ballot
-    // counts them (one loop over the batch per thread was 2 us of LDS
-    // latency at B = 64).
+    // of at most kQueueSortSeqs sequences). Every wave holds all the keys,
+    // 64 per register; wave w ranks sequences w, w + kWaves, ..., a ballot
+    // per register counting those ahead (a loop over the batch in LDS per
+    // thread was 2 us of LDS latency at B = 64).
+    int n_dec_seqs = 0;
     if constexpr (WITH_DECODE) {
+        constexpr int kRegs = kQueueSortSeqs / 64;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+        int ko[kRegs];
+#pragma unroll
+        for (int r = 0; r < kRegs; ++r) {
+            const int o = 64 * r + lane;
+            ko[r] = o < B ? dkey[o] : -1;
+            n_dec_seqs += __popcll(__ballot(ko[r] >= 0));
+        }
         for (int b = wave; b < B; b += kWaves) {
-            const int kb = dkey[b];
+            int kb = ko[0];
+#pragma unroll
+            for (int r = 1; r < kRegs; ++r)
+                if ((b >> 6) == r) kb = ko[r];
+            kb = __builtin_amdgcn_readlane(kb, b & 63);
             if (kb < 0) continue;
             int rank = 0;
-            for (int o0 = 0; o0 < B; o0 += 64) {
-                const int o = o0 + lane;
-                const int ko = o < B ? dkey[o] : -1;
-                rank += __popcll(__ballot(ko > kb || (ko == kb && o < b)));
-            }
-            if (lane == 0) {
-                dseq[rank] = b;
-                atomicAdd(&s_ndec, 1);
-            }
+#pragma unroll
+            for (int r = 0; r < kRegs; ++r)
+                if (64 * r < B) rank += __popcll(__ballot(ko[r] > kb || (ko[r] == kb && 64 * r + lane < b)));
+            if (lane == 0) dseq[rank] = b;
         }
+        __syncthreads();
     }
-    __syncthreads();
-    const int n_dec_seqs = s_ndec;
     const int n_dec = n_dec_seqs * a.nkvh;
-    const int U = min(blockExclusiveScan(ubase, B + 1, scan_tmp), a.block_units);
     // Per unit: splits, full splits, partial flag.
     for (int u = tid; u <= U; u += nthreads) {
         int ns = 0, full = 0;
@@ -632,8 +645,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         ppos[u] = ns > full ? 1 : 0;
     }
     __syncthreads();
-    const int n_full = blockExclusiveScan(fpre, U + 1, scan_tmp);
-    const int n_part = blockExclusiveScan(ppos, U + 1, scan_tmp);
+    int n_full = 0, n_part = 0;
+    blockExclusiveScan2(fpre, ppos, U + 1, scan_tmp, &n_full, &n_part);
     for (int u = tid; u < U; u += nthreads)
         if (nspl[u] > fpre[u + 1] - fpre[u]) punit[ppos[u]] = u;
     __syncthreads();
