@@ -52,6 +52,12 @@ __C {
      * M <= 128; y_packed (may be NULL) also receives y packed. */
     __export void llaisysTestSplitKPackedGemm(void *y, const void *x_packed, const void *w_packed, int M, int N,
                                               int K, int accumulate, void *y_packed);
+    /* The long steps' gate-up: out[2 di, K] = the rows of w [gate (di); up
+     * (di)] as 16-row blocks gate 0, up 0, gate 1, ... (di % 16 == 0); then
+     * act[M, di] = up * silu(gate) of x[M, K] . out^T in one GEMM launch,
+     * gate and up rounded to bf16 before the SwiGLU (x row-major). */
+    __export void llaisysTestSwigluInterleave(void *out, const void *w, int di, int K);
+    __export void llaisysTestLinearSwiglu(void *act, const void *x, const void *w_interleaved, int M, int di, int K);
 }
 
 #endif

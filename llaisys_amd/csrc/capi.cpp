@@ -703,6 +703,16 @@ void llaisysTestGateUpSwiglu(void *act, const void *x_packed, const void *w_pack
     });
 }
 
+void llaisysTestSwigluInterleave(void *out, const void *w, int di, int K) {
+    testHook([&](void *s, auto &) { llaisys::kernels::swigluInterleave(w16(out), r16(w), di, K, s); });
+}
+
+void llaisysTestLinearSwiglu(void *act, const void *x, const void *w_interleaved, int M, int di, int K) {
+    testHook([&](void *s, auto &) {
+        llaisys::kernels::linearSwiglu(act, x, w_interleaved, llaisys::kernels::ElemType::BF16, M, di, K, s);
+    });
+}
+
 void llaisysTestSplitKPackedGemm(void *y, const void *x_packed, const void *w_packed, int M, int N, int K,
                                  int accumulate, void *y_packed) {
     testHook([&](void *s, auto &rt) {

@@ -125,6 +125,7 @@ struct GemmParams {
     uint32_t x_bytes, w_bytes; // buffer extents (range checks)
     int splits;                // > 1: K split over workgroups, fp32 partials part[split][M][N]
     float *part;
+    int swiglu; // y = act[M][N / 2]: W rows are gate and up blocks of 16 in turn (swigluInterleave)
 };
 
 // Tile index of workgroup b: XCD b % 8 takes tiles [(b % 8) T / 8, ...) in
@@ -332,6 +333,41 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
         }
         return;
     }
+    if constexpr (T == ElemType::BF16 && TN % 2 == 0) {
+        if (p.swiglu) {
+            // W fragments 2t and 2t + 1 of the wave are a gate block and its up
+            // block (the wave's columns start at a multiple of 32): the lane
+            // holds gate and up of the same four act columns. Both are rounded
+            // to bf16 first, as the GEMM output swigluRows would read.
+            const int da = p.N / 2;
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int m = m0 + wm * (BM / WGM) + 16 * j + fr;
+                if (m >= p.M) continue;
+#pragma unroll
+                for (int t = 0; t < TN / 2; ++t) {
+                    const int ng = n0 + wn * (BN / WGN) + 32 * t; // gate block 2 (ng / 32)
+                    if (ng >= p.N) continue;
+                    const int col = ng / 2 + 4 * fg;
+                    uint32_t w2[2];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        uint32_t pk = 0;
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const float g = float(__bf16(acc[2 * t][j][2 * h + e]));
+                            const float u = float(__bf16(acc[2 * t + 1][j][2 * h + e]));
+                            pk |= uint32_t(__builtin_bit_cast(uint16_t, __bf16(u * g / (1.f + expf(-g))))) << (16 * e);
+                        }
+                        w2[h] = pk;
+                    }
+                    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(p.y) + size_t(m) * da + col) =
+                        make_uint2(w2[0], w2[1]);
+                }
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
         const int m = m0 + wm * (BM / WGM) + 16 * j + fr;
@@ -467,7 +503,7 @@ constexpr double kMacsPerUs = 2.1e6;         // bm * bn * k per us at eff 1 (bf1
 constexpr double kReduceBytesPerUs = 5.0e6;  // HBM rate of the reduce kernel
 constexpr double kReduceLaunchUs = 2.0;
 
-Plan planGemm(ElemType t, int M, int N, int K) {
+Plan planGemm(ElemType t, int M, int N, int K, bool no_split = false) {
     const long cus = cusOf();
     const int es = t == ElemType::F32 ? 4 : 2;
     const int nk = (K * es + kRowBytes - 1) / kRowBytes;
@@ -479,7 +515,7 @@ Plan planGemm(ElemType t, int M, int N, int K) {
         const TileShape &c = kTiles[i];
         const long mt = (M + c.bm - 1) / c.bm, nt = (N + c.bn - 1) / c.bn;
         for (int sp = 1; sp <= 8; sp *= 2) {
-            if (sp > 1 && nk / sp < kMinSplitTiles) break;
+            if (sp > 1 && (no_split || nk / sp < kMinSplitTiles)) break;
             const long rounds = (mt * nt * sp + cus - 1) / cus;
             double tm = double(rounds) * (kFixedUs + double(c.bm) * c.bn * (double(K) / sp) / (c.eff * kMacsPerUs));
             if (sp > 1)
@@ -613,6 +649,37 @@ void linear(void *y, const void *x, const void *w, const void *bias, ElemType t,
         case ElemType::F16: launchGemm<ElemType::F16>(p, plan, s); break;
         case ElemType::F32: launchGemm<ElemType::F32>(p, plan, s); break;
         }
+    }
+}
+
+bool linearSwigluSupported(ElemType t, int M, int di, int K) {
+    return t == ElemType::BF16 && M > 0 && di > 0 && di % 16 == 0 && tiled(t, K) &&
+           size_t(2 * di) * size_t(K) * 2 < kMaxBufferBytes && size_t(K) * 2 < kMaxRowBytes;
+}
+
+void linearSwiglu(void *act, const void *x, const void *w_interleaved, ElemType t, int M, int di, int K,
+                  void *stream) {
+    LLAISYS_CHECK(linearSwigluSupported(t, M, di, K),
+                  "linearSwiglu: needs bf16, di % 16 == 0 and whole 16 B rows (M=" << M << " di=" << di << " K=" << K
+                                                                                   << ")");
+    auto s = static_cast<hipStream_t>(stream);
+    const int N = 2 * di;
+    const size_t row_bytes = size_t(K) * 2;
+    const int rows_per_launch = rowsPerLaunch(t, M, K);
+    for (int r0 = 0; r0 < M; r0 += rows_per_launch) {
+        const int m = std::min(rows_per_launch, M - r0);
+        const Plan plan = planGemm(t, m, N, K, true);
+        GemmParams p{};
+        p.y = static_cast<uint16_t *>(act) + size_t(r0) * di;
+        p.x = static_cast<const char *>(x) + size_t(r0) * row_bytes;
+        p.w = w_interleaved;
+        p.M = m;
+        p.N = N;
+        p.K = K;
+        p.x_bytes = uint32_t(size_t(m) * row_bytes);
+        p.w_bytes = uint32_t(size_t(N) * row_bytes);
+        p.swiglu = 1;
+        launchGemm<ElemType::BF16>(p, plan, s);
     }
 }
 

@@ -147,6 +147,13 @@ void rearrange(void *out, const void *in, size_t esz, int ndim, const int64_t *s
 size_t linearWorkspaceBytes(ElemType t, int M, int N, int K);
 void linear(void *y, const void *x, const void *w, const void *bias, ElemType t, int M, int N, int K, void *stream,
             bool accumulate, void *workspace);
+// act[M, di] = up * silu(gate) of X[M, K] . W^T, one launch: the same GEMM with
+// W = swigluInterleave's row order of a [gate (di) | up (di)] weight, gate and
+// up rounded to bf16 before the SwiGLU (bit for bit linear() + swigluRows()).
+// bf16, di % 16 == 0, K * 2 % 16 == 0; K is never split.
+bool linearSwigluSupported(ElemType t, int M, int di, int K);
+void linearSwiglu(void *act, const void *x, const void *w_interleaved, ElemType t, int M, int di, int K,
+                  void *stream);
 
 // ---- decode-sized projections (decode_gemm.hip), bf16
 // Y[M, N] (+)= X[M, K] . W[N, K]^T for M <= kDecodeGemmMaxM, K == kDecodeGemmK,
@@ -249,6 +256,9 @@ void swigluRows(uint16_t *act, const uint16_t *gate_up, const uint16_t *x, size_
 // out[r, c] = w[r, c] * g[c] (bf16, one rounding): an RMSNorm weight folded
 // into the columns of the projection that consumes the normalised rows.
 void foldNormColumns(uint16_t *out, const uint16_t *w, const uint16_t *g, size_t rows, int cols, void *stream);
+// out = the rows of w [gate (di) | up (di)] as 16-row blocks gate 0, up 0,
+// gate 1, up 1, ... (linearSwiglu's weight order); di % 16 == 0.
+void swigluInterleave(uint16_t *out, const uint16_t *w, int di, int cols, void *stream);
 // Multi-step decode bookkeeping on the device (s = *counter, the steps
 // started): before step s, history[s - 1][:] = next (s > 0), ctx_before =
 // base + s, ctx_after = base + s + 1, tok = s ? next : first, *counter = s + 1;

@@ -320,6 +320,19 @@ void foldNormColumns(uint16_t *out, const uint16_t *w, const uint16_t *g, size_t
     HIP_CHECK(hipGetLastError());
 }
 
+void swigluInterleave(uint16_t *out, const uint16_t *w, int di, int cols, void *stream) {
+    LLAISYS_CHECK(di % 16 == 0 && cols % 8 == 0,
+                  "swigluInterleave: di % 16 and cols % 8 must be 0 (di=" << di << ", cols=" << cols << ")");
+    const size_t row_bytes = size_t(cols) * 2;
+    // Block 2j <- gate rows 16j .., block 2j + 1 <- up rows 16j ..: one 2-D
+    // copy per half, rows of 16-row blocks strided by two blocks.
+    for (int half = 0; half < 2; ++half)
+        HIP_CHECK(hipMemcpy2DAsync(reinterpret_cast<char *>(out) + size_t(half) * 16 * row_bytes, 32 * row_bytes,
+                                   reinterpret_cast<const char *>(w) + size_t(half) * di * row_bytes, 16 * row_bytes,
+                                   16 * row_bytes, size_t(di / 16), hipMemcpyDeviceToDevice,
+                                   static_cast<hipStream_t>(stream)));
+}
+
 void rmsNormRows(uint16_t *out, const uint16_t *x, const int64_t *rows, const uint16_t *w, size_t R, int d, float eps,
                  void *stream) {
     LLAISYS_CHECK(d % 8 == 0 && d <= kRowMaxVecs * 64 * 8,

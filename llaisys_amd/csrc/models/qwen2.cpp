@@ -75,6 +75,8 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
     if (const char *e = std::getenv("LLAISYS_PACKED_X")) packed_x_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_QKV_GEMM_EPILOGUE")) qkv_gemm_epilogue_ = e[0] != '0';
     if (const char *e = std::getenv("LLAISYS_SPLITK_PACKED")) splitk_packed_ = e[0] != '0';
+    if (const char *e = std::getenv("LLAISYS_GEMM_SWIGLU")) gemm_swiglu_ = e[0] != '0';
+    gemm_swiglu_ = gemm_swiglu_ && K::linearSwigluSupported(K::ElemType::BF16, 1, int(cfg.di), int(cfg.hs));
     const auto dt = cfg.dtype;
     const size_t q = cfg.nh * cfg.dh, kv = cfg.nkvh * cfg.dh;
     in_embed_ = dev({cfg.voc, cfg.hs}, dt, dev_);
@@ -106,6 +108,7 @@ Qwen2Model::Qwen2Model(const Qwen2Config &cfg, int device_id, size_t num_blocks)
             L.qkv_wfp = dev({q + 2 * kv, cfg.hs}, dt, dev_);
             L.gate_up_wfp = dev({2 * cfg.di, cfg.hs}, dt, dev_);
         }
+        if (gemm_swiglu_) L.gate_up_wi = dev({2 * cfg.di, cfg.hs}, dt, dev_);
         if (decode_gemm_ && K::decodeGemmSupported(1, int(cfg.hs), int(q))) L.o_wp = dev({cfg.hs, q}, dt, dev_);
         if (decode_gemm_ && K::splitKGemmSupported(1, int(cfg.hs), int(cfg.di)))
             L.down_wp = dev({cfg.hs, cfg.di}, dt, dev_);
@@ -465,6 +468,10 @@ void Qwen2Model::ensureFolded() {
                           int(L.down_w->shape()[1]), s);
             L.down_packed_from = L.down_w->version();
         }
+        if (L.gate_up_wi && L.gate_up_w->version() != L.interleaved_from) {
+            K::swigluInterleave(u16(L.gate_up_wi), u16(L.gate_up_w), int(cfg_.di), int(cfg_.hs), s);
+            L.interleaved_from = L.gate_up_w->version();
+        }
     }
     if (!fold_norm_) return;
     for (auto &L : layers_) {
@@ -572,11 +579,17 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
                             down_px);
         } else {
             if (!fold) K::rmsNormRows(u16(h_), u16(x_), nullptr, u16(L.mlp_norm), T, hs, cfg_.epsilon, s);
-            const tensor_t gup = fold ? L.gate_up_wfp : tensor_t();
-            project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, gup, M, 2 * di, hs, false, s);
-            // The decode GEMM over the interleaved packed copy leaves gate
-            // and up columns interleaved as well.
-            K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s, takesDecodeGemm(gup, M, 2 * di, hs));
+            if (!fold && L.gate_up_wi) {
+                // The general GEMM with the SwiGLU in its epilogue.
+                K::linearSwiglu(act_->data(), h_->data(), L.gate_up_wi->data(), K::ElemType::BF16, M, di, hs, s);
+            } else {
+                const tensor_t gup = fold ? L.gate_up_wfp : tensor_t();
+                project(gu_, fold ? x_ : h_, fold ? L.gate_up_wf : L.gate_up_w, gup, M, 2 * di, hs, false, s);
+                // The decode GEMM over the interleaved packed copy leaves gate
+                // and up columns interleaved as well.
+                K::swigluRows(u16(act_), u16(gu_), xr, T, di, hs, cfg_.epsilon, s,
+                              takesDecodeGemm(gup, M, 2 * di, hs));
+            }
         }
         if (down_px) {
             auto *part = static_cast<float *>(rt.scratch(K::splitKPackedWorkspaceBytes(M, hs, di)));

@@ -46,6 +46,10 @@ struct Qwen2LayerWeights {
     // the shapes do not qualify.
     tensor_t qkv_wfp, gate_up_wfp, o_wp, down_wp;
     uint64_t o_packed_from = ~0ull, down_packed_from = ~0ull;
+    // gate_up_w in linearSwiglu's row order (gate and up blocks of 16 rows in
+    // turn) for the long steps' one-launch gate-up + SwiGLU; null when off.
+    tensor_t gate_up_wi;
+    uint64_t interleaved_from = ~0ull;
 };
 
 class Qwen2Model {
@@ -160,6 +164,9 @@ private:
     // packed, streamed through registers (fewer splits than the LDS-staged
     // split-K); LLAISYS_SPLITK_PACKED=0 keeps the LDS-staged kernel.
     bool splitk_packed_ = true;
+    // Steps whose gate-up runs the general GEMM: the SwiGLU in its epilogue
+    // over gate_up_wi (LLAISYS_GEMM_SWIGLU=0: the GEMM, then swigluRows).
+    bool gemm_swiglu_ = true;
     void chooseDecodeAttention(size_t B, int32_t min_ctx, int32_t max_ctx);
     uint64_t ws_gen_ = 0;     // bumped whenever a step workspace buffer moves
     std::map<size_t, DecodeGraph> graphs_;       // one step (step())

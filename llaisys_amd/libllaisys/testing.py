@@ -12,6 +12,8 @@ def load_testing(lib):
         ("llaisysTestQkvRopeGemm", [P, P, P, P, P, P, P, P, I, I, I, I, I, I, F, F]),
         ("llaisysTestGateUpSwiglu", [P, P, P, I, I, I, F, I]),
         ("llaisysTestSplitKPackedGemm", [P, P, P, I, I, I, I, P]),
+        ("llaisysTestSwigluInterleave", [P, P, I, I]),
+        ("llaisysTestLinearSwiglu", [P, P, P, I, I, I]),
     ]:
         fn = getattr(lib, name)
         fn.argtypes = args

@@ -110,6 +110,23 @@ def test_long_prefill_matches():
         toks = toks + [int(ref.argmax())]
 
 
+def test_long_prefill_fused_gate_up_swiglu(monkeypatch):
+    # 700 tokens in one step: past 512 rows the gate-up runs the general GEMM
+    # with the SwiGLU in its epilogue (LLAISYS_GEMM_SWIGLU, on by default):
+    # bit for bit the GEMM + swiglu launches (K = 256 is never split), and
+    # transformers' logits.
+    toks = prompt(700, 1000, 31)
+    outs = []
+    for v in ("0", "1"):
+        monkeypatch.setenv("LLAISYS_GEMM_SWIGLU", v)
+        model, hf = build("tiny")
+        nxt = model.infer(toks)
+        outs.append(to_torch(model.logits())[0].clone())
+    assert torch.equal(outs[0], outs[1])
+    ref = hf_logits(hf, toks)[-1]
+    check_token(nxt, ref, check_logits(outs[1], ref))
+
+
 @pytest.mark.parametrize("nseq", [100, 130])
 def test_wide_decode_batches_match(nseq):
     # 100 and 130 sequences in one decode batch: the GEMMs see M = 100 / 130
@@ -475,10 +492,13 @@ def test_warm_up_leaves_the_pool_free_and_the_model_correct():
     check_token(nxt, ref, check_logits(to_torch(model.logits())[0], ref))
 
 
-def test_rewritten_weights_reach_the_folded_projections():
+@pytest.mark.parametrize("fold", ["1", "0"])
+def test_rewritten_weights_reach_the_folded_projections(fold, monkeypatch):
     # The qkv and gate/up projections run on copies with the RMSNorm weight
-    # folded into their columns. Weights written after a step, by tensorLoad
+    # folded into their columns (fold "1"), or, unfolded, the gate-up on a copy
+    # in linearSwiglu's row order. Weights written after a step, by tensorLoad
     # or through a raw data pointer, must refresh those copies at the next step.
+    monkeypatch.setenv("LLAISYS_QWEN2_FOLD_NORM", fold)
     model, hf = build("tiny")
     toks = prompt(23, model.meta.voc, 5)
     model.infer(toks)
