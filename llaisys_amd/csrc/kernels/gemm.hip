@@ -158,9 +158,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ int rowKey(int r) { return ((((r >> 2) ^ (r >> 3)) & 1) << 1) | (((r >> 1) ^ (r >> 3)) & 1); }
 __device__ __forceinline__ int slotOf(int r, int c) { return c ^ rowKey(r); }
 
-// Stages of the LDS ring: 4, or 5 when the fragments of the next k tile
-// are read from LDS while the current tile's MFMAs run (PIPE).
-template <bool PIPE> constexpr int ringStages() { return PIPE ? 5 : 4; }
+// Stages of the LDS ring, also when the fragments of the next k tile are
+// read from LDS while the current tile's MFMAs run (PIPE): 4 (PIPE with 5
+// stages was 3-5 % slower, 3 stages slower again: 8192 x 17920 x 1536 486
+// against 503 and 497 us; more loads in flight per CU than it can stream).
+template <bool PIPE> constexpr int ringStages() { return 4; }
 
 // WGM x WGN waves, wave (wm, wn) owning the (BM / WGM) x (BN / WGN) sub-tile.
 template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2, bool PIPE = false>
