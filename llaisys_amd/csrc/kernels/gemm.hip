@@ -14,21 +14,23 @@
 //
 // A workgroup of 4 or 8 waves (2 x 2, 2 x 4 or 4 x 2) owns a BM x BN tile
 // of Y; each wave one sub-tile of it (64 x 64 to 128 x 64). K advances in
-// tiles of 64 B per row (32 16-bit or 16 f32 elements) through a 5-stage LDS
+// tiles of 64 B per row (32 16-bit or 16 f32 elements) through a 4-stage LDS
 // ring: each wave moves whole 16-row blocks of X and W straight from global
 // memory into LDS by 16 B global_load_lds (buffer loads: out-of-range rows
-// and k come back as zeros, so edge tiles need no other guard), two stages
-// stay in flight beyond the next one, and one barrier per k tile both
+// and k come back as zeros, so edge tiles need no other guard), one stage
+// stays in flight beyond the next one, and one barrier per k tile both
 // publishes a stage and frees the slot the next issue refills. Each wave
 // reads the next stage's fragments from LDS while the current stage's
-// MFMAs run (two register sets, reads spread between the MFMAs). In LDS, piece c of row r sits at slot c ^ ((r / 4) % 4), so
-// a fragment read is free of bank conflicts. Shapes that leave CUs idle
-// split K over workgroups into fp32 partials that a second kernel sums in
-// split order (deterministic) before the single rounding.
+// MFMAs run (two register sets, reads spread between the MFMAs). In LDS,
+// piece c of row r sits at slot c ^ rowKey(r), so a fragment read is free of
+// bank conflicts. Shapes that leave CUs idle split K over workgroups into
+// fp32 partials that a second kernel sums in split order (deterministic)
+// before the single rounding.
 //
 // W is the MFMA's A operand and X its B operand, so a lane's accumulator
-// holds 4 consecutive columns n of one row m of Y: one 8 B (16-bit) or 16 B
-// (f32) store per lane and fragment.
+// holds 4 consecutive columns n of one row m of Y. 16-bit tiles leave
+// through the idle LDS ring as whole rows (16 B per lane); otherwise one 8 B
+// or 16 B store per lane and fragment.
 //
 // Workgroups go to the XCDs round-robin by id; the tile order puts each
 // XCD's workgroups on one contiguous run of tiles, walked m-fastest in groups
@@ -44,6 +46,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace llaisys::kernels {
@@ -126,7 +129,14 @@ struct GemmParams {
     int splits;                // > 1: K split over workgroups, fp32 partials part[split][M][N]
     float *part;
     int swiglu; // y = act[M][N / 2]: W rows are gate and up blocks of 16 in turn (swigluInterleave)
+    int staged; // 16-bit output, no split, N % 8 == 0, 16 B aligned rows: the tile leaves through LDS
 };
+
+// Bytes per row of a tile staged in LDS for the store: BN 16-bit values and
+// 32 B of padding, so that the 16 rows one fragment write touches start 8
+// banks apart.
+template <int BN> constexpr int stagePitch() { return BN * 2 + 32; }
+template <int BM, int BN> constexpr size_t stageBytes() { return size_t(BM) * stagePitch<BN>(); }
 
 // Tile index of workgroup b: XCD b % 8 takes tiles [(b % 8) T / 8, ...) in
 // order b / 8 (T = tiles; when T % 8 != 0 the plain order is kept).
@@ -335,6 +345,81 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
         }
         return;
     }
+    if constexpr (ES == 2) {
+        if (p.staged) {
+            // The tile leaves through LDS (the ring is idle now): every lane
+            // writes its 8 B pieces to a row-major copy, then each lane stores
+            // 16 B of a row, so one store instruction writes whole 128 B lines
+            // (the fragment layout writes 32 B of 16 rows each, and the stores
+            // then took a fifth of a 256 x 256 x 1536 tile's time).
+            using E = typename Elem<T>::type;
+            typedef E e4 __attribute__((ext_vector_type(4)));
+            constexpr int PITCH = stagePitch<BN>();
+            char *stage = reinterpret_cast<char *>(lds);
+            __syncthreads(); // every wave is done with the ring
+            if constexpr (T == ElemType::BF16 && TN % 2 == 0) {
+                if (p.swiglu) {
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) {
+                        const int ml = wm * (BM / WGM) + 16 * j + fr;
+#pragma unroll
+                        for (int t = 0; t < TN / 2; ++t) {
+                            const int nl = (wn * (BN / WGN) + 32 * t) / 2 + 4 * fg; // act column in the tile
+                            uint32_t w2[2];
+#pragma unroll
+                            for (int h = 0; h < 2; ++h) {
+                                uint32_t pk = 0;
+#pragma unroll
+                                for (int e = 0; e < 2; ++e) {
+                                    const float g = float(__bf16(acc[2 * t][j][2 * h + e]));
+                                    const float u = float(__bf16(acc[2 * t + 1][j][2 * h + e]));
+                                    pk |= uint32_t(__builtin_bit_cast(uint16_t, __bf16(u * g / (1.f + expf(-g)))))
+                                          << (16 * e);
+                                }
+                                w2[h] = pk;
+                            }
+                            *reinterpret_cast<uint2 *>(stage + ml * PITCH + nl * 2) = make_uint2(w2[0], w2[1]);
+                        }
+                    }
+                }
+            }
+            if (!p.swiglu) {
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    const int ml = wm * (BM / WGM) + 16 * j + fr, m = m0 + ml;
+#pragma unroll
+                    for (int i = 0; i < TN; ++i) {
+                        const int nl = wn * (BN / WGN) + 16 * i + 4 * fg, n = n0 + nl;
+                        f32x4 v = acc[i][j];
+                        if (m < p.M && n < p.N) {
+                            if (p.accumulate) v = load4<T>(p.y, size_t(m) * p.N + n) + v;
+                            if (p.bias) v += load4<T>(p.bias, n);
+                        }
+                        *reinterpret_cast<e4 *>(stage + ml * PITCH + nl * 2) = e4{E(v[0]), E(v[1]), E(v[2]), E(v[3])};
+                    }
+                }
+            }
+            __syncthreads();
+            // Rows out, 16 B (8 values) per lane.
+            auto storeRows = [&](auto cpr_tag) {
+                constexpr int CPR = decltype(cpr_tag)::value; // 16 B chunks per tile row
+                const int n_out = p.swiglu ? p.N / 2 : p.N, c0 = p.swiglu ? n0 / 2 : n0;
+#pragma unroll 4
+                for (int q = tid; q < BM * CPR; q += 64 * NW) {
+                    const int row = q / CPR, c = q % CPR;
+                    const int m = m0 + row, col = c0 + 8 * c;
+                    if (m < p.M && col < n_out)
+                        *reinterpret_cast<u32x4 *>(static_cast<E *>(p.y) + size_t(m) * n_out + col) =
+                            *reinterpret_cast<const u32x4 *>(stage + row * PITCH + c * 16);
+                }
+            };
+            if (p.swiglu)
+                storeRows(std::integral_constant<int, BN / 16>{});
+            else
+                storeRows(std::integral_constant<int, BN / 8>{});
+            return;
+        }
+    }
     if constexpr (T == ElemType::BF16 && TN % 2 == 0) {
         if (p.swiglu) {
             // W fragments 2t and 2t + 1 of the wave are a gate block and its up
@@ -451,7 +536,8 @@ int cusOf() {
 }
 
 template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE> void launchTileAs(GemmParams p, hipStream_t s) {
-    const size_t lds = size_t(ringStages<PIPE>()) * (BM + BN) * kRowBytes;
+    const size_t lds = std::max(size_t(ringStages<PIPE>()) * (BM + BN) * kRowBytes,
+                                Elem<T>::size == 2 ? stageBytes<BM, BN>() : size_t(0));
     // The LDS limit is raised once per device the kernel runs on.
     static std::mutex mu;
     static std::vector<bool> raised;
@@ -532,6 +618,12 @@ Plan planGemm(ElemType t, int M, int N, int K, bool no_split = false) {
         }
     }
     return best;
+}
+
+// LLAISYS_GEMM_STAGED=0: 16-bit tiles stored straight from the fragments.
+bool stagedStores() {
+    static const bool v = [] { const char *e = std::getenv("LLAISYS_GEMM_STAGED"); return !(e && e[0] == '0'); }();
+    return v;
 }
 
 // 128 x 256 and 256 x 128 tiles with 8 waves (two per SIMD, 64 x 64 each)
@@ -646,6 +738,8 @@ void linear(void *y, const void *x, const void *w, const void *bias, ElemType t,
         p.x_bytes = uint32_t(size_t(m) * row_bytes);
         p.w_bytes = uint32_t(size_t(N) * row_bytes);
         p.part = static_cast<float *>(workspace);
+        p.staged = es == 2 && plan.splits == 1 && N % 8 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0 &&
+                   stagedStores();
         switch (t) {
         case ElemType::BF16: launchGemm<ElemType::BF16>(p, plan, s); break;
         case ElemType::F16: launchGemm<ElemType::F16>(p, plan, s); break;
@@ -681,6 +775,7 @@ void linearSwiglu(void *act, const void *x, const void *w_interleaved, ElemType 
         p.x_bytes = uint32_t(size_t(m) * row_bytes);
         p.w_bytes = uint32_t(size_t(N) * row_bytes);
         p.swiglu = 1;
+        p.staged = di % 8 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0 && stagedStores();
         launchGemm<ElemType::BF16>(p, plan, s);
     }
 }
