@@ -130,6 +130,8 @@ struct GemmParams {
     float *part;
     int swiglu; // y = act[M][N / 2]: W rows are gate and up blocks of 16 in turn (swigluInterleave)
     int staged; // 16-bit output, no split, N % 8 == 0, 16 B aligned rows: the tile leaves through LDS
+    int ldy;    // elements between rows of y (N, or N / 2 for swiglu, unless y is a column range of a wider
+                // matrix); split partials and the reduce keep ldy == N
 };
 
 // Bytes per row of a tile staged in LDS for the store: BN 16-bit values and
@@ -392,7 +394,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
                         const int nl = wn * (BN / WGN) + 16 * i + 4 * fg, n = n0 + nl;
                         f32x4 v = acc[i][j];
                         if (m < p.M && n < p.N) {
-                            if (p.accumulate) v = load4<T>(p.y, size_t(m) * p.N + n) + v;
+                            if (p.accumulate) v = load4<T>(p.y, size_t(m) * p.ldy + n) + v;
                             if (p.bias) v += load4<T>(p.bias, n);
                         }
                         *reinterpret_cast<e4 *>(stage + ml * PITCH + nl * 2) = e4{E(v[0]), E(v[1]), E(v[2]), E(v[3])};
@@ -409,7 +411,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
                     const int row = q / CPR, c = q % CPR;
                     const int m = m0 + row, col = c0 + 8 * c;
                     if (m < p.M && col < n_out)
-                        *reinterpret_cast<u32x4 *>(static_cast<E *>(p.y) + size_t(m) * n_out + col) =
+                        *reinterpret_cast<u32x4 *>(static_cast<E *>(p.y) + size_t(m) * p.ldy + col) =
                             *reinterpret_cast<const u32x4 *>(stage + row * PITCH + c * 16);
                 }
             };
@@ -426,7 +428,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
             // block (the wave's columns start at a multiple of 32): the lane
             // holds gate and up of the same four act columns. Both are rounded
             // to bf16 first, as the GEMM output swigluRows would read.
-            const int da = p.N / 2;
+            const int da = p.ldy;
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
                 const int m = m0 + wm * (BM / WGM) + 16 * j + fr;
@@ -463,7 +465,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
         for (int i = 0; i < TN; ++i) {
             const int n = n0 + wn * (BN / WGN) + 16 * i + 4 * fg;
             if (n >= p.N) continue;
-            const size_t base = size_t(m) * p.N + n;
+            const size_t base = size_t(m) * p.ldy + n;
             f32x4 v = acc[i][j];
             if (vec) {
                 if (p.accumulate) v = load4<T>(p.y, base) + v;
@@ -582,6 +584,7 @@ template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2> void launchTile(
 struct Plan {
     int tile = 0; // index into kTiles
     int mtiles = 0, ntiles = 0, splits = 1;
+    double est = 0; // the model's time, us
 };
 struct TileShape { int bm, bn; double eff; };
 constexpr TileShape kTiles[] = {{128, 256, 1.0}, {256, 128, 1.0}, {128, 128, 0.8}, {64, 64, 0.45}, {256, 256, 1.2}};
@@ -614,10 +617,41 @@ Plan planGemm(ElemType t, int M, int N, int K, bool no_split = false) {
                 best.mtiles = int(mt);
                 best.ntiles = int(nt);
                 best.splits = sp;
+                best.est = tm;
             }
         }
     }
     return best;
+}
+
+// A plan whose last round of workgroups leaves most CUs idle (2048 x 17920:
+// 560 tiles of 256 x 256 in three rounds on 256 CUs, the last under a fifth
+// full) runs as two launches instead: columns [0, na) on the plan's tiles in
+// whole rounds, the rest on their own (smaller) tiles, when the model prices
+// the two below the one. Splits of K are left alone. na is a multiple of the
+// tile width (so of 64: whole SwiGLU pairs, 16 B aligned rows).
+constexpr double kSecondLaunchUs = 3.0;
+struct ColumnSplit {
+    int na = 0; // 0: one launch
+    Plan a, b;
+};
+ColumnSplit splitColumns(ElemType t, int M, int N, int K, const Plan &one) {
+    ColumnSplit cs;
+    static const bool on = [] { const char *e = std::getenv("LLAISYS_GEMM_COLUMN_SPLIT"); return !(e && e[0] == '0'); }();
+    if (!on || one.splits != 1 || N % 8 != 0) return cs; // (vector stores need rows of whole 16 B)
+    const long cus = cusOf();
+    const long tiles = long(one.mtiles) * one.ntiles, rounds = (tiles + cus - 1) / cus;
+    if (rounds < 2 || tiles % cus == 0) return cs;
+    const int nta = int((rounds - 1) * cus / one.mtiles); // column tiles that fill rounds - 1 rounds
+    if (nta <= 0 || nta >= one.ntiles) return cs;
+    const int na = nta * kTiles[one.tile].bn;
+    const Plan a = planGemm(t, M, na, K, true), b = planGemm(t, M, N - na, K, true);
+    if (a.est + b.est + kSecondLaunchUs < 0.95 * one.est) {
+        cs.na = na;
+        cs.a = a;
+        cs.b = b;
+    }
+    return cs;
 }
 
 // LLAISYS_GEMM_STAGED=0: 16-bit tiles stored straight from the fragments.
@@ -726,24 +760,35 @@ void linear(void *y, const void *x, const void *w, const void *bias, ElemType t,
         const int m = std::min(rows_per_launch, M - r0);
         const Plan plan = planGemm(t, m, N, K);
         LLAISYS_CHECK(plan.splits == 1 || workspace, "linear: this shape needs linearWorkspaceBytes() of workspace");
-        GemmParams p{};
-        p.y = static_cast<char *>(y) + size_t(r0) * N * es;
-        p.x = static_cast<const char *>(x) + size_t(r0) * row_bytes;
-        p.w = w;
-        p.bias = bias;
-        p.M = m;
-        p.N = N;
-        p.K = K;
-        p.accumulate = accumulate ? 1 : 0;
-        p.x_bytes = uint32_t(size_t(m) * row_bytes);
-        p.w_bytes = uint32_t(size_t(N) * row_bytes);
-        p.part = static_cast<float *>(workspace);
-        p.staged = es == 2 && plan.splits == 1 && N % 8 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0 &&
-                   stagedStores();
-        switch (t) {
-        case ElemType::BF16: launchGemm<ElemType::BF16>(p, plan, s); break;
-        case ElemType::F16: launchGemm<ElemType::F16>(p, plan, s); break;
-        case ElemType::F32: launchGemm<ElemType::F32>(p, plan, s); break;
+        // Columns [c0, c1) of this launch's rows on `pl` (y keeps its row stride N).
+        auto run = [&](int c0, int c1, const Plan &pl) {
+            GemmParams p{};
+            p.y = static_cast<char *>(y) + (size_t(r0) * N + c0) * es;
+            p.x = static_cast<const char *>(x) + size_t(r0) * row_bytes;
+            p.w = static_cast<const char *>(w) + size_t(c0) * row_bytes;
+            p.bias = bias ? static_cast<const char *>(bias) + size_t(c0) * es : nullptr;
+            p.M = m;
+            p.N = c1 - c0;
+            p.K = K;
+            p.ldy = N;
+            p.accumulate = accumulate ? 1 : 0;
+            p.x_bytes = uint32_t(size_t(m) * row_bytes);
+            p.w_bytes = uint32_t(size_t(c1 - c0) * row_bytes);
+            p.part = static_cast<float *>(workspace);
+            p.staged = es == 2 && pl.splits == 1 && N % 8 == 0 && (c1 - c0) % 8 == 0 &&
+                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0 && stagedStores();
+            switch (t) {
+            case ElemType::BF16: launchGemm<ElemType::BF16>(p, pl, s); break;
+            case ElemType::F16: launchGemm<ElemType::F16>(p, pl, s); break;
+            case ElemType::F32: launchGemm<ElemType::F32>(p, pl, s); break;
+            }
+        };
+        const ColumnSplit cs = splitColumns(t, m, N, K, plan);
+        if (cs.na) {
+            run(0, cs.na, cs.a);
+            run(cs.na, N, cs.b);
+        } else {
+            run(0, N, plan);
         }
     }
 }
@@ -765,18 +810,30 @@ void linearSwiglu(void *act, const void *x, const void *w_interleaved, ElemType 
     for (int r0 = 0; r0 < M; r0 += rows_per_launch) {
         const int m = std::min(rows_per_launch, M - r0);
         const Plan plan = planGemm(t, m, N, K, true);
-        GemmParams p{};
-        p.y = static_cast<uint16_t *>(act) + size_t(r0) * di;
-        p.x = static_cast<const char *>(x) + size_t(r0) * row_bytes;
-        p.w = w_interleaved;
-        p.M = m;
-        p.N = N;
-        p.K = K;
-        p.x_bytes = uint32_t(size_t(m) * row_bytes);
-        p.w_bytes = uint32_t(size_t(N) * row_bytes);
-        p.swiglu = 1;
-        p.staged = di % 8 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0 && stagedStores();
-        launchGemm<ElemType::BF16>(p, plan, s);
+        // Columns [c0, c1) of the gate-up product, act columns [c0 / 2, c1 / 2).
+        auto run = [&](int c0, int c1, const Plan &pl) {
+            GemmParams p{};
+            p.y = static_cast<uint16_t *>(act) + size_t(r0) * di + c0 / 2;
+            p.x = static_cast<const char *>(x) + size_t(r0) * row_bytes;
+            p.w = static_cast<const char *>(w_interleaved) + size_t(c0) * row_bytes;
+            p.M = m;
+            p.N = c1 - c0;
+            p.K = K;
+            p.ldy = di;
+            p.x_bytes = uint32_t(size_t(m) * row_bytes);
+            p.w_bytes = uint32_t(size_t(c1 - c0) * row_bytes);
+            p.swiglu = 1;
+            p.staged = di % 8 == 0 && ((c1 - c0) / 2) % 8 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0 &&
+                       stagedStores();
+            launchGemm<ElemType::BF16>(p, pl, s);
+        };
+        const ColumnSplit cs = splitColumns(t, m, N, K, plan);
+        if (cs.na) {
+            run(0, cs.na, cs.a);
+            run(cs.na, N, cs.b);
+        } else {
+            run(0, N, plan);
+        }
     }
 }
 
