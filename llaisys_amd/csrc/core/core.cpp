@@ -45,6 +45,7 @@ Runtime::~Runtime() {
         if (slot_rec_) api_->free_device(slot_rec_);
         if (error_word_) api_->free_device(error_word_);
         if (queue_counters_) api_->free_device(queue_counters_);
+        if (flag_slots_) api_->free_host(flag_slots_);
         api_->destroy_stream(stream_);
     } catch (...) {
     }
@@ -131,6 +132,20 @@ int Runtime::takeErrorFlags() {
 }
 
 void Runtime::stashErrorFlags() { pending_error_flags_ |= takeDeviceErrorFlags(); }
+
+void Runtime::flagSnapshotAsync(int slot) {
+    LLAISYS_CHECK(type_ == LLAISYS_DEVICE_AMD && slot >= 0 && slot < 2, "flag snapshots: AMD runtimes, slots 0 and 1");
+    int *word = errorWord();
+    if (!flag_slots_) {
+        flag_slots_ = static_cast<int *>(api_->malloc_host(2 * sizeof(int)));
+        flag_slots_[0] = flag_slots_[1] = 0;
+    }
+    api_->memcpy_async(flag_slots_ + slot, word, sizeof(int), LLAISYS_MEMCPY_D2H, stream());
+    if (hipMemsetAsync(word, 0, sizeof(int), static_cast<hipStream_t>(stream())) != hipSuccess)
+        LLAISYS_RAISE("hipMemsetAsync failed");
+}
+
+int Runtime::flagSnapshot(int slot) const { return flag_slots_ && slot >= 0 && slot < 2 ? flag_slots_[slot] : 0; }
 
 int Runtime::takeDeviceErrorFlags() {
     if (type_ == LLAISYS_DEVICE_CPU) return __atomic_exchange_n(&host_error_word_, 0, __ATOMIC_RELAXED);

@@ -102,6 +102,14 @@ public:
     // alone. The pending bits stay for takeErrorFlags().
     void stashErrorFlags();
     int takeDeviceErrorFlags();
+    // The same split without waiting (AMD runtimes): flagSnapshotAsync(i)
+    // enqueues on the stream a copy of the device word into pinned host slot
+    // i (of 2) and the word's clearing; once the caller has synchronised the
+    // stream, flagSnapshot(i) holds the bits. addPendingErrorFlags keeps bits
+    // for takeErrorFlags(), as stashErrorFlags does.
+    void flagSnapshotAsync(int slot);
+    int flagSnapshot(int slot) const;
+    void addPendingErrorFlags(int bits) { pending_error_flags_ |= bits; }
 
     void activate();
 
@@ -117,6 +125,7 @@ private:
     int *queue_counters_ = nullptr;
     int host_error_word_ = 0;
     int pending_error_flags_ = 0; // stashed by stashErrorFlags(), returned by takeErrorFlags()
+    int *flag_slots_ = nullptr;   // pinned host, 2 ints (flagSnapshotAsync)
     int *slot_hdr_ = nullptr;
     size_t slot_hdr_ints_ = 0;
     void *slot_rec_ = nullptr;

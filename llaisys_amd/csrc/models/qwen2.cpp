@@ -46,6 +46,38 @@ int64_t *i64(const tensor_t &t) { return reinterpret_cast<int64_t *>(t->data());
 int32_t *i32(const tensor_t &t) { return reinterpret_cast<int32_t *>(t->data()); }
 tensor_t rows(const tensor_t &t, size_t n) { return t->slice(0, 0, n); }
 
+// Stream-ordered error-flag snapshots around one model call: slot 0 (taken
+// on construction) holds the bits earlier calls raised, slot 1 (end()) this
+// call's; collect() reads both after the call's own stream sync. If the call
+// throws in between, the destructor waits for the stream and keeps whatever
+// was snapshotted for llaisysGetDeviceErrorFlags, as the device word would
+// have.
+class FlagSnapshots {
+public:
+    explicit FlagSnapshots(core::Runtime &rt) : rt_(rt) { rt_.flagSnapshotAsync(0); }
+    void end() {
+        rt_.flagSnapshotAsync(1);
+        ended_ = true;
+    }
+    int collect() {
+        rt_.addPendingErrorFlags(rt_.flagSnapshot(0));
+        collected_ = true;
+        return rt_.flagSnapshot(1);
+    }
+    ~FlagSnapshots() {
+        if (collected_) return;
+        try {
+            rt_.api()->stream_synchronize(rt_.stream());
+            rt_.addPendingErrorFlags(rt_.flagSnapshot(0) | (ended_ ? rt_.flagSnapshot(1) : 0));
+        } catch (...) {
+        }
+    }
+
+private:
+    core::Runtime &rt_;
+    bool ended_ = false, collected_ = false;
+};
+
 // Y[M, N] = X W^T (+ bias) (+ Y) through the MFMA GEMM over row-major W.
 void gemm(const tensor_t &y, const tensor_t &x, const tensor_t &w, const tensor_t &bias, int M, int N, int K,
           bool accumulate, void *s) {
@@ -264,7 +296,9 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     ensureFolded();
     auto &rt = core::context().runtime();
-    rt.stashErrorFlags(); // earlier calls' bits stay for llaisysGetDeviceErrorFlags
+    // Earlier calls' bits stay for llaisysGetDeviceErrorFlags: snapshot (and
+    // clear) the device word in stream order, read after the step's one sync.
+    FlagSnapshots flag_snaps(rt);
     const size_t B = nseq;
     size_t T = 0;
     for (size_t i = 0; i < B; ++i) {
@@ -328,9 +362,10 @@ void Qwen2Model::step(const int64_t *ids, size_t nseq, const int64_t *tokens, co
 
     // next tokens back to the host; the staging buffers are free after this.
     int64_t *hnext = h64 + n64;
+    flag_snaps.end(); // this call's kernels only
     api->memcpy_async(hnext, next_->data(), B * sizeof(int64_t), LLAISYS_MEMCPY_D2H, rt.stream());
     api->stream_synchronize(rt.stream());
-    const int flags = rt.takeDeviceErrorFlags(); // this call's kernels only
+    const int flags = flag_snaps.collect();
     LLAISYS_CHECK(flags == 0, "qwen2 step: kernels reported error flags " << flags);
     std::memcpy(next, hnext, B * sizeof(int64_t));
     last_B_ = B;
@@ -350,7 +385,7 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     core::context().setDevice(LLAISYS_DEVICE_AMD, dev_);
     ensureFolded();
     auto &rt = core::context().runtime();
-    rt.stashErrorFlags(); // earlier calls' bits stay for llaisysGetDeviceErrorFlags
+    FlagSnapshots flag_snaps(rt); // earlier calls' bits, read after the call's one sync
     const size_t B = nseq;
     for (size_t i = 0; i < B; ++i) {
         LLAISYS_CHECK(size_t(blocks_.length(ids[i])) + nsteps <= cfg_.maxseq,
@@ -436,9 +471,10 @@ void Qwen2Model::decode(const int64_t *ids, size_t nseq, const int64_t *first, s
     K::decodeRecordLast(history, i64(next_), counter, int(B), s);
 
     int64_t *hout = h64 + 3 * B;
+    flag_snaps.end(); // this call's kernels only
     api->memcpy_async(hout, history, nsteps * B * sizeof(int64_t), LLAISYS_MEMCPY_D2H, s);
     api->stream_synchronize(s);
-    const int flags = rt.takeDeviceErrorFlags(); // this call's kernels only
+    const int flags = flag_snaps.collect();
     LLAISYS_CHECK(flags == 0, "qwen2 decode: kernels reported error flags " << flags);
     std::memcpy(out, hout, nsteps * B * sizeof(int64_t));
     last_B_ = B;
