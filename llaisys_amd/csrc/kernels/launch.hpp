@@ -38,7 +38,9 @@ void pagedAppendGather(uint16_t *k_out, uint16_t *v_out, uint16_t *k_pool, uint1
 // Batched decode: stream-K over all page pairs, then a combine kernel for
 // sequences split across waves. cu_q == nullptr: sequence b's query is row b
 // (T == B); else its row is cu_q[b] and sequences with cu_q[b+1]-cu_q[b] != 1
-// are skipped (left to pagedPrefill).
+// are skipped (left to pagedPrefill). out_packed (bf16 only): the rows go
+// there in operand order (packedRowIndex over nh * 128 columns) instead of to
+// out, for a packed-X projection after it.
 struct DecodePlan {
     int waves;           // grid of single-wave workgroups
     int stages;          // page pairs in flight per wave
@@ -52,7 +54,7 @@ DecodePlan planDecode(int B, int nkvh, int group, int max_pages);
 void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_pool, const uint16_t *v_pool,
                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                  int nkvh, int max_pages, int num_blocks, float scale, const DecodePlan &plan, float *records,
-                 int *err, int *slot_headers, void *slot_records, void *stream);
+                 int *err, int *slot_headers, void *slot_records, void *stream, uint16_t *out_packed = nullptr);
 
 // The same attention (cu_q null: query row b is sequence b) with one
 // workgroup of 4 waves per (sequence, kv head), merging in LDS: no records,

@@ -65,9 +65,27 @@ struct DecodeArgs {
     int *err;
     int *slot_hdr;   // null: every split unit uses the per-wave records
     float *slot_rec; // kUnitSlots records of G * (kHeadDim + 2) floats per unit
+    uint16_t *out_packed; // non-null (bf16 out): rows go there in operand order (packedRowIndex) instead of to out
     int B, T, nh, nkvh, G, max_pages, num_blocks, W;
     float scale_log2;
 };
+
+// Dims 16 i + 4 grp .. + 3 (i < 8) of output column block col0 - 4 grp of
+// query row `row`, times inv, rounded to bf16 into the packed row copy: one
+// 8 B piece each (4 consecutive columns never cross an 8-column chunk).
+__device__ __forceinline__ void storePackedPieces(uint16_t *dst, int row, int col0, int K, const f32x4 (&o)[8],
+                                                  float inv) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 v = o[i] * inv;
+        const __bf16 e0 = (__bf16)v[0], e1 = (__bf16)v[1], e2 = (__bf16)v[2], e3 = (__bf16)v[3];
+        const uint32_t w0 =
+            uint32_t(__builtin_bit_cast(uint16_t, e0)) | (uint32_t(__builtin_bit_cast(uint16_t, e1)) << 16);
+        const uint32_t w1 =
+            uint32_t(__builtin_bit_cast(uint16_t, e2)) | (uint32_t(__builtin_bit_cast(uint16_t, e3)) << 16);
+        *reinterpret_cast<uint2 *>(dst + packedRowIndex(row, col0 + 16 * i, K)) = make_uint2(w0, w1);
+    }
+}
 
 // Exclusive prefix (over b) of nkvh * npairs(b) into S[0..B], lengths into C,
 // query rows into Q. Invalid lengths (< 1 or beyond the block table) count as
@@ -134,8 +152,10 @@ template <int NSTAGE> struct Ring {
 };
 
 // Two stages fit 256 registers (two waves per SIMD); three need the whole
-// register file (one wave per SIMD) to avoid spilling.
-template <bool OUT_F32, int NSTAGE>
+// register file (one wave per SIMD) to avoid spilling. PACKED (bf16): rows
+// go to a.out_packed; a separate instance, since the branch in the finish
+// cost the plain kernel 14 % (53.8 -> 61.3 us at config 3).
+template <bool OUT_F32, int NSTAGE, bool PACKED = false>
 __global__ void __launch_bounds__(64)
     __attribute__((amdgpu_waves_per_eu(NSTAGE == 2 ? 2 : 1, NSTAGE == 2 ? 2 : 1))) decodeKernel(DecodeArgs a) {
     extern __shared__ int lds[];
@@ -226,6 +246,11 @@ __global__ void __launch_bounds__(64)
         if (first >= s && first + npr <= e) {
             if (n < G) {
                 const float inv = 1.f / lt;
+                if constexpr (PACKED && !OUT_F32) {
+                    storePackedPieces(a.out_packed, Q[cur_b], (cur_h * G + n) * kHeadDim + 4 * grp, a.nh * kHeadDim,
+                                      acc.o, inv);
+                    return;
+                }
                 const size_t row = (size_t(Q[cur_b]) * a.nh + cur_h * G + n) * kHeadDim;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, row, i, grp, acc.o[i] * inv);
@@ -319,7 +344,8 @@ __global__ void __launch_bounds__(64)
 // meet in LDS and wave 0 writes the output.
 constexpr int kCombineWaves = 4;
 
-template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) decodeCombineKernel(DecodeArgs a) {
+template <bool OUT_F32, bool PACKED = false>
+__global__ void __launch_bounds__(64 * kCombineWaves) decodeCombineKernel(DecodeArgs a) {
     extern __shared__ int lds[];
     int *S = lds;
     int *C = lds + a.B + 1;
@@ -464,6 +490,10 @@ template <bool OUT_F32> __global__ void __launch_bounds__(64 * kCombineWaves) de
         M = Mn;
     }
     const float inv = 1.f / L;
+    if constexpr (PACKED && !OUT_F32) {
+        storePackedPieces(a.out_packed, row, (h * G + n) * kHeadDim + 4 * grp, a.nh * kHeadDim, o, inv);
+        return;
+    }
     const size_t orow = (size_t(row) * a.nh + h * G + n) * kHeadDim;
 #pragma unroll
     for (int i = 0; i < 8; ++i) storeOut<OUT_F32>(a.out, orow, i, grp, o[i] * inv);
@@ -916,7 +946,7 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
                  const int32_t *block_table, const int32_t *ctx_len, const int32_t *cu_q, int B, int T, int nh,
                  int nkvh, int max_pages,
                  int num_blocks, float scale, const DecodePlan &plan, float *records, int *err,
-                 int *slot_headers, void *slot_records, void *stream) {
+                 int *slot_headers, void *slot_records, void *stream, uint16_t *out_packed) {
     if (B == 0) return;
     DecodeArgs a;
     a.q = q;
@@ -928,6 +958,9 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
     a.cu_q = cu_q;
     a.records = records;
     a.err = err;
+    LLAISYS_CHECK(!out_packed || (!out_f32 && (nh * kHeadDim) % 32 == 0),
+                  "pagedDecode: a packed output needs bf16 and nh * 128 % 32 == 0");
+    a.out_packed = out_packed;
     const bool slots = plan.slot_headers && slot_headers && slot_records;
     a.slot_hdr = slots ? slot_headers : nullptr;
     a.slot_rec = slots ? static_cast<float *>(slot_records) : nullptr;
@@ -950,11 +983,19 @@ void pagedDecode(void *out, bool out_f32, const uint16_t *q, const uint16_t *k_p
             hipLaunchKernelGGL((decodeKernel<true, 2>), grid, block, lds, s, a);
         hipLaunchKernelGGL((decodeCombineKernel<true>), comb, comb_block, lds, s, a);
     } else {
-        if (plan.stages == 3)
-            hipLaunchKernelGGL((decodeKernel<false, 3>), grid, block, lds, s, a);
-        else
-            hipLaunchKernelGGL((decodeKernel<false, 2>), grid, block, lds, s, a);
-        hipLaunchKernelGGL((decodeCombineKernel<false>), comb, comb_block, lds, s, a);
+        if (out_packed) {
+            if (plan.stages == 3)
+                hipLaunchKernelGGL((decodeKernel<false, 3, true>), grid, block, lds, s, a);
+            else
+                hipLaunchKernelGGL((decodeKernel<false, 2, true>), grid, block, lds, s, a);
+            hipLaunchKernelGGL((decodeCombineKernel<false, true>), comb, comb_block, lds, s, a);
+        } else {
+            if (plan.stages == 3)
+                hipLaunchKernelGGL((decodeKernel<false, 3>), grid, block, lds, s, a);
+            else
+                hipLaunchKernelGGL((decodeKernel<false, 2>), grid, block, lds, s, a);
+            hipLaunchKernelGGL((decodeCombineKernel<false>), comb, comb_block, lds, s, a);
+        }
     }
     HIP_CHECK(hipGetLastError());
 }

@@ -544,16 +544,20 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
     // Packed-operand decode path: qkv and o read x and the attention output
     // in MFMA operand order, written beside their rows by the embedding, the
     // down projection's split-K reduce and the attention itself.
+    // Batches of unequal lengths (stream-K attention, not one workgroup per
+    // unit) take it too when the QKV epilogue runs in the projection: the
+    // stream-K kernels then write their rows packed as well.
     const auto &L0 = layers_[0];
-    const bool px = packed_x_ && decode_only && unit_decode_ && unit_rope_ && fold_norm_ && T <= kFoldMaxRows &&
-                    cfg_.dtype == LLAISYS_DTYPE_BF16 && L0.qkv_wfp && L0.o_wp && L0.down_wp &&
+    const bool qkv_epi_ok = qkv_gemm_epilogue_ && K::qkvRopeGemmSupported(M, int(cfg_.nh), int(cfg_.nkvh), hs);
+    const bool px = packed_x_ && decode_only && ((unit_decode_ && unit_rope_) || qkv_epi_ok) && fold_norm_ &&
+                    T <= kFoldMaxRows && cfg_.dtype == LLAISYS_DTYPE_BF16 && L0.qkv_wfp && L0.o_wp && L0.down_wp &&
                     K::packedXGemmSupported(M, q + 2 * kv, hs) && K::packedXGemmSupported(M, hs, q) &&
                     K::splitKGemmSupported(M, hs, di);
     // On that path the gate-up projection, the row's 1/rms and the SwiGLU
     // run as one kernel over the packed x the o projection leaves.
     const bool fused_mlp = px && L0.gate_up_wfp && K::gateUpSwigluSupported(M, di, hs);
     // and the QKV epilogue runs in the QKV projection's epilogue.
-    const bool qkv_epi = px && qkv_gemm_epilogue_ && K::qkvRopeGemmSupported(M, int(cfg_.nh), int(cfg_.nkvh), hs);
+    const bool qkv_epi = px && qkv_epi_ok;
     // and the down projection reads the SwiGLU output packed.
     const bool down_px = fused_mlp && splitk_packed_ && K::splitKPackedSupported(M, hs, di) && di % 32 == 0;
     if (px)
@@ -578,9 +582,21 @@ void Qwen2Model::forward(size_t T, size_t B, bool decode_only) {
             K::qkvRopeGemm(u16(q_), u16(k_pool_[l]), u16(v_pool_[l]), u16(xp_), u16(L.qkv_wfp), u16(L.qkv_b),
                            i32(table_), i32(ctx_before_), M, int(cfg_.nh), int(cfg_.nkvh), hs,
                            int(table_->shape()[1]), int(num_blocks_), cfg_.epsilon, cfg_.theta, rt.errorWord(), s);
-            K::pagedDecodeUnits(a3->data(), false, u16(q3), u16(k_pool_[l]), u16(v_pool_[l]), i32(table_),
-                                i32(ctx_after_), int(B), int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]),
-                                int(num_blocks_), scale, rt.errorWord(), s, u16(ap_));
+            if (unit_decode_) {
+                K::pagedDecodeUnits(a3->data(), false, u16(q3), u16(k_pool_[l]), u16(v_pool_[l]), i32(table_),
+                                    i32(ctx_after_), int(B), int(cfg_.nh), int(cfg_.nkvh), int(table_->shape()[1]),
+                                    int(num_blocks_), scale, rt.errorWord(), s, u16(ap_));
+            } else {
+                const int max_pages = int(table_->shape()[1]);
+                const auto plan = K::planDecode(int(B), int(cfg_.nkvh), int(cfg_.nh / cfg_.nkvh), max_pages);
+                auto *records = static_cast<float *>(rt.scratch(plan.record_bytes));
+                K::pagedDecode(a3->data(), false, u16(q3), u16(k_pool_[l]), u16(v_pool_[l]), i32(table_),
+                               i32(ctx_after_), nullptr, int(B), int(B), int(cfg_.nh), int(cfg_.nkvh), max_pages,
+                               int(num_blocks_), scale, plan, records, rt.errorWord(),
+                               plan.slot_headers ? rt.decodeSlotHeaders(plan.slot_headers) : nullptr,
+                               plan.slot_headers ? rt.decodeSlotRecords(plan.slot_record_bytes) : nullptr, s,
+                               u16(ap_));
+            }
         } else if (px)
             K::packedXGemm(u16(qkv_), u16(xp_), u16(L.qkv_wfp), M, q + 2 * kv, hs, false, s);
         else

@@ -209,9 +209,10 @@ def test_fused_qkv_epilogue_matches_separate_launch(monkeypatch):
         assert (lg_a - lg_b).abs().max().item() <= 1e-2 * lg_b.abs().max().item()
 
 
-@pytest.mark.parametrize("qkv_epilogue,splitk_packed", [("1", "1"), ("0", "1"), ("1", "0")],
-                         ids=["default", "epilogue-in-attention", "lds-split-k"])
-def test_packed_operand_projections_match_library_and_reference(monkeypatch, qkv_epilogue, splitk_packed):
+@pytest.mark.parametrize("qkv_epilogue,splitk_packed,units", [("1", "1", "1"), ("0", "1", "1"), ("1", "0", "1"),
+                                                              ("1", "1", "0")],
+                         ids=["default", "epilogue-in-attention", "lds-split-k", "stream-k-attention"])
+def test_packed_operand_projections_match_library_and_reference(monkeypatch, qkv_epilogue, splitk_packed, units):
     # Decode steps on the unit attention at K = 1536 run the projections over
     # packed operands: the embedding, the split-K reduce, the attention and
     # the o projection write copies of their rows in MFMA operand order; qkv
@@ -228,9 +229,11 @@ def test_packed_operand_projections_match_library_and_reference(monkeypatch, qkv
     # single steps. The two non-default packed paths run too: the QKV
     # epilogue inside the attention (which then writes its output packed),
     # and the down projection staging x in LDS (its reduce writes x packed).
+    # And the stream-K attention (the batches of unequal lengths take it),
+    # whose main and combine kernels then write the rows packed.
     monkeypatch.setenv("LLAISYS_QKV_GEMM_EPILOGUE", qkv_epilogue)
     monkeypatch.setenv("LLAISYS_SPLITK_PACKED", splitk_packed)
-    monkeypatch.setenv("LLAISYS_DECODE_UNITS", "1")
+    monkeypatch.setenv("LLAISYS_DECODE_UNITS", units)
     monkeypatch.setenv("LLAISYS_DECODE_UNIT_ROPE", "1")
     nseq = 66
     lens = [200 + (i * 53) % 190 for i in range(nseq)]
