@@ -140,6 +140,12 @@ struct GemmParams {
 template <int BN> constexpr int stagePitch() { return BN * 2 + 32; }
 template <int BM, int BN> constexpr size_t stageBytes() { return size_t(BM) * stagePitch<BN>(); }
 
+// 1 KiB blocks of one ring stage: the tile's X blocks, then its W blocks
+// rounded up to whole blocks per wave (a BN / 16 that is not a multiple of the
+// wave count leaves some waves one masked load into the spare blocks, so
+// every wave issues the same number of loads and waits on the same counts).
+template <int BM, int BN, int NW> constexpr int stageBlocks() { return BM / 16 + (BN / 16 + NW - 1) / NW * NW; }
+
 // Tile index of workgroup b: XCD b % 8 takes tiles [(b % 8) T / 8, ...) in
 // order b / 8 (T = tiles; when T % 8 != 0 the plain order is kept).
 __device__ __forceinline__ void tileOf(const GemmParams &p, int b, int &mt, int &nt) {
@@ -185,10 +191,10 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
     constexpr int KT = kRowBytes / ES;              // elements per k tile
     constexpr int TM = BM / (16 * WGM), TN = BN / (16 * WGN); // 16-row fragments per wave
     constexpr int XB = BM / 16, WB = BN / 16;       // 1 KiB blocks per operand per k tile
-    constexpr int XW = XB / NW, WW = WB / NW;       // ... issued by each wave
-    constexpr int STAGE = (BM + BN) * kRowBytes / 16; // u32x4 per stage
+    constexpr int XW = XB / NW, WW = (WB + NW - 1) / NW; // ... issued by each wave
+    constexpr int STAGE = stageBlocks<BM, BN, NW>() * 64; // u32x4 per stage
     constexpr int kLoadsPerStage = XW + WW;          // per wave
-    static_assert(XB % NW == 0 && WB % NW == 0, "each wave issues whole blocks");
+    static_assert(XB % NW == 0, "each wave issues whole X blocks");
     extern __shared__ u32x4 lds[];                   // [NS][X blocks | W blocks]
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -227,8 +233,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
                                                      int(in_k ? xbase + kb + b * bstride : kMasked), 0, 0, 0);
 #pragma unroll
         for (int b = 0; b < WW; ++b)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void *)(st + (XB + wave + NW * b) * 64), 16,
-                                                     int(in_k ? wbase + kb + b * bstride : kMasked), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wr, (lds_void *)(st + (XB + wave + NW * b) * 64), 16,
+                int(in_k && (WB % NW == 0 || wave + NW * b < WB) ? wbase + kb + b * bstride : kMasked), 0, 0, 0);
     };
 
     f32x4 acc[TN][TM];
@@ -538,7 +545,7 @@ int cusOf() {
 }
 
 template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE> void launchTileAs(GemmParams p, hipStream_t s) {
-    const size_t lds = std::max(size_t(ringStages<PIPE>()) * (BM + BN) * kRowBytes,
+    const size_t lds = std::max(size_t(ringStages<PIPE>()) * stageBlocks<BM, BN, WGM * WGN>() * 1024,
                                 Elem<T>::size == 2 ? stageBytes<BM, BN>() : size_t(0));
     // The LDS limit is raised once per device the kernel runs on.
     static std::mutex mu;
@@ -587,27 +594,41 @@ struct Plan {
     double est = 0; // the model's time, us
 };
 struct TileShape { int bm, bn; double eff; };
-constexpr TileShape kTiles[] = {{128, 256, 1.0}, {256, 128, 1.0}, {128, 128, 0.8}, {64, 64, 0.45}, {256, 256, 1.2}};
+// 256 x 192 (8 waves of 128 x 48) fills the 256 CUs where 256 x 256 tiles
+// leave a quarter idle (8192 x 1536 x 1536: 256 tiles against 192, 44.6 ->
+// 40.2 us; 2048 x 1536 x 8960 split in 4: 76 -> 69.5 us); its wave columns
+// are not whole SwiGLU block pairs, so the fused gate-up skips it.
+constexpr TileShape kTiles[] = {{128, 256, 1.0}, {256, 128, 1.0}, {128, 128, 0.8},
+                                {64, 64, 0.45},  {256, 256, 1.2}, {256, 192, 1.1}};
+constexpr int kTile192 = 5;
 constexpr int kMinSplitTiles = 8;            // k tiles per split at least
 constexpr double kFixedUs = 6.0;             // per round of workgroups
 constexpr double kMacsPerUs = 2.1e6;         // bm * bn * k per us at eff 1 (bf16)
 constexpr double kReduceBytesPerUs = 5.0e6;  // HBM rate of the reduce kernel
 constexpr double kReduceLaunchUs = 2.0;
 
-Plan planGemm(ElemType t, int M, int N, int K, bool no_split = false) {
+Plan planGemm(ElemType t, int M, int N, int K, bool no_split = false, bool swiglu = false) {
     const long cus = cusOf();
     const int es = t == ElemType::F32 ? 4 : 2;
     const int nk = (K * es + kRowBytes - 1) / kRowBytes;
     Plan best;
     double best_t = 1e300;
-    // LLAISYS_GEMM_BIG=0 leaves out the 256 x 256 tile (8 waves of 128 x 64).
-    static const int ntiles = [] { const char *e = std::getenv("LLAISYS_GEMM_BIG"); return e && e[0] == '0' ? 4 : 5; }();
-    for (int i = 0; i < (t == ElemType::F32 ? 4 : ntiles); ++i) { // f32: 128 accumulators at most
+    // LLAISYS_GEMM_BIG=0 leaves out the 256 x 256 tile (8 waves of 128 x 64),
+    // LLAISYS_GEMM_192=0 the 256 x 192 one.
+    static const bool big = [] { const char *e = std::getenv("LLAISYS_GEMM_BIG"); return !(e && e[0] == '0'); }();
+    static const bool t192 = [] { const char *e = std::getenv("LLAISYS_GEMM_192"); return !(e && e[0] == '0'); }();
+    for (int i = 0; i < int(sizeof(kTiles) / sizeof(kTiles[0])); ++i) {
+        if (t == ElemType::F32 && i >= 4) break; // f32: 128 accumulators at most
+        if ((i == 4 && !big) || (i == kTile192 && (!t192 || swiglu))) continue;
         const TileShape &c = kTiles[i];
         const long mt = (M + c.bm - 1) / c.bm, nt = (N + c.bn - 1) / c.bn;
         for (int sp = 1; sp <= 8; sp *= 2) {
             if (sp > 1 && (no_split || nk / sp < kMinSplitTiles)) break;
             const long rounds = (mt * nt * sp + cus - 1) / cus;
+            // 256 x 192 only in one round: over several (2048 x 17920 x 1536:
+            // 3 rounds, 128-131 us) 256 x 256 tiles with the column split below
+            // run faster (123-125 us) than the model prices them.
+            if (i == kTile192 && rounds > 1) continue;
             double tm = double(rounds) * (kFixedUs + double(c.bm) * c.bn * (double(K) / sp) / (c.eff * kMacsPerUs));
             if (sp > 1)
                 tm += kReduceLaunchUs + (2.0 * sp * 4.0 + es) * double(M) * N / kReduceBytesPerUs;
@@ -635,7 +656,7 @@ struct ColumnSplit {
     int na = 0; // 0: one launch
     Plan a, b;
 };
-ColumnSplit splitColumns(ElemType t, int M, int N, int K, const Plan &one) {
+ColumnSplit splitColumns(ElemType t, int M, int N, int K, const Plan &one, bool swiglu = false) {
     ColumnSplit cs;
     static const bool on = [] { const char *e = std::getenv("LLAISYS_GEMM_COLUMN_SPLIT"); return !(e && e[0] == '0'); }();
     if (!on || one.splits != 1 || N % 8 != 0) return cs; // (vector stores need rows of whole 16 B)
@@ -645,7 +666,7 @@ ColumnSplit splitColumns(ElemType t, int M, int N, int K, const Plan &one) {
     const int nta = int((rounds - 1) * cus / one.mtiles); // column tiles that fill rounds - 1 rounds
     if (nta <= 0 || nta >= one.ntiles) return cs;
     const int na = nta * kTiles[one.tile].bn;
-    const Plan a = planGemm(t, M, na, K, true), b = planGemm(t, M, N - na, K, true);
+    const Plan a = planGemm(t, M, na, K, true, swiglu), b = planGemm(t, M, N - na, K, true, swiglu);
     if (a.est + b.est + kSecondLaunchUs < 0.95 * one.est) {
         cs.na = na;
         cs.a = a;
@@ -685,6 +706,12 @@ template <ElemType T> void launchGemm(GemmParams p, const Plan &plan, hipStream_
     case 4:
         if constexpr (T != ElemType::F32) {
             launchTile<T, 256, 256, 2, 4>(p, s);
+            break;
+        }
+        [[fallthrough]];
+    case kTile192:
+        if constexpr (T != ElemType::F32) {
+            launchTile<T, 256, 192, 2, 4>(p, s);
             break;
         }
         [[fallthrough]];
@@ -809,7 +836,7 @@ void linearSwiglu(void *act, const void *x, const void *w_interleaved, ElemType 
     const int rows_per_launch = rowsPerLaunch(t, M, K);
     for (int r0 = 0; r0 < M; r0 += rows_per_launch) {
         const int m = std::min(rows_per_launch, M - r0);
-        const Plan plan = planGemm(t, m, N, K, true);
+        const Plan plan = planGemm(t, m, N, K, true, true);
         // Columns [c0, c1) of the gate-up product, act columns [c0 / 2, c1 / 2).
         auto run = [&](int c0, int c1, const Plan &pl) {
             GemmParams p{};
@@ -827,7 +854,7 @@ void linearSwiglu(void *act, const void *x, const void *w_interleaved, ElemType 
                        stagedStores();
             launchGemm<ElemType::BF16>(p, pl, s);
         };
-        const ColumnSplit cs = splitColumns(t, m, N, K, plan);
+        const ColumnSplit cs = splitColumns(t, m, N, K, plan, true);
         if (cs.na) {
             run(0, cs.na, cs.a);
             run(cs.na, N, cs.b);

@@ -196,7 +196,8 @@ def test_linear_bf16_decode_batches(M, N, K, use_bias):
 # ragged ones: together they take every tile of the GEMM planner, with and
 # without a K split (fp32 partials summed by the reduce kernel).
 PREFILL = [(2048, 2048, 1536), (2048, 1536, 8960), (8192, 1536, 1536), (600, 17920, 1536), (600, 1536, 1536),
-           (1000, 2048, 1536), (333, 1536, 8960), (4099, 264, 1536), (2048, 17920, 1536)]
+           (1000, 2048, 1536), (333, 1536, 8960), (4099, 264, 1536), (2048, 17920, 1536), (7999, 1528, 1536),
+           (6000, 1530, 1536)]
 
 
 @pytest.mark.parametrize("M,N,K", PREFILL, ids=[f"{m}x{n}x{k}" for m, n, k in PREFILL])
