@@ -593,14 +593,19 @@ struct Plan {
     int mtiles = 0, ntiles = 0, splits = 1;
     double est = 0; // the model's time, us
 };
-struct TileShape { int bm, bn; double eff; };
-// 256 x 192 (8 waves of 128 x 48) fills the 256 CUs where 256 x 256 tiles
-// leave a quarter idle (8192 x 1536 x 1536: 256 tiles against 192, 44.6 ->
-// 40.2 us; 2048 x 1536 x 8960 split in 4: 76 -> 69.5 us); its wave columns
-// are not whole SwiGLU block pairs, so the fused gate-up skips it.
-constexpr TileShape kTiles[] = {{128, 256, 1.0}, {256, 128, 1.0}, {128, 128, 0.8},
-                                {64, 64, 0.45},  {256, 256, 1.2}, {256, 192, 1.1}};
-constexpr int kTile192 = 5;
+// narrow: waves 48 columns wide. 256 x 192 (8 waves of 128 x 48) and
+// 128 x 96 (4 waves of 64 x 48) fill the 256 CUs where the tiles twice their
+// size leave a quarter idle (8192 x 1536 x 1536: 256 tiles against 192, 44.6
+// -> 40.2 us; 2048 x 1536 x 8960 split in 4: 76 -> 69.5 us). They run only
+// where one round holds all their workgroups: over several (2048 x 17920 x
+// 1536: 3 rounds, 128-131 us) 256 x 256 tiles with the column split below run
+// faster (123-125 us) than the model prices them. Their wave columns are not
+// whole SwiGLU block pairs, so the fused gate-up skips them.
+struct TileShape { int bm, bn; double eff; bool narrow; };
+constexpr TileShape kTiles[] = {{128, 256, 1.0, false}, {256, 128, 1.0, false}, {128, 128, 0.8, false},
+                                {64, 64, 0.45, false},  {256, 256, 1.2, false}, {256, 192, 1.1, true},
+                                {128, 96, 0.7, true}};
+constexpr int kTile192 = 5, kTile96 = 6;
 constexpr int kMinSplitTiles = 8;            // k tiles per split at least
 constexpr double kFixedUs = 6.0;             // per round of workgroups
 constexpr double kMacsPerUs = 2.1e6;         // bm * bn * k per us at eff 1 (bf16)
@@ -614,21 +619,18 @@ Plan planGemm(ElemType t, int M, int N, int K, bool no_split = false, bool swigl
     Plan best;
     double best_t = 1e300;
     // LLAISYS_GEMM_BIG=0 leaves out the 256 x 256 tile (8 waves of 128 x 64),
-    // LLAISYS_GEMM_192=0 the 256 x 192 one.
+    // LLAISYS_GEMM_NARROW=0 the narrow ones.
     static const bool big = [] { const char *e = std::getenv("LLAISYS_GEMM_BIG"); return !(e && e[0] == '0'); }();
-    static const bool t192 = [] { const char *e = std::getenv("LLAISYS_GEMM_192"); return !(e && e[0] == '0'); }();
+    static const bool narrow = [] { const char *e = std::getenv("LLAISYS_GEMM_NARROW"); return !(e && e[0] == '0'); }();
     for (int i = 0; i < int(sizeof(kTiles) / sizeof(kTiles[0])); ++i) {
         if (t == ElemType::F32 && i >= 4) break; // f32: 128 accumulators at most
-        if ((i == 4 && !big) || (i == kTile192 && (!t192 || swiglu))) continue;
+        if ((i == 4 && !big) || (kTiles[i].narrow && (!narrow || swiglu))) continue;
         const TileShape &c = kTiles[i];
         const long mt = (M + c.bm - 1) / c.bm, nt = (N + c.bn - 1) / c.bn;
         for (int sp = 1; sp <= 8; sp *= 2) {
             if (sp > 1 && (no_split || nk / sp < kMinSplitTiles)) break;
             const long rounds = (mt * nt * sp + cus - 1) / cus;
-            // 256 x 192 only in one round: over several (2048 x 17920 x 1536:
-            // 3 rounds, 128-131 us) 256 x 256 tiles with the column split below
-            // run faster (123-125 us) than the model prices them.
-            if (i == kTile192 && rounds > 1) continue;
+            if (c.narrow && rounds > 1) continue;
             double tm = double(rounds) * (kFixedUs + double(c.bm) * c.bn * (double(K) / sp) / (c.eff * kMacsPerUs));
             if (sp > 1)
                 tm += kReduceLaunchUs + (2.0 * sp * 4.0 + es) * double(M) * N / kReduceBytesPerUs;
@@ -712,6 +714,12 @@ template <ElemType T> void launchGemm(GemmParams p, const Plan &plan, hipStream_
     case kTile192:
         if constexpr (T != ElemType::F32) {
             launchTile<T, 256, 192, 2, 4>(p, s);
+            break;
+        }
+        [[fallthrough]];
+    case kTile96:
+        if constexpr (T != ElemType::F32) {
+            launchTile<T, 128, 96>(p, s);
             break;
         }
         [[fallthrough]];

@@ -197,7 +197,7 @@ def test_linear_bf16_decode_batches(M, N, K, use_bias):
 # without a K split (fp32 partials summed by the reduce kernel).
 PREFILL = [(2048, 2048, 1536), (2048, 1536, 8960), (8192, 1536, 1536), (600, 17920, 1536), (600, 1536, 1536),
            (1000, 2048, 1536), (333, 1536, 8960), (4099, 264, 1536), (2048, 17920, 1536), (7999, 1528, 1536),
-           (6000, 1530, 1536)]
+           (6000, 1530, 1536), (1300, 1544, 1536), (1999, 1530, 1536), (900, 1536, 8960)]
 
 
 @pytest.mark.parametrize("M,N,K", PREFILL, ids=[f"{m}x{n}x{k}" for m, n, k in PREFILL])
@@ -211,6 +211,24 @@ def test_linear_bf16_prefill_shapes(M, N, K):
     rows = torch.cat([torch.arange(0, M, 7, device=DEV), torch.tensor([M - 1], device=DEV)])
     xs = x[rows].double()
     ref = xs @ w.double().T + b.double()
+    got = to_torch(out)[rows].double()
+    bound = ref.abs() * 2.0 ** -8 + 1e-6 * (xs.abs() @ w.double().abs().T) * K ** 0.5 + 1e-30
+    assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
+
+
+NARROW = [(8192, 1536, 1536), (1999, 1530, 1536), (900, 1536, 8960)]
+
+
+@pytest.mark.parametrize("M,N,K", NARROW, ids=[f"{m}x{n}x{k}" for m, n, k in NARROW])
+def test_linear_f16_narrow_tiles(M, N, K):
+    # f16 through the 256 x 192 and 128 x 96 tiles (waves 48 columns wide,
+    # spare W loads masked), same bound as bf16 (f16 rounds finer).
+    x, w = rnd((M, K), torch.float16, 0.5, seed=M + 1), rnd((N, K), torch.float16, 0.05, seed=N + 2)
+    out = to_llaisys(torch.full((M, N), float("nan"), dtype=torch.float16, device=DEV))
+    L.Ops.linear(out, to_llaisys(x), to_llaisys(w), None)
+    rows = torch.cat([torch.arange(0, M, 5, device=DEV), torch.tensor([M - 1], device=DEV)])
+    xs = x[rows].double()
+    ref = xs @ w.double().T
     got = to_torch(out)[rows].double()
     bound = ref.abs() * 2.0 ** -8 + 1e-6 * (xs.abs() @ w.double().abs().T) * K ** 0.5 + 1e-30
     assert ((got - ref).abs() <= bound).all(), float(((got - ref).abs() / bound).max())
