@@ -144,7 +144,9 @@ template <int BM, int BN> constexpr size_t stageBytes() { return size_t(BM) * st
 // rounded up to whole blocks per wave (a BN / 16 that is not a multiple of the
 // wave count leaves some waves one masked load into the spare blocks, so
 // every wave issues the same number of loads and waits on the same counts).
-template <int BM, int BN, int NW> constexpr int stageBlocks() { return BM / 16 + (BN / 16 + NW - 1) / NW * NW; }
+template <int BM, int BN, int NW, int RB = 64> constexpr int stageBlocks() {
+    return BM / (1024 / RB) + (BN / (1024 / RB) + NW - 1) / NW * NW;
+}
 
 // Tile index of workgroup b: XCD b % 8 takes tiles [(b % 8) T / 8, ...) in
 // order b / 8 (T = tiles; when T % 8 != 0 the plain order is kept).
@@ -180,19 +182,34 @@ __device__ __forceinline__ int slotOf(int r, int c) { return c ^ rowKey(r); }
 // read from LDS while the current tile's MFMAs run (PIPE): 4 (PIPE with 5
 // stages was 3-5 % slower, 3 stages slower again: 8192 x 17920 x 1536 486
 // against 503 and 497 us; more loads in flight per CU than it can stream).
-template <bool PIPE> constexpr int ringStages() { return 4; }
+template <bool PIPE, int RB = 64> constexpr int ringStages() { return RB == 128 ? 2 : 4; }
 
+// Wide k tiles (RB = 128: 64 16-bit k per row and stage). A 64 B row piece
+// per load instruction made every L1 -> L2 request 64 B, half a cache line:
+// at 256 x 256 x 1536 the kernel sent 54 M requests where hipBLASLt's
+// 128 B pieces send 28 M for the same bytes, and a CU's requests in flight
+// (~62 at ~290 cycles each) then bound the k loop. With 128 B per row a
+// block of one instruction is 8 rows x 128 B, piece c of row r sits at slot
+// c ^ (r % 8) (the 8 lanes one LDS cycle serves read 8 rows of one piece:
+// 8 distinct slots), and a stage is twice the bytes, so the ring holds two
+// stages: the next stage's loads go out right after the barrier that frees
+// its slot and have the current stage's two MFMA steps to land; the second
+// step's fragments are read under the first step's MFMAs.
 // WGM x WGN waves, wave (wm, wn) owning the (BM / WGM) x (BN / WGN) sub-tile.
-template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2, bool PIPE = false>
+template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2, bool PIPE = false, int RB = 64>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
-    constexpr int NS = ringStages<PIPE>();
+    static_assert(RB == 64 || RB == 128, "k tiles of 64 or 128 B per row");
+    constexpr bool WIDE = RB == 128;
+    constexpr int NS = ringStages<PIPE, RB>();
     constexpr int NW = WGM * WGN;
     constexpr int ES = Elem<T>::size;
-    constexpr int KT = kRowBytes / ES;              // elements per k tile
+    constexpr int KT = RB / ES;                     // elements per k tile
+    constexpr int PPR = RB / 16;                    // 16 B pieces per row and k tile
+    constexpr int RPB = 64 / PPR;                   // rows per 1 KiB block (one load instruction)
     constexpr int TM = BM / (16 * WGM), TN = BN / (16 * WGN); // 16-row fragments per wave
-    constexpr int XB = BM / 16, WB = BN / 16;       // 1 KiB blocks per operand per k tile
+    constexpr int XB = BM / RPB, WB = BN / RPB;     // 1 KiB blocks per operand per k tile
     constexpr int XW = XB / NW, WW = (WB + NW - 1) / NW; // ... issued by each wave
-    constexpr int STAGE = stageBlocks<BM, BN, NW>() * 64; // u32x4 per stage
+    constexpr int STAGE = stageBlocks<BM, BN, NW, RB>() * 64; // u32x4 per stage
     constexpr int kLoadsPerStage = XW + WW;          // per wave
     static_assert(XB % NW == 0, "each wave issues whole X blocks");
     extern __shared__ u32x4 lds[];                   // [NS][X blocks | W blocks]
@@ -214,18 +231,18 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p.w), (short)0, int(p.w_bytes), kRsrcWord3);
     const uint32_t row_bytes = uint32_t(p.K) * ES;
 
-    // Lane's piece of a block: row lr = lane / 4 of the block, global piece lc.
-    const int lr = lane >> 2, lc = (lane & 3) ^ rowKey(lr);
-    // Block b of the wave is block wave + NW b of the operand (rows 16 (wave + NW b) ..).
-    const uint32_t xbase = uint32_t(m0 + 16 * wave + lr) * row_bytes + 16 * lc;
-    const uint32_t wbase = uint32_t(n0 + 16 * wave + lr) * row_bytes + 16 * lc;
-    const uint32_t bstride = 16u * NW * row_bytes; // NW blocks of 16 rows
+    // Lane's piece of a block: row lr = lane / PPR of the block, global piece lc.
+    const int lr = lane / PPR, lc = WIDE ? (lane % PPR) ^ lr : (lane & 3) ^ rowKey(lr);
+    // Block b of the wave is block wave + NW b of the operand (rows RPB (wave + NW b) ..).
+    const uint32_t xbase = uint32_t(m0 + RPB * wave + lr) * row_bytes + 16 * lc;
+    const uint32_t wbase = uint32_t(n0 + RPB * wave + lr) * row_bytes + 16 * lc;
+    const uint32_t bstride = uint32_t(RPB) * NW * row_bytes; // NW blocks of RPB rows
     const int nk_all = (p.K + KT - 1) / KT;
     const int kt0 = split * nk_all / p.splits;
     const int nk = (split + 1) * nk_all / p.splits - kt0;
     auto issue = [&](int kt) {
         u32x4 *st = lds + (kt % NS) * STAGE;
-        const uint32_t kb = uint32_t(kt0 + kt) * kRowBytes;
+        const uint32_t kb = uint32_t(kt0 + kt) * RB;
         const bool in_k = kt < nk && kb + 16 * lc < row_bytes;
 #pragma unroll
         for (int b = 0; b < XW; ++b)
@@ -245,7 +262,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s) issue(s);
+    for (int s = 0; s < (WIDE ? 2 : NS - 1); ++s) issue(s);
     // Fragment reads: lane reads row l % 16 of a 16-row block, piece l / 16.
     const int fr = lane & 15, fslot = slotOf(fr, lane >> 4);
     const int xblk0 = wm * TM, wblk0 = XB + wn * TN;
@@ -278,7 +295,45 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
     // (The compiler does not count global_load_lds against LDS reads, so
     // the waits for the ring are explicit; the barrier after each makes
     // every wave's part of a stage visible.)
-    if constexpr (PIPE) {
+    if constexpr (WIDE) {
+        // Row R of the stage (X rows, then W rows) at R * 8 + (piece ^ (R % 8)).
+        auto readHalf = [&](int kt, int half, u32x4 (&a)[TN], u32x4 (&b)[TM]) {
+            const u32x4 *st = lds + (kt % NS) * STAGE;
+            const int slot = ((lane >> 4) + 4 * half) ^ (fr & 7);
+#pragma unroll
+            for (int i = 0; i < TN; ++i) a[i] = st[(BM + 16 * (wn * TN + i) + fr) * PPR + slot];
+#pragma unroll
+            for (int j = 0; j < TM; ++j) b[j] = st[(16 * (wm * TM + j) + fr) * PPR + slot];
+        };
+        constexpr int kReads = TN + TM;
+        constexpr int kMfmas = TN * TM * (T == ElemType::F32 ? 4 : 1);
+        constexpr int kPer = kMfmas / kReads > 0 ? kMfmas / kReads : 1;
+        // The reads of one half between the MFMAs of the other.
+        auto interleave = [&]() {
+#pragma unroll
+            for (int g = 0; g < kReads; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // one LDS read
+                __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0); // then MFMAs
+            }
+        };
+        // Stage 0 has landed once only stage 1's loads are in flight.
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kLoadsPerStage) : "memory");
+        u32x4 a0[TN], b0[TM], a1[TN], b1[TM];
+        readHalf(0, 0, a0, b0);
+        for (int kt = 0; kt < nk; ++kt) {
+            readHalf(kt, 1, a1, b1);
+            mfmaTile(a0, b0);
+            interleave();
+            // Stage kt + 1 has landed (this wave's loads; the barrier: every
+            // wave's) and every wave has read all of stage kt, whose slot
+            // stage kt + 2 takes.
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue(kt + 2);
+            readHalf(kt + 1, 0, a0, b0); // past the end: the zero-filled stage
+            mfmaTile(a1, b1);
+            interleave();
+        }
+    } else if constexpr (PIPE) {
         // Stage 0 has landed once at most NS - 2 stages are in flight.
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * kLoadsPerStage) : "memory");
         // One k tile: wait for stage kt + 1, refill the slot of stage kt - 1,
@@ -544,8 +599,9 @@ int cusOf() {
     return cache[dev];
 }
 
-template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE> void launchTileAs(GemmParams p, hipStream_t s) {
-    const size_t lds = std::max(size_t(ringStages<PIPE>()) * stageBlocks<BM, BN, WGM * WGN>() * 1024,
+template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE, int RB = 64>
+void launchTileAs(GemmParams p, hipStream_t s) {
+    const size_t lds = std::max(size_t(ringStages<PIPE, RB>()) * stageBlocks<BM, BN, WGM * WGN, RB>() * 1024,
                                 Elem<T>::size == 2 ? stageBytes<BM, BN>() : size_t(0));
     // The LDS limit is raised once per device the kernel runs on.
     static std::mutex mu;
@@ -556,12 +612,12 @@ template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE> void launchTi
         std::lock_guard<std::mutex> lock(mu);
         if (size_t(dev) >= raised.size()) raised.resize(dev + 1, false);
         if (!raised[dev]) {
-            HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN, PIPE>),
+            HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN, PIPE, RB>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
             raised[dev] = true;
         }
     }
-    hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN, PIPE>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
+    hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN, PIPE, RB>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
                        dim3(64 * WGM * WGN), lds, s, p);
 }
 
@@ -572,7 +628,20 @@ bool pipelined() {
     return v;
 }
 
+// 16-bit tiles move k in 128 B row pieces (two stages) unless
+// LLAISYS_GEMM_WIDE_K=0 (64 B pieces, four stages).
+bool wideK() {
+    static const bool v = [] { const char *e = std::getenv("LLAISYS_GEMM_WIDE_K"); return !(e && e[0] == '0'); }();
+    return v;
+}
+
 template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2> void launchTile(GemmParams p, hipStream_t s) {
+    if constexpr (Elem<T>::size == 2) {
+        if (wideK()) {
+            launchTileAs<T, BM, BN, WGM, WGN, true, 128>(p, s);
+            return;
+        }
+    }
     if (pipelined())
         launchTileAs<T, BM, BN, WGM, WGN, true>(p, s);
     else
