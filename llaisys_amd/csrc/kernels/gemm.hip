@@ -13,19 +13,19 @@
 //    so the sum is over the same products.
 //
 // A workgroup of 4 or 8 waves (2 x 2, 2 x 4 or 4 x 2) owns a BM x BN tile
-// of Y; each wave one sub-tile of it (64 x 64 to 128 x 64). K advances in
-// tiles of 64 B per row (32 16-bit or 16 f32 elements) through a 4-stage LDS
-// ring: each wave moves whole 16-row blocks of X and W straight from global
-// memory into LDS by 16 B global_load_lds (buffer loads: out-of-range rows
-// and k come back as zeros, so edge tiles need no other guard), one stage
-// stays in flight beyond the next one, and one barrier per k tile both
+// of Y; each wave one sub-tile of it (64 x 48 to 128 x 64). K advances in
+// tiles of 128 B per row (64 16-bit elements; f32: 64 B, 16 elements)
+// through an LDS ring of two stages (f32: four): each wave moves whole 1 KiB
+// blocks of X and W rows straight from global memory into LDS by 16 B
+// global_load_lds (buffer loads: out-of-range rows and k come back as zeros,
+// so edge tiles need no other guard), and one barrier per stage both
 // publishes a stage and frees the slot the next issue refills. Each wave
-// reads the next stage's fragments from LDS while the current stage's
-// MFMAs run (two register sets, reads spread between the MFMAs). In LDS,
-// piece c of row r sits at slot c ^ rowKey(r), so a fragment read is free of
-// bank conflicts. Shapes that leave CUs idle split K over workgroups into
-// fp32 partials that a second kernel sums in split order (deterministic)
-// before the single rounding.
+// reads the next fragments from LDS while the current MFMAs run (two
+// register sets, reads spread between the MFMAs). In LDS, piece c of row r
+// sits at a slot swizzled by r, so a fragment read is free of bank
+// conflicts. Shapes that leave CUs idle split K over workgroups into fp32
+// partials that a second kernel sums in split order (deterministic) before
+// the single rounding.
 //
 // W is the MFMA's A operand and X its B operand, so a lane's accumulator
 // holds 4 consecutive columns n of one row m of Y. 16-bit tiles leave
@@ -164,7 +164,8 @@ __device__ __forceinline__ void tileOf(const GemmParams &p, int b, int &mt, int 
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// One k tile of an operand is ROWS rows x 64 B (4 pieces of 16 B), kept in
+// 64 B k tiles (f32, and 16-bit types with LLAISYS_GEMM_WIDE_K=0):
+// one k tile of an operand is ROWS rows x 64 B (4 pieces of 16 B), kept in
 // LDS as blocks of 16 rows x 64 B: one 64-lane global_load_lds instruction
 // fills one block, lane i writing bytes 16 i .. 16 i + 15 of it (row i / 4,
 // slot i % 4). Piece c of row r sits at slot c ^ key(r). A fragment read
