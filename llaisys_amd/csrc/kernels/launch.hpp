@@ -15,8 +15,11 @@ constexpr int kPageElems = kPageTokens * kHeadDim; // bf16 elements per (block, 
 enum class ElemType { F32, F16, BF16 };
 
 // Contiguous causal GQA attention (the reference's self_attention op).
+// Small grids (few query rows x heads) split the keys over workgroups into
+// fp32 partials in `workspace` (selfAttentionWorkspaceBytes; 0: none needed).
+size_t selfAttentionWorkspaceBytes(int L, int S, int nh, int dv);
 void selfAttention(void *out, const void *q, const void *k, const void *v, ElemType type, int L, int S, int nh,
-                   int nkvh, int d, int dv, float scale, void *stream);
+                   int nkvh, int d, int dv, float scale, void *stream, void *workspace);
 
 // Paged KV append; cu_new may be null (one token per sequence, T == B).
 void pagedAppend(uint16_t *k_pool, uint16_t *v_pool, const uint16_t *k_new, const uint16_t *v_new,

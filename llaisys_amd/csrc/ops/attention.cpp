@@ -116,8 +116,9 @@ void selfAttention(const tensor_t &out, const tensor_t &q, const tensor_t &k, co
     if (host)
         return C::selfAttention(out->data(), q->data(), k->data(), v->data(), elemType(q->dtype(), op), int(L),
                                 int(S), int(nh), int(nkvh), int(d), int(dv), scale);
+    void *ws = core::context().runtime().scratch(K::selfAttentionWorkspaceBytes(int(L), int(S), int(nh), int(dv)));
     K::selfAttention(out->data(), q->data(), k->data(), v->data(), elemType(q->dtype(), op), int(L), int(S),
-                     int(nh), int(nkvh), int(d), int(dv), scale, streamOf());
+                     int(nh), int(nkvh), int(d), int(dv), scale, streamOf(), ws);
 }
 
 void pagedKVAppend(const tensor_t &k_pool, const tensor_t &v_pool, const tensor_t &k_new, const tensor_t &v_new,

@@ -56,6 +56,8 @@ def test_reference_shapes_and_tolerances(shape, dtype, atol, rtol):
     (9, 9, 4, 4, 64, 64),
     (3, 130, 8, 1, 256, 256),
     (6, 20, 6, 3, 32, 48),
+    (40, 1000, 12, 2, 128, 128),  # many key chunks per wave
+    (2, 70, 2, 1, 64, 128),
 ])
 def test_against_fp32_oracle(L_, S, nh, nkvh, d, dv):
     qn = oracle.randn(1, (L_, nh, d))
