@@ -84,7 +84,6 @@ __global__ void __launch_bounds__(64 * kWaves) selfAttentionKernel(T *__restrict
                                                                    int L, int S, int nh, int nkvh, int d, int dv,
                                                                    float scale_log2, float *part) {
     constexpr int VEC = Vec16<T>::N;
-    __shared__ float qs[kMaxDim];
     __shared__ float ps[kWaves][64];
     __shared__ float wo[kWaves][kMaxDim];
     __shared__ float wml[kWaves][2];
@@ -92,8 +91,9 @@ __global__ void __launch_bounds__(64 * kWaves) selfAttentionKernel(T *__restrict
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = lane >> 4, t = lane & 15;
     const int kh = h / (nh / nkvh);
-    for (int e = threadIdx.x; e < d; e += 64 * kWaves) qs[e] = toF32(q[(size_t(i) * nh + h) * d + e]) * scale_log2;
-    __syncthreads();
+    // q is the same for every lane: read through the scalar cache inside the
+    // dot products (no LDS copy and no barrier ahead of the key loads).
+    const T *qr = q + (size_t(i) * nh + h) * d;
 
     const int n_keys = i + S - L + 1; // keys 0 .. i+S-L
     const size_t kstride = size_t(nkvh) * d, vstride = size_t(nkvh) * dv;
@@ -113,12 +113,12 @@ __global__ void __launch_bounds__(64 * kWaves) selfAttentionKernel(T *__restrict
                     float f[VEC];
                     Vec16<T>::load(kr + e0, f);
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) dot = fmaf(qs[e0 + e], f[e], dot);
+                    for (int e = 0; e < VEC; ++e) dot = fmaf(toF32(qr[e0 + e]), f[e], dot);
                 }
             } else {
-                for (int e = 0; e < d; ++e) dot = fmaf(qs[e], toF32(kr[e]), dot);
+                for (int e = 0; e < d; ++e) dot = fmaf(toF32(qr[e]), toF32(kr[e]), dot);
             }
-            s = dot;
+            s = dot * scale_log2;
         }
         const float m_new = fmaxf(m, waveMax(s)); // finite: key j0 is valid
         const float alpha = exp2f(m - m_new);
