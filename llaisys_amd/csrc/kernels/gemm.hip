@@ -183,7 +183,17 @@ __device__ __forceinline__ int slotOf(int r, int c) { return c ^ rowKey(r); }
 // read from LDS while the current tile's MFMAs run (PIPE): 4 (PIPE with 5
 // stages was 3-5 % slower, 3 stages slower again: 8192 x 17920 x 1536 486
 // against 503 and 497 us; more loads in flight per CU than it can stream).
-template <bool PIPE, int RB = 64> constexpr int ringStages() { return RB == 128 ? 2 : 4; }
+template <bool PIPE, int RB = 64, int WS = 2> constexpr int ringStages() { return RB == 128 ? WS : 4; }
+
+// Stages of the wide ring: two for the 8-wave tiles (256 x 256 and 256 x 192
+// fit no more; 128 x 256 and 256 x 128 ran 1-6 % slower with three), four
+// for the 4-wave ones, whose short k loops wait on their loads more: 1024 x
+// 2048 x 1536 16.9 -> 14.1 us, 1024 x 1536 x 8960 47.6 -> 37.4 us, 2048 x 1536
+// x 1536 17.1 -> 14.8 us (LLAISYS_GEMM_WIDE_DEEP=0: two everywhere).
+template <int BM, int BN, int NW> constexpr int wideStages() {
+    constexpr int n = 163840 / (((BM / 8) + (BN / 8 + NW - 1) / NW * NW) * 1024);
+    return NW > 4 ? 2 : n > 4 ? 4 : n < 2 ? 2 : n;
+}
 
 // Wide k tiles (RB = 128: 64 16-bit k per row and stage). A 64 B row piece
 // per load instruction made every L1 -> L2 request 64 B, half a cache line:
@@ -197,11 +207,11 @@ template <bool PIPE, int RB = 64> constexpr int ringStages() { return RB == 128 
 // its slot and have the current stage's two MFMA steps to land; the second
 // step's fragments are read under the first step's MFMAs.
 // WGM x WGN waves, wave (wm, wn) owning the (BM / WGM) x (BN / WGN) sub-tile.
-template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2, bool PIPE = false, int RB = 64>
+template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2, bool PIPE = false, int RB = 64, int WS = 2>
 __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
     static_assert(RB == 64 || RB == 128, "k tiles of 64 or 128 B per row");
     constexpr bool WIDE = RB == 128;
-    constexpr int NS = ringStages<PIPE, RB>();
+    constexpr int NS = ringStages<PIPE, RB, WS>();
     constexpr int NW = WGM * WGN;
     constexpr int ES = Elem<T>::size;
     constexpr int KT = RB / ES;                     // elements per k tile
@@ -263,7 +273,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
         for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-    for (int s = 0; s < (WIDE ? 2 : NS - 1); ++s) issue(s);
+    for (int s = 0; s < (WIDE ? NS : NS - 1); ++s) issue(s);
     // Fragment reads: lane reads row l % 16 of a 16-row block, piece l / 16.
     const int fr = lane & 15, fslot = slotOf(fr, lane >> 4);
     const int xblk0 = wm * TM, wblk0 = XB + wn * TN;
@@ -317,8 +327,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
                 __builtin_amdgcn_sched_group_barrier(0x008, kPer, 0); // then MFMAs
             }
         };
-        // Stage 0 has landed once only stage 1's loads are in flight.
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kLoadsPerStage) : "memory");
+        // Stage 0 has landed once only stages 1 .. NS - 1 are in flight.
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 1) * kLoadsPerStage) : "memory");
         u32x4 a0[TN], b0[TM], a1[TN], b1[TM];
         readHalf(0, 0, a0, b0);
         for (int kt = 0; kt < nk; ++kt) {
@@ -327,9 +337,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemmKernel(GemmParams p) {
             interleave();
             // Stage kt + 1 has landed (this wave's loads; the barrier: every
             // wave's) and every wave has read all of stage kt, whose slot
-            // stage kt + 2 takes.
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            issue(kt + 2);
+            // stage kt + NS takes.
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NS - 2) * kLoadsPerStage) : "memory");
+            issue(kt + NS);
             readHalf(kt + 1, 0, a0, b0); // past the end: the zero-filled stage
             mfmaTile(a1, b1);
             interleave();
@@ -600,9 +610,9 @@ int cusOf() {
     return cache[dev];
 }
 
-template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE, int RB = 64>
+template <ElemType T, int BM, int BN, int WGM, int WGN, bool PIPE, int RB = 64, int WS = 2>
 void launchTileAs(GemmParams p, hipStream_t s) {
-    const size_t lds = std::max(size_t(ringStages<PIPE, RB>()) * stageBlocks<BM, BN, WGM * WGN, RB>() * 1024,
+    const size_t lds = std::max(size_t(ringStages<PIPE, RB, WS>()) * stageBlocks<BM, BN, WGM * WGN, RB>() * 1024,
                                 Elem<T>::size == 2 ? stageBytes<BM, BN>() : size_t(0));
     // The LDS limit is raised once per device the kernel runs on.
     static std::mutex mu;
@@ -613,12 +623,12 @@ void launchTileAs(GemmParams p, hipStream_t s) {
         std::lock_guard<std::mutex> lock(mu);
         if (size_t(dev) >= raised.size()) raised.resize(dev + 1, false);
         if (!raised[dev]) {
-            HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN, PIPE, RB>),
+            HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(&gemmKernel<T, BM, BN, WGM, WGN, PIPE, RB, WS>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
             raised[dev] = true;
         }
     }
-    hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN, PIPE, RB>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
+    hipLaunchKernelGGL((gemmKernel<T, BM, BN, WGM, WGN, PIPE, RB, WS>), dim3(unsigned(p.mtiles * p.ntiles * p.splits)),
                        dim3(64 * WGM * WGN), lds, s, p);
 }
 
@@ -639,7 +649,11 @@ bool wideK() {
 template <ElemType T, int BM, int BN, int WGM = 2, int WGN = 2> void launchTile(GemmParams p, hipStream_t s) {
     if constexpr (Elem<T>::size == 2) {
         if (wideK()) {
-            launchTileAs<T, BM, BN, WGM, WGN, true, 128>(p, s);
+            static const bool deep = [] { const char *e = std::getenv("LLAISYS_GEMM_WIDE_DEEP"); return !(e && e[0] == '0'); }();
+            if (deep)
+                launchTileAs<T, BM, BN, WGM, WGN, true, 128, wideStages<BM, BN, WGM * WGN>()>(p, s);
+            else
+                launchTileAs<T, BM, BN, WGM, WGN, true, 128, 2>(p, s);
             return;
         }
     }
